@@ -1,0 +1,237 @@
+#!/usr/bin/env python3
+"""Benchmark of the Volta conv / matmul hot path on one MI355X.
+
+Default workload (the Conv2d fwd+bwd metric's
+config): ResNet-style 3x3 conv block, bf16 storage with fp32 accumulation,
+N=128, layers 64->64 @56x56, 128->128 @28x28, 256->256 @14x14 (3x3, stride 1,
+pad 1) and the 1x1 stride-2 projection 64->128 @56x56.  One step = forward,
+input gradient and weight gradient of every layer (dY ~ N(0,1) injected).
+Inputs are synthetic and resident in HBM before timing starts.
+
+Prints ONE JSON line (driver contract).  `value` is whole-job TFLOP/s of the
+step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass).  `roofline` is for the
+dominant kernel, timed with HIP events on the stream it runs on.
+`cpu_baseline` times the CPU oracle (a C restatement of Volta's
+single-threaded CPU loops) on a bounded sample and extrapolates.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"bf16": 2516.6, "f32": 157.3}  # MI355X dense MFMA
+PEAK_HBM_GBS = 8000.0
+
+METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
+
+# (name, C, O, H, K, stride, pad) at N=128
+C3_LAYERS = [
+    ("3x3 64->64 @56", 64, 64, 56, 3, 1, 1),
+    ("3x3 128->128 @28", 128, 128, 28, 3, 1, 1),
+    ("3x3 256->256 @14", 256, 256, 14, 3, 1, 1),
+    ("1x1 s2 64->128 @56", 64, 128, 56, 1, 2, 0),
+]
+C3_BATCH = 128
+
+
+def conv_out(h, k, s, p):
+    return (h + 2 * p - k) // s + 1
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--verbose", action="store_true")
+    return ap.parse_args()
+
+
+def build_layers(torch, vnn, dev):
+    g = torch.Generator().manual_seed(0)
+    layers = []
+    for name, C, O, H, K, S, P in C3_LAYERS:
+        conv = vnn.Conv2d(C, O, K, S, P, use_bias=False, device=dev, dtype=torch.bfloat16, generator=g)
+        # Kaiming init (fan_in = C*K*K) is what Conv2d::new uses (he_initialization)
+        conv.set_algo(vnn.ConvAlgo.IGEMM)
+        x = torch.randn((C3_BATCH, C, H, H), generator=g).to(dev, torch.bfloat16)
+        HO = conv_out(H, K, S, P)
+        dy = torch.randn((C3_BATCH, O, HO, HO), generator=g).to(dev, torch.bfloat16)
+        y = torch.empty((C3_BATCH, O, HO, HO), device=dev, dtype=torch.bfloat16)
+        dx = torch.empty_like(x)
+        dw = torch.empty_like(conv.weight)
+        flops = 2.0 * C3_BATCH * O * C * K * K * HO * HO
+        byts = 2.0 * (x.numel() + conv.weight.numel() + y.numel())
+        layers.append(dict(name=name, conv=conv, x=x, dy=dy, y=y, dx=dx, dw=dw, flops=flops, bytes=byts))
+    return layers
+
+
+def run_step(layers, timers=None):
+    for i, L in enumerate(layers):
+        conv = L["conv"]
+        t = timers[i] if timers is not None else None
+        if t:
+            t["fwd"][0].record()
+        conv.forward(L["x"], out=L["y"])
+        if t:
+            t["fwd"][1].record()
+            t["dgrad"][0].record()
+        conv.backward(L["dy"], L["x"], input_grad=True, weight_grad=False, algo=conv.algo,
+                      outs=(L["dx"], None, None))
+        if t:
+            t["dgrad"][1].record()
+            t["wgrad"][0].record()
+        conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=conv.algo,
+                      outs=(None, L["dw"], None))
+        if t:
+            t["wgrad"][1].record()
+
+
+def cpu_baseline(sample_budget_s=20.0):
+    """Time the oracle's restatement of Volta's CPU Direct loops (what Volta's
+    CPU auto-select picks for every C3 layer, conv.rs:55-57) on a sample of
+    each loop nest's outer iterations and extrapolate to the full step."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle
+
+    lib = oracle.lib()
+    rng = np.random.default_rng(0)
+    total_s = 0.0
+    detail = []
+    used = 0.0
+    for name, C, O, H, K, S, P in C3_LAYERS:
+        HO = conv_out(H, K, S, P)
+        # forward (conv.rs:1359-1419): one image, extrapolated x N
+        x = rng.standard_normal((1, C, H, H)).astype(np.float32)
+        w = rng.standard_normal((O, C, K, K)).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.direct_conv(x, w, (S, S), (P, P))
+        tf = (time.perf_counter() - t0) * C3_BATCH
+        # weight grad (conv.rs:544-606): one image, x N
+        dy = rng.standard_normal((1, O, HO, HO)).astype(np.float32)
+        t0 = time.perf_counter()
+        oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P))
+        tw = (time.perf_counter() - t0) * C3_BATCH
+        # input grad, literal O(B*C*H*W*O*HO*WO) scan (conv.rs:450-515): run it on
+        # a 4-row strip of one input channel of one image, take the cost per
+        # (input element x output position) iteration, scale to the full scan
+        rows = 4
+        HO_s = conv_out(rows, K, S, P)
+        ws = np.ascontiguousarray(w[:, :1])
+        dys = np.ascontiguousarray(dy[:, :, :HO_s, :])
+        dxs = np.empty((1, 1, rows, H), np.float32)
+        fp = ctypes.POINTER(ctypes.c_float)
+        t0 = time.perf_counter()
+        lib.or_direct_conv_backward_input_literal(
+            dys.ctypes.data_as(fp), ws.ctypes.data_as(fp), dxs.ctypes.data_as(fp),
+            *map(ctypes.c_size_t, (1, 1, O, rows, H, K, K, S, S, P, P)))
+        t1 = time.perf_counter() - t0
+        per_iter = t1 / (rows * H * O * HO_s * HO)
+        td = per_iter * C3_BATCH * C * H * H * O * HO * HO
+        used += tf / C3_BATCH + tw / C3_BATCH + t1
+        detail.append((name, tf, td, tw))
+        total_s += tf + td + tw
+    flops = sum(2.0 * C3_BATCH * O * C * K * K * conv_out(H, K, S, P) ** 2 * 3 for _, C, O, H, K, S, P in C3_LAYERS)
+    return dict(value=flops / total_s / 1e12, unit="TFLOP/s", cores=1, kind="port",
+                sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on 1 of "
+                        "128 images, literal dX scan on 1 row of 1 input channel; extrapolated linearly to the full "
+                        f"step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
+                seconds_per_step_extrapolated=total_s)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note "
+                                   "(DESIGN.md), not an implemented path", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    import volta_amd
+    from volta_amd import nn as vnn
+
+    dev = torch.device("cuda:0")
+    volta_amd.lib()
+    layers = build_layers(torch, vnn, dev)
+    step_flops = 3.0 * sum(L["flops"] for L in layers)
+
+    for _ in range(args.warmup):
+        run_step(layers)
+    torch.cuda.synchronize()
+
+    # timed region: K steps, per-op HIP events on the torch stream our kernels run on
+    ev = lambda: torch.cuda.Event(enable_timing=True)  # noqa: E731
+    per_step_timers = [[{k: (ev(), ev()) for k in ("fwd", "dgrad", "wgrad")} for _ in layers]
+                       for _ in range(args.steps)]
+    start, end = ev(), ev()
+    torch.cuda.synchronize()
+    start.record()
+    for s in range(args.steps):
+        run_step(layers, per_step_timers[s])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    ms_per_step = total_ms / args.steps
+    tflops = step_flops / (ms_per_step * 1e-3) / 1e12
+
+    # per-op averages
+    ops = []
+    for i, L in enumerate(layers):
+        for k in ("fwd", "dgrad", "wgrad"):
+            ms = sum(t[i][k][0].elapsed_time(t[i][k][1]) for t in per_step_timers) / args.steps
+            ops.append(dict(layer=L["name"], op=k, ms=ms, flops=L["flops"], bytes=L["bytes"]))
+    dom = max(ops, key=lambda o: o["ms"])
+    ai = dom["flops"] / dom["bytes"]
+    ridge = PEAK_TFLOPS["bf16"] * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if ai >= ridge:
+        ach = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+        roof = dict(bound="mfma", achieved=round(ach, 2), peak=PEAK_TFLOPS["bf16"], unit="TFLOP/s",
+                    frac=round(ach / PEAK_TFLOPS["bf16"], 4), traffic=None)
+    else:
+        ach = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
+        roof = dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                    frac=round(ach / PEAK_HBM_GBS, 4), traffic=None)
+    roof["kernel"] = f"{dom['layer']} {dom['op']}"
+    roof["launch_ms"] = round(dom["ms"], 4)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "configs[2] ResNet-style 3x3 conv block fwd+dgrad+wgrad, bf16 storage, fp32 accum",
+                   "global_batch": C3_BATCH, "layers": [l[0] for l in C3_LAYERS], "bias": False,
+                   "algo": "IGEMM", "parallelism": "none (1 GPU)"},
+        "pct_bf16_peak": round(100.0 * tflops / PEAK_TFLOPS["bf16"], 2),
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,225 @@
+/*
+ * volta_hip.h -- C ABI of libvolta_hip.so, the MI355X (gfx950) implementation of
+ * Volta's convolution and matrix-product hot path.
+ *
+ * Each compute entry point replaces one `RawTensor::gpu_*` function of the
+ * reference's device-dispatch boundary (src/ops/gpu_ops.rs) or one CPU-only layer
+ * routine of the same path, with the same argument meaning and order.  Cited
+ * lines are under the reference root.
+ *
+ * Conventions
+ *  - All pointers are device pointers (hipMalloc'd or torch-owned) except in
+ *    vh_upload/vh_download.  Layouts are the reference's: NCHW activations,
+ *    Conv2d weights OIHW (conv.rs:130), ConvTranspose2d weights IOHW
+ *    (conv_transpose.rs:22,40), Linear weights [in, out] (linear.rs:9-10),
+ *    row-major matrices.
+ *  - `dtype` selects the storage type of every floating-point tensor argument of
+ *    the call: VH_F32 (the reference's only type, storage.rs:583-585) or
+ *    VH_BF16 (raw bf16 bits; the reference cannot compute in bf16).  Arithmetic
+ *    always accumulates in fp32.  Bias vectors use the same dtype.
+ *  - Outputs are written in full (no accumulation into existing contents).
+ *  - `stream` is a hipStream_t (NULL = the default stream).  Calls are
+ *    asynchronous with respect to the host; order is the stream's order.
+ *  - Return value: VH_OK (0) or a vh_status code.  Where the reference returns
+ *    Option::None (no device, CPU storage, allocation failure) this ABI returns
+ *    a non-zero status so the caller keeps its CPU fallback; where the reference
+ *    panics on a shape mismatch (kernels.rs:1129-1130) this ABI returns
+ *    VH_ERR_BAD_SHAPE and never aborts the host.  vh_last_error() describes the
+ *    last failure of the calling thread.
+ *  - Every tensor must hold fewer than 2^31 elements (VH_ERR_UNSUPPORTED otherwise).
+ *  - Workspace (split-K partials, re-laid-out weights, im2col matrices) is taken
+ *    from a per-stream cache inside the library; calls on one stream may reuse it.
+ */
+#ifndef VOLTA_HIP_H
+#define VOLTA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  VH_OK = 0,
+  VH_ERR_NO_DEVICE = 1,   /* no GPU: the reference's get_gpu_context() -> None */
+  VH_ERR_BAD_SHAPE = 2,   /* dimension mismatch: the reference's assert_eq! panics */
+  VH_ERR_OOM = 3,         /* device allocation failed: GpuBuffer::zeros -> None */
+  VH_ERR_LAUNCH = 4,      /* HIP runtime / kernel launch error */
+  VH_ERR_BAD_ARG = 5,     /* null pointer, bad enum value */
+  VH_ERR_UNSUPPORTED = 6  /* tensor too large for 32-bit indexing */
+} vh_status;
+
+typedef enum { VH_F32 = 0, VH_BF16 = 1 } vh_dtype;
+
+/* ConvAlgo (src/nn/layers/conv.rs:11-24), same discriminant order. */
+typedef enum { VH_ALGO_DIRECT = 0, VH_ALGO_IM2COL = 1, VH_ALGO_IGEMM = 2, VH_ALGO_AUTO = 3 } vh_conv_algo;
+
+/* ------------------------------------------------------------------ runtime */
+/* get_gpu_context (src/gpu/mod.rs:34-47): selects device 0 on first use. */
+int vh_init(void);
+const char* vh_last_error(void);
+/* GpuBuffer::zeros / from_slice / to_vec (src/gpu/buffer.rs:40-220) and the
+ * size-bucketed pool (src/gpu/pool.rs:28-35, 123-190). */
+int vh_alloc(size_t bytes, void** dptr);
+int vh_free(void* dptr);
+int vh_upload(void* dst_dev, const void* src_host, size_t bytes, void* stream);
+int vh_download(void* dst_host, const void* src_dev, size_t bytes, void* stream);
+/* GpuContext::sync (src/gpu/context.rs:342-382). */
+int vh_stream_sync(void* stream);
+/* Releases cached workspace and pooled buffers (pool.rs clear). */
+int vh_release_cache(void);
+
+/* ------------------------------------------------------------------ matmul */
+/* RawTensor::gpu_matmul, src/ops/gpu_ops.rs:151-169 (GpuKernels::matmul,
+ * src/gpu/kernels.rs:1128-1210): c[m,n] = a[m,k] . b[k,n]. */
+int vh_matmul(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t k,
+              int64_t n, void* stream);
+/* RawTensor::gpu_matmul_backward_a, gpu_ops.rs:408-428 (kernels.rs:1218-1310):
+ * grad_a[m,k] = grad[m,n] . b[k,n]^T. */
+int vh_matmul_backward_a(int dtype, const void* grad, const void* b, void* grad_a,
+                         int64_t m, int64_t k, int64_t n, void* stream);
+/* RawTensor::gpu_matmul_backward_b, gpu_ops.rs:430-450 (kernels.rs:1318-1400):
+ * grad_b[k,n] = a[m,k]^T . grad[m,n]. */
+int vh_matmul_backward_b(int dtype, const void* a, const void* grad, void* grad_b,
+                         int64_t m, int64_t k, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------ im2col */
+/* RawTensor::gpu_im2col, gpu_ops.rs:515-544 (kernels.rs:2110-2215): input is the
+ * already padded (B,C,H,W) tensor (conv.rs:1862-1879); col is
+ * [B*h_out*w_out, C*kh*kw], row (b,oh,ow), column (c,kh,kw). */
+int vh_im2col(int dtype, const void* input, void* col, int64_t batch, int64_t channels,
+              int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+              int64_t stride_h, int64_t stride_w, int64_t h_out, int64_t w_out,
+              void* stream);
+/* RawTensor::gpu_col2im, gpu_ops.rs:546-572 (kernels.rs:2223-2310): adjoint of
+ * vh_im2col (sum over every column entry that maps to an input element). */
+int vh_col2im(int dtype, const void* col, void* output, int64_t batch, int64_t channels,
+              int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+              int64_t stride_h, int64_t stride_w, int64_t h_out, int64_t w_out,
+              void* stream);
+
+/* ------------------------------------------------------------------ conv kernels */
+/* Common dimension list, in the reference's order (stride BEFORE pad):
+ * batch, in_channels, out_channels, height, width, kernel_h, kernel_w,
+ * stride_h, stride_w, pad_h, pad_w, h_out, w_out.
+ * h_out/w_out must equal (H + 2p - k)/s + 1, else VH_ERR_BAD_SHAPE. */
+
+/* RawTensor::gpu_direct_conv, gpu_ops.rs:574-620 (kernels.rs:2318-2417,
+ * direct_conv.wgsl:27-105): one output element per lane, fp32 accumulation. */
+int vh_direct_conv(int dtype, const void* input, const void* weight, void* output,
+                   int64_t batch, int64_t in_channels, int64_t out_channels, int64_t height,
+                   int64_t width, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                   int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
+                   int64_t w_out, void* stream);
+/* RawTensor::gpu_igemm, gpu_ops.rs:622-668 (kernels.rs:2425-2536, igemm.wgsl):
+ * implicit GEMM on MFMA (same math as vh_direct_conv). */
+int vh_igemm(int dtype, const void* input, const void* weight, void* output, int64_t batch,
+             int64_t in_channels, int64_t out_channels, int64_t height, int64_t width,
+             int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+             int64_t pad_h, int64_t pad_w, int64_t h_out, int64_t w_out, void* stream);
+/* RawTensor::gpu_conv_backward_input, gpu_ops.rs:670-716 (kernels.rs:2543-2640,
+ * conv_backward_input.wgsl): grad_input (B,C,H,W) from out_grad and weight. */
+int vh_conv_backward_input(int dtype, const void* out_grad, const void* weight,
+                           void* grad_input, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t height, int64_t width,
+                           int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                           int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
+                           int64_t w_out, void* stream);
+/* RawTensor::gpu_conv_backward_weight, gpu_ops.rs:718-764 (kernels.rs:2647-2744,
+ * conv_backward_weight.wgsl): grad_weight (O,C,KH,KW); note (out_grad, input). */
+int vh_conv_backward_weight(int dtype, const void* out_grad, const void* input,
+                            void* grad_weight, int64_t batch, int64_t in_channels,
+                            int64_t out_channels, int64_t height, int64_t width,
+                            int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                            int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
+                            int64_t w_out, void* stream);
+/* RawTensor::gpu_igemm_backward_input, gpu_ops.rs:766-812 (kernels.rs:2750-2847). */
+int vh_igemm_backward_input(int dtype, const void* out_grad, const void* weight,
+                            void* grad_input, int64_t batch, int64_t in_channels,
+                            int64_t out_channels, int64_t height, int64_t width,
+                            int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                            int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
+                            int64_t w_out, void* stream);
+/* RawTensor::gpu_igemm_backward_weight, gpu_ops.rs:814-861 (kernels.rs:2853-2950). */
+int vh_igemm_backward_weight(int dtype, const void* out_grad, const void* input,
+                             void* grad_weight, int64_t batch, int64_t in_channels,
+                             int64_t out_channels, int64_t height, int64_t width,
+                             int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                             int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
+                             int64_t w_out, void* stream);
+
+/* ------------------------------------------------------------------ layers */
+/* ConvAlgo::auto_select, conv.rs:29-69, verbatim rule (both branches); returns
+ * the vh_conv_algo value, or -1 if height/width < kernel_size. */
+int vh_conv_algo_auto_select(int64_t batch, int64_t channels, int64_t height, int64_t width,
+                             int64_t kernel_size, int has_gpu);
+/* The selector this library applies for VH_ALGO_AUTO on MI355X (same inputs as
+ * conv.rs:1821-1832 plus the full geometry); returns DIRECT, IM2COL or IGEMM. */
+int vh_conv_algo_select_mi355x(int64_t batch, int64_t in_channels, int64_t out_channels,
+                               int64_t height, int64_t width, int64_t kernel_h,
+                               int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                               int64_t pad_h, int64_t pad_w);
+
+/* Conv2d::forward, conv.rs:1787-1927: algorithm dispatch (algo may be AUTO) and
+ * the bias add of conv.rs:1915-1926 (bias may be NULL). *algo_used receives the
+ * algorithm that ran (may be NULL).  Dimensions as above without h_out/w_out. */
+int vh_conv2d_forward(int dtype, int algo, const void* input, const void* weight,
+                      const void* bias, void* output, int64_t batch, int64_t in_channels,
+                      int64_t out_channels, int64_t height, int64_t width, int64_t kernel_h,
+                      int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                      int64_t pad_w, int* algo_used, void* stream);
+/* Backward of Conv2d::forward: DirectConvGradFn (conv.rs:216-414),
+ * Im2colGradFn + MatMulGradFn (conv.rs:139-208, matmul.rs:378-460),
+ * IGEMMGradFn (conv.rs:617-768), bias grad via expand backward
+ * (movement.rs:441-485).  Any of grad_input / grad_weight / grad_bias may be
+ * NULL to skip it.  algo must be the algorithm the forward used (not AUTO). */
+int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* input,
+                       const void* weight, void* grad_input, void* grad_weight,
+                       void* grad_bias, int64_t batch, int64_t in_channels,
+                       int64_t out_channels, int64_t height, int64_t width, int64_t kernel_h,
+                       int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                       int64_t pad_w, void* stream);
+
+/* ConvTranspose2d forward, conv_transpose.rs:356-435 (CPU-only in the
+ * reference): weight IOHW [in, out, kh, kw], bias may be NULL, output
+ * (B, out, (H-1)s+kh-2p, (W-1)s+kw-2p). */
+int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight,
+                                const void* bias, void* output, int64_t batch,
+                                int64_t in_channels, int64_t out_channels, int64_t height,
+                                int64_t width, int64_t kernel_h, int64_t kernel_w,
+                                int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                                int64_t pad_w, void* stream);
+/* ConvTranspose2dGradFn::backward, conv_transpose.rs:161-341; NULL skips. */
+int vh_conv_transpose2d_backward(int dtype, const void* out_grad, const void* input,
+                                 const void* weight, void* grad_input, void* grad_weight,
+                                 void* grad_bias, int64_t batch, int64_t in_channels,
+                                 int64_t out_channels, int64_t height, int64_t width,
+                                 int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                                 int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 void* stream);
+
+/* Linear::forward, linear.rs:110-117: y[m,out] = x[m,in] . w[in,out] + bias
+ * (bias may be NULL). */
+int vh_linear_forward(int dtype, const void* x, const void* weight, const void* bias, void* y,
+                      int64_t m, int64_t in_features, int64_t out_features, void* stream);
+/* Linear backward: MatMulGradFn (matmul.rs:389-444) + BinaryGradFn bias
+ * reduction (binary.rs:533-598); NULL skips an output. */
+int vh_linear_backward(int dtype, const void* out_grad, const void* x, const void* weight,
+                       void* grad_x, void* grad_weight, void* grad_bias, int64_t m,
+                       int64_t in_features, int64_t out_features, void* stream);
+
+/* PixelShuffle::forward, pixelshuffle.rs:50-85: (B, C*r*r, H, W) -> (B, C, H*r, W*r);
+ * `channels` is the OUTPUT channel count C. */
+int vh_pixel_shuffle(int dtype, const void* input, void* output, int64_t batch,
+                     int64_t channels, int64_t height, int64_t width, int64_t upscale,
+                     void* stream);
+/* Backward: the inverse permutation (movement.rs:407-440). */
+int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
+                              int64_t batch, int64_t channels, int64_t height, int64_t width,
+                              int64_t upscale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VOLTA_HIP_H */

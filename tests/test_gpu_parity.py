@@ -1,0 +1,248 @@
+"""GPU parity: every hot-path entry point of libvolta_hip.so against the CPU oracle.
+
+Inputs are seeded numpy arrays; the same arrays (bf16-rounded for bf16) go to
+the oracle and, through the C ABI, to the MI355X.  Sizes keep the oracle to
+seconds; full-size configurations are covered in test_gpu_fullsize.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import volta_amd
+from volta_amd import nn as vnn
+from volta_amd import ops
+from tests.parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+DTYPES = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+
+def rng(seed):
+    return np.random.default_rng(seed)
+
+
+def prep(a, dt):
+    """numpy f32 -> (oracle input, device tensor) with identical values."""
+    a = np.ascontiguousarray(a, np.float32)
+    r = oracle.round_bf16(a) if dt == "bf16" else a
+    return r, torch.from_numpy(r).to(DEV, DTYPES[dt])
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------------ known answers
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_matmul_known_answers(dt):
+    a = torch.tensor([[1, 2], [3, 4]], dtype=DTYPES[dt], device=DEV)
+    b = torch.tensor([[5, 6], [7, 8]], dtype=DTYPES[dt], device=DEV)
+    assert host(ops.gpu_matmul(a, b, 2, 2, 2)).ravel().tolist() == [19, 22, 43, 50]  # tests/gpu_test.rs:46-60
+    a = torch.tensor([[1, 2, 3], [4, 5, 6]], dtype=DTYPES[dt], device=DEV)
+    b = torch.tensor([[1, 0], [0, 1], [1, 1]], dtype=DTYPES[dt], device=DEV)
+    assert host(ops.gpu_matmul(a, b, 2, 3, 2)).ravel().tolist() == [4, 5, 10, 11]  # lib.rs:4538-4547
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_linear_known_answer(dt):
+    lin = vnn.Linear(2, 3, device=DEV, dtype=DTYPES[dt])
+    lin.weight = torch.tensor([[1, 2, 3], [4, 5, 6]], dtype=DTYPES[dt], device=DEV)
+    lin.bias = torch.tensor([10, 20, 30], dtype=DTYPES[dt], device=DEV)
+    y = lin.forward(torch.ones(1, 2, dtype=DTYPES[dt], device=DEV))
+    assert host(y).ravel().tolist() == [15, 27, 39]  # lib.rs:4693-4712
+
+
+@pytest.mark.parametrize("algo", [vnn.ConvAlgo.Direct, vnn.ConvAlgo.Im2col, vnn.ConvAlgo.IGEMM])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_conv_all_ones_closed_form(algo, dt):
+    # conv.rs:2930-2976: C=2 -> 4, 3x3, pad 1, ones 1x2x8x8 => 2 * (#valid taps)
+    conv = vnn.Conv2d(2, 4, 3, 1, 1, use_bias=True, device=DEV, dtype=DTYPES[dt])
+    conv.weight = torch.ones(4, 2, 3, 3, dtype=DTYPES[dt], device=DEV)
+    conv.set_algo(algo)
+    y = host(conv.forward(torch.ones(1, 2, 8, 8, dtype=DTYPES[dt], device=DEV)))
+    taps = np.full(8, 3.0)
+    taps[0] = taps[-1] = 2.0
+    for o in range(4):
+        assert np.array_equal(y[0, o], 2.0 * np.outer(taps, taps))
+
+
+@pytest.mark.parametrize("algo", [vnn.ConvAlgo.Direct, vnn.ConvAlgo.Im2col, vnn.ConvAlgo.IGEMM])
+def test_conv_ramp_window_sums(algo):
+    # conv.rs:3021-3065
+    conv = vnn.Conv2d(1, 1, 2, 1, 0, use_bias=False, device=DEV)
+    conv.weight = torch.ones(1, 1, 2, 2, device=DEV)
+    conv.set_algo(algo)
+    x = torch.arange(16, dtype=torch.float32, device=DEV).reshape(1, 1, 4, 4)
+    y = host(conv.forward(x))[0, 0]
+    r = np.arange(16, dtype=np.float32).reshape(4, 4)
+    assert np.array_equal(y, r[:-1, :-1] + r[:-1, 1:] + r[1:, :-1] + r[1:, 1:])
+
+
+# ------------------------------------------------------------------ matmul family
+MM_CASES = [(37, 19, 23), (128, 256, 64), (130, 70, 200), (64, 1024, 96), (256, 512, 384), (3, 5, 300)]
+
+
+@pytest.mark.parametrize("mkn", MM_CASES)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_matmul_family(mkn, dt):
+    m, k, n = mkn
+    g = rng(m * 7 + n)
+    a, at = prep(g.standard_normal((m, k)), dt)
+    b, bt = prep(g.standard_normal((k, n)), dt)
+    gr, grt = prep(g.standard_normal((m, n)), dt)
+    assert_parity(host(ops.gpu_matmul(at, bt, m, k, n)), oracle.matmul(a, b), dt, "matmul")
+    assert_parity(host(ops.gpu_matmul_backward_a(grt, bt, m, k, n)), oracle.matmul_backward_a(gr, b), dt, "dA")
+    assert_parity(host(ops.gpu_matmul_backward_b(at, grt, m, k, n)), oracle.matmul_backward_b(a, gr), dt, "dB")
+
+
+@pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (1, 7, 5)])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_linear_fwd_bwd(shape, dt):
+    m, i, o = shape
+    g = rng(m + i + o)
+    x, xt = prep(g.standard_normal((m, i)), dt)
+    w, wt = prep(g.uniform(-0.5, 0.5, (i, o)), dt)
+    b, bt = prep(g.uniform(-1, 1, (o,)), dt)
+    dy, dyt = prep(g.standard_normal((m, o)), dt)
+    lin = vnn.Linear(i, o, device=DEV, dtype=DTYPES[dt])
+    lin.weight, lin.bias = wt, bt
+    assert_parity(host(lin.forward(xt)), oracle.linear_forward(x, w, b), dt, "y")
+    dx, dw, db = lin.backward(dyt, xt)
+    rdx, rdw, rdb = oracle.linear_backward(dy, x, w)
+    assert_parity(host(dx), rdx, dt, "dx")
+    assert_parity(host(dw), rdw, dt, "dw")
+    assert_parity(host(db), rdb, dt, "db")
+
+
+# ------------------------------------------------------------------ Conv2d
+CONV_CASES = [
+    # (B, C, O, H, W, K, S, P)
+    (2, 3, 8, 9, 7, 3, 1, 1),
+    (2, 16, 24, 10, 12, 3, 1, 1),
+    (2, 32, 64, 28, 28, 3, 1, 1),    # config 1 conv2, batch 2
+    (2, 1, 32, 28, 28, 3, 1, 1),     # config 1 conv1, batch 2
+    (2, 64, 128, 56, 56, 1, 2, 0),   # config 3 projection, batch 2
+    (2, 64, 64, 14, 14, 3, 1, 1),
+    (1, 3, 64, 32, 32, 5, 1, 2),     # config 5 conv1 shape, smaller image
+    (2, 8, 4, 9, 9, 4, 2, 1),
+    (3, 5, 7, 6, 5, 2, 3, 0),
+]
+
+
+def _conv_ids(c):
+    return "B{}C{}O{}H{}W{}K{}S{}P{}".format(*c)
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=_conv_ids)
+@pytest.mark.parametrize("algo", [vnn.ConvAlgo.Direct, vnn.ConvAlgo.Im2col, vnn.ConvAlgo.IGEMM])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_conv2d_fwd_bwd(case, algo, dt):
+    B, C, O, H, W, K, S, P = case
+    if algo == vnn.ConvAlgo.Direct and C * O * H * W > 2_000_000:
+        pytest.skip("direct kernels are for small layers")
+    g = rng(sum(case))
+    x, xt = prep(g.standard_normal((B, C, H, W)), dt)
+    w, wt = prep(g.standard_normal((O, C, K, K)) * np.sqrt(2.0 / (C * K * K)), dt)
+    b, bt = prep(g.uniform(-1, 1, (O,)), dt)
+    conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=DEV, dtype=DTYPES[dt])
+    conv.weight, conv.bias = wt, bt
+    conv.set_algo(algo)
+    y = conv.forward(xt)
+    assert conv.last_algo == algo
+    ref_y = oracle.direct_conv(x, w, (S, S), (P, P)) + b[None, :, None, None]
+    assert_parity(host(y), ref_y, dt, "y")
+    dy, dyt = prep(g.standard_normal(ref_y.shape), dt)
+    dx, dw, db = conv.backward(dyt, xt)
+    assert_parity(host(dx), oracle.direct_conv_backward_input(dy, w, x.shape, (S, S), (P, P)), dt, "dx")
+    assert_parity(host(dw), oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P)), dt, "dw")
+    assert_parity(host(db), oracle.conv_bias_grad(dy), dt, "db")
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_gpu_ops_boundary_functions(dt):
+    # The gpu_ops.rs-named entry points, including argument order (stride before pad).
+    B, C, O, H, W, K, S, P = 2, 8, 16, 11, 9, 3, 2, 1
+    HO, WO = oracle.conv_out(H, K, S, P), oracle.conv_out(W, K, S, P)
+    g = rng(5)
+    x, xt = prep(g.standard_normal((B, C, H, W)), dt)
+    w, wt = prep(g.standard_normal((O, C, K, K)) * 0.2, dt)
+    dy, dyt = prep(g.standard_normal((B, O, HO, WO)), dt)
+    dims = (B, C, O, H, W, K, K, S, S, P, P, HO, WO)
+    ry = oracle.direct_conv(x, w, (S, S), (P, P))
+    rdx = oracle.direct_conv_backward_input(dy, w, x.shape, (S, S), (P, P))
+    rdw = oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P))
+    assert_parity(host(ops.gpu_direct_conv(xt, wt, *dims)), ry, dt, "direct")
+    assert_parity(host(ops.gpu_igemm(xt, wt, *dims)), ry, dt, "igemm")
+    assert_parity(host(ops.gpu_conv_backward_input(dyt, wt, *dims)), rdx, dt, "direct dx")
+    assert_parity(host(ops.gpu_igemm_backward_input(dyt, wt, *dims)), rdx, dt, "igemm dx")
+    assert_parity(host(ops.gpu_conv_backward_weight(dyt, xt, *dims)), rdw, dt, "direct dw")
+    assert_parity(host(ops.gpu_igemm_backward_weight(dyt, xt, *dims)), rdw, dt, "igemm dw")
+    # im2col / col2im on the padded input, exact copies (sums for col2im)
+    xp = oracle.pad(x, P, P)
+    xpt = torch.from_numpy(xp).to(DEV, DTYPES[dt])
+    HP, WP = xp.shape[2:]
+    col = ops.gpu_im2col(xpt, B, C, HP, WP, K, K, S, S, HO, WO)
+    assert np.array_equal(host(col), oracle.im2col(xp, (K, K), (S, S)))
+    gcol, gcolt = prep(g.standard_normal(col.shape), dt)
+    back = ops.gpu_col2im(gcolt, B, C, HP, WP, K, K, S, S, HO, WO)
+    assert_parity(host(back), oracle.col2im(gcol, xp.shape, (K, K), (S, S)), dt, "col2im")
+
+
+def test_bad_shape_is_an_error_not_a_crash():
+    x = torch.zeros(1, 2, 5, 5, device=DEV)
+    w = torch.zeros(3, 2, 3, 3, device=DEV)
+    with pytest.raises(volta_amd.VoltaHipError) as e:
+        ops.gpu_igemm(x, w, 1, 2, 3, 5, 5, 3, 3, 1, 1, 1, 1, 4, 5)  # h_out should be 5
+    assert e.value.status == 2
+    y = ops.gpu_igemm(x, w, 0, 2, 3, 5, 5, 3, 3, 1, 1, 1, 1, 5, 5)  # empty batch is a no-op
+    assert y.shape == (0, 3, 5, 5)
+
+
+# ------------------------------------------------------------------ ConvTranspose2d
+CT_CASES = [
+    # (B, CI, CO, H, W, K, S, P)
+    (2, 4, 3, 4, 4, 4, 2, 1),
+    (4, 100, 32, 1, 1, 4, 1, 0),     # config 4 layer 1 (512 -> 32 out channels)
+    (2, 64, 32, 8, 8, 4, 2, 1),      # config 4 inner layer shape
+    (2, 16, 3, 16, 16, 4, 2, 1),     # config 4 last layer (to RGB)
+    (1, 5, 6, 5, 3, 3, 2, 1),
+]
+
+
+@pytest.mark.parametrize("case", CT_CASES, ids=_conv_ids)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_conv_transpose2d_fwd_bwd(case, dt):
+    B, CI, CO, H, W, K, S, P = case
+    g = rng(sum(case) + 1)
+    x, xt = prep(g.standard_normal((B, CI, H, W)), dt)
+    w, wt = prep(g.normal(0, 0.02 * 10, (CI, CO, K, K)), dt)
+    b, bt = prep(g.uniform(-1, 1, (CO,)), dt)
+    ct = vnn.ConvTranspose2d(CI, CO, K, S, P, device=DEV, dtype=DTYPES[dt])
+    ct.weight, ct.bias = wt, bt
+    y = ct.forward(xt)
+    ref_y = oracle.conv_transpose_forward(x, w, b, (S, S), (P, P))
+    assert_parity(host(y), ref_y, dt, "y")
+    dy, dyt = prep(g.standard_normal(ref_y.shape), dt)
+    dx, dw, db = ct.backward(dyt, xt)
+    rdx, rdw, rdb = oracle.conv_transpose_backward(dy, x, w, (S, S), (P, P))
+    assert_parity(host(dx), rdx, dt, "dx")
+    assert_parity(host(dw), rdw, dt, "dw")
+    assert_parity(host(db), rdb, dt, "db")
+
+
+# ------------------------------------------------------------------ PixelShuffle
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 27, 8, 9, 3), (1, 12, 4, 4, 2), (2, 3, 5, 7, 1)])
+def test_pixel_shuffle_exact(shape, dt):
+    B, CR, H, W, r = shape
+    g = rng(CR)
+    x, xt = prep(g.standard_normal((B, CR, H, W)), dt)
+    ps = vnn.PixelShuffle(r)
+    y = ps.forward(xt)
+    assert np.array_equal(host(y), oracle.pixel_shuffle(x, r))
+    dy, dyt = prep(g.standard_normal(y.shape), dt)
+    assert np.array_equal(host(ps.backward(dyt)), oracle.pixel_shuffle_backward(dy, r))

@@ -1,0 +1,89 @@
+// vh_common.hpp -- shared device/host helpers for libvolta_hip (gfx950 only).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/volta_hip.h"
+
+namespace vh {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+
+// bf16 is carried as raw uint16_t bits in memory.
+struct bf16 {
+  uint16_t bits;
+};
+
+__host__ __device__ inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+// Round-to-nearest-even, NaN kept quiet (same rule as half::bf16::from_f32).
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  using storage = float;
+  static constexpr int vec = 4;  // elements per 16-byte unit
+  __device__ static inline float to_f32(float v) { return v; }
+  __device__ static inline float from_f32(float v) { return v; }
+};
+template <> struct Elem<bf16> {
+  using storage = uint16_t;
+  static constexpr int vec = 8;
+  __device__ static inline float to_f32(uint16_t v) { return bf16_to_f32(v); }
+  __device__ static inline uint16_t from_f32(float v) { return f32_to_bf16(v); }
+};
+
+// Division by a runtime constant via multiply-high (Granlund-Montgomery,
+// round-up variant). Valid for numerators < 2^31 and divisors in [1, 2^31).
+struct FastDiv {
+  uint32_t d, m, s;
+  FastDiv() : d(1), m(0), s(0) {}
+  explicit FastDiv(uint32_t div) : d(div) {
+    s = 0;
+    while ((1u << s) < div) ++s;
+    uint64_t one = 1;
+    m = (uint32_t)(((one << 32) * ((one << s) - div)) / div + 1);
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    uint32_t t = __umulhi(n, m);
+    return (t + n) >> s;
+  }
+  __device__ __forceinline__ void divmod(uint32_t n, uint32_t& q, uint32_t& r) const {
+    q = div(n);
+    r = n - q * d;
+  }
+};
+
+// Record an error message for vh_last_error(); returns the status.
+int set_error(int status, const char* fmt, ...);
+
+}  // namespace vh
+
+#define VH_HIP_CHECK(expr)                                                          \
+  do {                                                                              \
+    hipError_t _e = (expr);                                                         \
+    if (_e != hipSuccess)                                                           \
+      return ::vh::set_error(_e == hipErrorOutOfMemory ? VH_ERR_OOM : VH_ERR_LAUNCH, \
+                             "%s failed: %s", #expr, hipGetErrorString(_e));        \
+  } while (0)
+
+#define VH_LAUNCH_CHECK()                                                           \
+  do {                                                                              \
+    hipError_t _e = hipGetLastError();                                              \
+    if (_e != hipSuccess)                                                           \
+      return ::vh::set_error(VH_ERR_LAUNCH, "kernel launch failed: %s",            \
+                             hipGetErrorString(_e));                                \
+  } while (0)

@@ -1,0 +1,116 @@
+// vh_gemm.hip -- instantiations and host dispatch of the MFMA implicit GEMM.
+#include <algorithm>
+
+#include "vh_kernels.hpp"
+
+namespace vh {
+
+ConvGeom make_geom(int N, int C, int H, int W, int O, int R, int S, int P, int Q, int sh, int sw, int ph,
+                   int pw) {
+  ConvGeom g;
+  g.N = N; g.C = C; g.H = H; g.W = W; g.O = O; g.R = R; g.S = S; g.P = P; g.Q = Q;
+  g.sh = sh; g.sw = sw; g.ph = ph; g.pw = pw;
+  g.fPQ = FastDiv((uint32_t)std::max(1, P * Q));
+  g.fQ = FastDiv((uint32_t)std::max(1, Q));
+  g.fHW = FastDiv((uint32_t)std::max(1, H * W));
+  g.fW = FastDiv((uint32_t)std::max(1, W));
+  g.fC = FastDiv((uint32_t)std::max(1, C));
+  g.fO = FastDiv((uint32_t)std::max(1, O));
+  g.fS = FastDiv((uint32_t)std::max(1, S));
+  return g;
+}
+
+namespace {
+
+template <typename T> constexpr int bk_for() { return Elem<T>::vec == 8 ? 32 : 16; }
+
+struct Tile {
+  int bm, bn;
+};
+
+Tile pick_tile(int M, int N) {
+  Tile t{128, 128};
+  if (M <= 64) t.bm = 64;
+  if (N <= 64) t.bn = 64;
+  return t;
+}
+
+template <typename T, int AK, int BKIND, int OUT, int BM, int BN>
+int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
+  constexpr int BK = bk_for<T>();
+  IgemmArgs a = p.args;
+  const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+  dim3 grid((unsigned)tiles, 1, (unsigned)p.splits);
+  if (p.splits > 1) {
+    IgemmArgs pa = a;
+    pa.d = ws;
+    igemm_kernel<T, AK, BKIND, OK_PARTIAL, BM, BN, BK><<<grid, 256, 0, st>>>(pa);
+    VH_LAUNCH_CHECK();
+    long total = (long)a.M * a.N;
+    int g = (int)std::min<long>((total + 255) / 256, 4096);
+    splitk_reduce_kernel<T, OUT><<<g, 256, 0, st>>>(a, ws, p.splits);
+    VH_LAUNCH_CHECK();
+  } else {
+    igemm_kernel<T, AK, BKIND, OUT, BM, BN, BK><<<grid, 256, 0, st>>>(a);
+    VH_LAUNCH_CHECK();
+  }
+  return VH_OK;
+}
+
+template <typename T, int AK, int BKIND, int OUT>
+int launch_kinds(IgemmPlan& p, float* ws, hipStream_t st) {
+  Tile t = pick_tile(p.args.M, p.args.N);
+  if (t.bm == 128 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 128, 128>(p, ws, st);
+  if (t.bm == 64 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 64, 128>(p, ws, st);
+  if (t.bm == 128 && t.bn == 64) return launch_tile<T, AK, BKIND, OUT, 128, 64>(p, ws, st);
+  return launch_tile<T, AK, BKIND, OUT, 64, 64>(p, ws, st);
+}
+
+template <typename T>
+int launch_typed(IgemmPlan& p, float* ws, hipStream_t st) {
+#define VH_COMBO(A, B, O)                                          \
+  if (p.akind == A && p.bkind == B && p.okind == O) return launch_kinds<T, A, B, O>(p, ws, st);
+  VH_COMBO(KD_DENSE_K, KD_DENSE_MN, OK_DENSE)            // matmul, Linear forward
+  VH_COMBO(KD_DENSE_K, KD_DENSE_K, OK_DENSE)             // matmul backward A
+  VH_COMBO(KD_DENSE_MN, KD_DENSE_MN, OK_DENSE)           // matmul backward B
+  VH_COMBO(KD_DENSE_K, KD_CONV_FWD_X, OK_NCHW)           // conv fwd, convT dX
+  VH_COMBO(KD_DENSE_K, KD_CONV_DGRAD_DY, OK_NCHW)        // conv dgrad, convT fwd
+  VH_COMBO(KD_CONV_WGRAD_DY, KD_CONV_WGRAD_X, OK_WGRAD_OIHW)  // conv wgrad, convT dW
+  VH_COMBO(KD_DENSE_K, KD_DENSE_K, OK_NCHW)              // im2col conv fwd
+  VH_COMBO(KD_DENSE_MN, KD_CONV_FWD_X, OK_DENSE_T)       // im2col conv dcol
+  VH_COMBO(KD_CONV_WGRAD_DY, KD_DENSE_MN, OK_DENSE)      // im2col conv dW
+#undef VH_COMBO
+  return set_error(VH_ERR_BAD_ARG, "unsupported implicit-GEMM operand combination %d/%d/%d", p.akind,
+                   p.bkind, p.okind);
+}
+
+}  // namespace
+
+int pick_splits(int M, int N, int K, int dtype) {
+  Tile t = pick_tile(M, N);
+  const int bk = dtype == VH_BF16 ? 32 : 16;
+  long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+  if (tiles >= 512) return 1;
+  long want = (512 + tiles - 1) / tiles;
+  long maxk = std::max<long>(1, K / (bk * 8));
+  return (int)std::max<long>(1, std::min<long>(std::min(want, maxk), 256));
+}
+
+size_t igemm_prepare(IgemmPlan& p) {
+  const int bk = p.dtype == VH_BF16 ? 32 : 16;
+  int splits = std::max(1, p.splits);
+  int K = std::max(1, p.args.K);
+  int chunk = (K + splits - 1) / splits;
+  chunk = (chunk + bk - 1) / bk * bk;
+  p.args.k_chunk = chunk;
+  p.splits = (K + chunk - 1) / chunk;
+  return p.splits > 1 ? (size_t)p.splits * p.args.M * p.args.N * sizeof(float) : 0;
+}
+
+int run_igemm(IgemmPlan& p, float* ws, hipStream_t st) {
+  if (p.args.M <= 0 || p.args.N <= 0) return VH_OK;
+  if (p.dtype == VH_BF16) return launch_typed<bf16>(p, ws, st);
+  return launch_typed<float>(p, ws, st);
+}
+
+}  // namespace vh

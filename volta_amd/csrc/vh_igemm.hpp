@@ -1,0 +1,425 @@
+// vh_igemm.hpp -- generic MFMA implicit-GEMM kernel for gfx950.
+//
+// One kernel template computes D[M][N] = sum_k A(row m, k) * B(row n, k) with fp32
+// accumulation, where each operand is fetched by an "operand kind" (a dense
+// matrix in either orientation, or one of the implicit-im2col gathers of a
+// convolution pass) and the result is stored by an "output kind" (row-major,
+// NCHW scatter, OIHW weight-gradient scatter, or fp32 split-K partials).
+//
+// Tiling: 256 threads = 4 waves (2 x 2), block tile BM x BN, K step BK.
+//  * bf16: v_mfma_f32_32x32x16_bf16, wave tile (BM/2) x (BN/2) of 32x32 tiles.
+//  * f32 : v_mfma_f32_16x16x4_f32,  wave tile (BM/2) x (BN/2) of 16x16 tiles.
+// LDS holds both operands K-major ([row][k], 16-byte units of VEC elements, row
+// pitch BK+PADK elements = 80 bytes) and is double-buffered: global loads for
+// step k+1 are in flight while the MFMAs of step k run.
+#pragma once
+#include "vh_common.hpp"
+
+namespace vh {
+
+enum OpndKind : int {
+  KD_DENSE_K = 0,       // elem(r,k) = p[r*ld + k]
+  KD_DENSE_MN = 1,      // elem(r,k) = p[k*ld + r]
+  KD_CONV_FWD_X = 2,    // r = out position (n,p,q); k = (kh,kw,c): x[n][c][p*sh+kh-ph][q*sw+kw-pw]
+  KD_CONV_DGRAD_DY = 3, // r = in position (n,h,w); k = (kh,kw,o): dy[n][o][(h+ph-kh)/sh][(w+pw-kw)/sw]
+  KD_CONV_WGRAD_DY = 4, // r = o; k = out position (n,p,q): dy[n][o][p][q]
+  KD_CONV_WGRAD_X = 5,  // r = (kh,kw,c); k = out position (n,p,q): x[n][c][p*sh+kh-ph][q*sw+kw-pw]
+};
+
+enum OutKind : int {
+  OK_DENSE = 0,      // d[row*ldd + col]
+  OK_DENSE_T = 1,    // d[col*ldd + row]
+  OK_NCHW = 2,       // row = channel (M channels), col = (n, hw) over N*HWo
+  OK_WGRAD_OIHW = 3, // row = o, col = (kh,kw,c) -> d[o][c][kh][kw]
+  OK_PARTIAL = 4,    // fp32 ws[(z*M + row)*N + col]
+};
+
+// Convolution geometry (x: N,C,H,W; weight O,C,R,S; y: N,O,P,Q).
+struct ConvGeom {
+  int N, C, H, W, O, R, S, P, Q, sh, sw, ph, pw;
+  FastDiv fPQ, fQ, fHW, fW, fC, fO, fS;
+};
+
+struct Operand {
+  const void* p;
+  int ld;      // dense leading dimension (elements)
+  int rows;    // valid rows (M for A, N for B)
+  int vec_ok;  // dense K-major: 16-byte vector loads allowed (aligned ld/base)
+};
+
+struct IgemmArgs {
+  int M, N, K;
+  Operand a, b;
+  void* d;
+  int ldd;
+  const void* bias;  // same dtype as T; nullptr = none
+  int bias_mode;     // 0 none, 1 per row, 2 per column
+  int k_chunk;       // K range per blockIdx.z (multiple of BK)
+  int hwo;           // OK_NCHW: spatial size of the output
+  FastDiv f_hwo;     // OK_NCHW: divide by hwo
+  FastDiv f_cw;      // OK_WGRAD_OIHW: divide by C (channels of the weight grad)
+  int wg_c, wg_rs;   // OK_WGRAD_OIHW: C and R*S
+  ConvGeom g;
+};
+
+// ---------------------------------------------------------------- operand loaders
+// Each thread fills "units" of VEC consecutive k for one operand row.
+template <typename T, int KIND>
+struct Loader {
+  using S = typename Elem<T>::storage;
+  static constexpr int VEC = Elem<T>::vec;
+  static constexpr bool kFastest =
+      (KIND == KD_DENSE_K || KIND == KD_CONV_WGRAD_DY || KIND == KD_CONV_WGRAD_X);
+
+  // per-unit row state
+  int row;
+  bool valid;
+  int s0, s1, s2;  // kind-specific precomputed quantities
+  const S* base;
+
+  __device__ __forceinline__ void init(const Operand& op, const ConvGeom& g, int r) {
+    row = r;
+    valid = r < op.rows;
+    base = reinterpret_cast<const S*>(op.p);
+    if (!valid) return;
+    if (KIND == KD_CONV_FWD_X) {
+      uint32_t n, pq, p, q;
+      g.fPQ.divmod((uint32_t)r, n, pq);
+      g.fQ.divmod(pq, p, q);
+      s0 = (int)p * g.sh - g.ph;
+      s1 = (int)q * g.sw - g.pw;
+      s2 = (int)n * g.C * g.H * g.W;
+    } else if (KIND == KD_CONV_DGRAD_DY) {
+      uint32_t n, hw, h, w;
+      g.fHW.divmod((uint32_t)r, n, hw);
+      g.fW.divmod(hw, h, w);
+      s0 = (int)h + g.ph;
+      s1 = (int)w + g.pw;
+      s2 = (int)n * g.O * g.P * g.Q;
+    } else if (KIND == KD_CONV_WGRAD_DY) {
+      s0 = r * g.P * g.Q;
+    } else if (KIND == KD_CONV_WGRAD_X) {
+      uint32_t rs, c, kh, kw;
+      g.fC.divmod((uint32_t)r, rs, c);
+      g.fS.divmod(rs, kh, kw);
+      s0 = (int)kh - g.ph;
+      s1 = (int)kw - g.pw;
+      s2 = (int)c * g.H * g.W;
+    }
+  }
+
+  // Loads VEC elements for k0..k0+VEC-1 into out (zeros where out of range).
+  __device__ __forceinline__ void load(const Operand& op, const ConvGeom& g, int k0, int K,
+                                       S (&out)[VEC]) const {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[j] = S(0);
+    if (!valid || k0 >= K) return;
+    if (KIND == KD_DENSE_K) {
+      const S* src = base + (long)row * op.ld + k0;
+      if (op.vec_ok && k0 + VEC <= K) {
+        *reinterpret_cast<uint4*>(out) = *reinterpret_cast<const uint4*>(src);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j)
+          if (k0 + j < K) out[j] = src[j];
+      }
+    } else if (KIND == KD_DENSE_MN) {
+      const S* src = base + (long)k0 * op.ld + row;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j)
+        if (k0 + j < K) out[j] = src[(long)j * op.ld];
+    } else if (KIND == KD_CONV_FWD_X) {
+      const int HW = g.H * g.W;
+      if ((g.C % VEC) == 0) {
+        uint32_t rs, c0, kh, kw;
+        g.fC.divmod((uint32_t)k0, rs, c0);
+        g.fS.divmod(rs, kh, kw);
+        int h = s0 + (int)kh, w = s1 + (int)kw;
+        if (h >= 0 && h < g.H && w >= 0 && w < g.W) {
+          const S* src = base + s2 + (int)c0 * HW + h * g.W + w;
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) out[j] = src[j * HW];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          int k = k0 + j;
+          if (k < K) {
+            uint32_t rs, c, kh, kw;
+            g.fC.divmod((uint32_t)k, rs, c);
+            g.fS.divmod(rs, kh, kw);
+            int h = s0 + (int)kh, w = s1 + (int)kw;
+            if (h >= 0 && h < g.H && w >= 0 && w < g.W) out[j] = base[s2 + (int)c * HW + h * g.W + w];
+          }
+        }
+      }
+    } else if (KIND == KD_CONV_DGRAD_DY) {
+      const int PQ = g.P * g.Q;
+      if ((g.O % VEC) == 0) {
+        uint32_t rs, o0, kh, kw;
+        g.fO.divmod((uint32_t)k0, rs, o0);
+        g.fS.divmod(rs, kh, kw);
+        int t = s0 - (int)kh, u = s1 - (int)kw;
+        if (t >= 0 && u >= 0) {
+          int p = t / g.sh, q = u / g.sw;
+          if (p * g.sh == t && q * g.sw == u && p < g.P && q < g.Q) {
+            const S* src = base + s2 + (int)o0 * PQ + p * g.Q + q;
+#pragma unroll
+            for (int j = 0; j < VEC; ++j) out[j] = src[j * PQ];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          int k = k0 + j;
+          if (k < K) {
+            uint32_t rs, o, kh, kw;
+            g.fO.divmod((uint32_t)k, rs, o);
+            g.fS.divmod(rs, kh, kw);
+            int t = s0 - (int)kh, u = s1 - (int)kw;
+            if (t >= 0 && u >= 0) {
+              int p = t / g.sh, q = u / g.sw;
+              if (p * g.sh == t && q * g.sw == u && p < g.P && q < g.Q)
+                out[j] = base[s2 + (int)o * PQ + p * g.Q + q];
+            }
+          }
+        }
+      }
+    } else if (KIND == KD_CONV_WGRAD_DY) {
+      const int PQ = g.P * g.Q;
+      uint32_t n, pq;
+      g.fPQ.divmod((uint32_t)k0, n, pq);
+      const S* src = base + (int)n * g.O * PQ + s0 + (int)pq;
+      if ((PQ % VEC) == 0 && op.vec_ok && k0 + VEC <= K) {
+        *reinterpret_cast<uint4*>(out) = *reinterpret_cast<const uint4*>(src);
+      } else {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          if (k0 + j < K) {
+            out[j] = src[0];
+          }
+          ++pq;
+          ++src;
+          if ((int)pq == PQ) {  // next image: skip the other channels
+            pq = 0;
+            src += (g.O - 1) * PQ;
+          }
+        }
+      }
+    } else if (KIND == KD_CONV_WGRAD_X) {
+      uint32_t n, pq, p, q;
+      g.fPQ.divmod((uint32_t)k0, n, pq);
+      g.fQ.divmod(pq, p, q);
+      const int HW = g.H * g.W;
+      int nb = (int)n * g.C * HW + s2;
+      int pi = (int)p, qi = (int)q;
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        if (k0 + j < K) {
+          int h = pi * g.sh + s0, w = qi * g.sw + s1;
+          if (h >= 0 && h < g.H && w >= 0 && w < g.W) out[j] = base[nb + h * g.W + w];
+        }
+        if (++qi == g.Q) {
+          qi = 0;
+          if (++pi == g.P) {
+            pi = 0;
+            nb += g.C * HW;
+          }
+        }
+      }
+    }
+  }
+};
+
+// ---------------------------------------------------------------- MFMA traits
+template <typename T> struct Mma;
+
+template <> struct Mma<bf16> {
+  static constexpr int TM = 32, TN = 32, TK = 16, NACC = 16;
+  using acc_t = f32x16;
+  // lane l supplies row l%32, k = 8*(l/32)..+8 of the 32x16 operand slice
+  __device__ static inline int frag_row(int lane) { return lane & 31; }
+  __device__ static inline int frag_k(int lane) { return (lane >> 5) * 8; }
+  __device__ static inline acc_t mma(const uint16_t* a, const uint16_t* b, acc_t c) {
+    bf16x8 av = *reinterpret_cast<const bf16x8*>(a);
+    bf16x8 bv = *reinterpret_cast<const bf16x8*>(b);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, c, 0, 0, 0);
+  }
+  // accumulator register v of lane l holds (row, col) of the 32x32 tile
+  __device__ static inline int acc_row(int lane, int v) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+  __device__ static inline int acc_col(int lane) { return lane & 31; }
+};
+
+template <> struct Mma<float> {
+  static constexpr int TM = 16, TN = 16, TK = 4, NACC = 4;
+  using acc_t = f32x4;
+  __device__ static inline int frag_row(int lane) { return lane & 15; }
+  __device__ static inline int frag_k(int lane) { return lane >> 4; }
+  __device__ static inline acc_t mma(const float* a, const float* b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(*a, *b, c, 0, 0, 0);
+  }
+  __device__ static inline int acc_row(int lane, int v) { return (lane >> 4) * 4 + v; }
+  __device__ static inline int acc_col(int lane) { return lane & 15; }
+};
+
+// ---------------------------------------------------------------- output store
+template <typename T, int OUT>
+__device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int col, float v) {
+  using S = typename Elem<T>::storage;
+  if (row >= args.M || col >= args.N) return;
+  if (OUT == OK_PARTIAL) {
+    float* ws = reinterpret_cast<float*>(args.d);
+    ws[((long)blockIdx.z * args.M + row) * args.N + col] = v;
+    return;
+  }
+  if (args.bias_mode == 1) v += Elem<T>::to_f32(reinterpret_cast<const S*>(args.bias)[row]);
+  else if (args.bias_mode == 2) v += Elem<T>::to_f32(reinterpret_cast<const S*>(args.bias)[col]);
+  S* d = reinterpret_cast<S*>(args.d);
+  long idx;
+  if (OUT == OK_DENSE) {
+    idx = (long)row * args.ldd + col;
+  } else if (OUT == OK_DENSE_T) {
+    idx = (long)col * args.ldd + row;
+  } else if (OUT == OK_NCHW) {
+    uint32_t n, hw;
+    args.f_hwo.divmod((uint32_t)col, n, hw);
+    idx = ((long)n * args.M + row) * args.hwo + hw;
+  } else {  // OK_WGRAD_OIHW
+    uint32_t rs, c;
+    args.f_cw.divmod((uint32_t)col, rs, c);
+    idx = ((long)row * args.wg_c + c) * args.wg_rs + rs;
+  }
+  d[idx] = Elem<T>::from_f32(v);
+}
+
+// ---------------------------------------------------------------- the kernel
+template <typename T, int AK, int BKIND, int OUT, int BM, int BN, int BK>
+__global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
+  using S = typename Elem<T>::storage;
+  using MM = Mma<T>;
+  constexpr int VEC = Elem<T>::vec;
+  constexpr int PADK = VEC;            // row pitch (BK + VEC) elements
+  constexpr int LDK = BK + PADK;
+  constexpr int KU = BK / VEC;         // units per row per K step
+  constexpr int UA = BM * KU / 256;    // units per thread, A
+  constexpr int UB = BN * KU / 256;    // units per thread, B
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int FM = WM / MM::TM, FN = WN / MM::TN;
+  static_assert(UA >= 1 && UB >= 1 && (BM * KU) % 256 == 0 && (BN * KU) % 256 == 0, "tile");
+
+  __shared__ __attribute__((aligned(16))) S smem[2 * (BM + BN) * LDK];
+  S* As = smem;
+  S* Bs = smem + 2 * BM * LDK;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave >> 1) * WM, wn = (wave & 1) * WN;
+
+  // XCD-aware tile order: consecutive logical tiles land on one XCD (the
+  // hardware deals workgroups round-robin over 8 XCDs), column-major groups of 8
+  // row tiles so a group shares its B panel in that XCD's L2.
+  const int tiles_m = (args.M + BM - 1) / BM, tiles_n = (args.N + BN - 1) / BN;
+  const int nt = tiles_m * tiles_n;
+  int pid = blockIdx.x;
+  if ((nt & 7) == 0) pid = (pid & 7) * (nt >> 3) + (pid >> 3);
+  const int group = 8;
+  const int gsz = group * tiles_n;
+  const int gid = pid / gsz, first_m = gid * group;
+  const int gm = min(tiles_m - first_m, group);
+  const int tm = first_m + (pid % gsz) % gm, tn = (pid % gsz) / gm;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int kb = blockIdx.z * args.k_chunk;
+  const int ke = min(args.K, kb + args.k_chunk);
+  const int nk = (ke - kb + BK - 1) / BK;
+
+  Loader<T, AK> la[UA];
+  Loader<T, BKIND> lb[UB];
+  int a_k[UA], a_r[UA], b_k[UB], b_r[UB];
+#pragma unroll
+  for (int u = 0; u < UA; ++u) {
+    int id = tid + u * 256;
+    a_r[u] = Loader<T, AK>::kFastest ? id / KU : id % BM;
+    a_k[u] = Loader<T, AK>::kFastest ? (id % KU) * VEC : (id / BM) * VEC;
+    la[u].init(args.a, args.g, m0 + a_r[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < UB; ++u) {
+    int id = tid + u * 256;
+    b_r[u] = Loader<T, BKIND>::kFastest ? id / KU : id % BN;
+    b_k[u] = Loader<T, BKIND>::kFastest ? (id % KU) * VEC : (id / BN) * VEC;
+    lb[u].init(args.b, args.g, n0 + b_r[u]);
+  }
+
+  S ra[UA][VEC], rb[UB][VEC];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < UA; ++u) la[u].load(args.a, args.g, k0 + a_k[u], ke, ra[u]);
+#pragma unroll
+    for (int u = 0; u < UB; ++u) lb[u].load(args.b, args.g, k0 + b_k[u], ke, rb[u]);
+  };
+  auto sstore = [&](int buf) {
+    S* a = As + buf * BM * LDK;
+    S* b = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int u = 0; u < UA; ++u)
+      *reinterpret_cast<uint4*>(a + a_r[u] * LDK + a_k[u]) = *reinterpret_cast<const uint4*>(ra[u]);
+#pragma unroll
+    for (int u = 0; u < UB; ++u)
+      *reinterpret_cast<uint4*>(b + b_r[u] * LDK + b_k[u]) = *reinterpret_cast<const uint4*>(rb[u]);
+  };
+
+  typename MM::acc_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < MM::NACC; ++v) acc[i][j][v] = 0.f;
+
+  if (nk > 0) {
+    gload(kb);
+    sstore(0);
+  }
+  __syncthreads();
+  const int fr = MM::frag_row(lane), fk = MM::frag_k(lane);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) gload(kb + (kt + 1) * BK);
+    const S* a = As + buf * BM * LDK;
+    const S* b = Bs + buf * BN * LDK;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += MM::TK) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = MM::mma(a + (wm + i * MM::TM + fr) * LDK + kk + fk,
+                              b + (wn + j * MM::TN + fr) * LDK + kk + fk, acc[i][j]);
+    }
+    if (kt + 1 < nk) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < MM::NACC; ++v)
+        store_out<T, OUT>(args, m0 + wm + i * MM::TM + MM::acc_row(lane, v),
+                          n0 + wn + j * MM::TN + MM::acc_col(lane), acc[i][j][v]);
+}
+
+// Split-K reduction: out(row, col) = bias + sum_z ws[z][row][col], stored by OUT.
+template <typename T, int OUT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(IgemmArgs args, const float* ws, int splits) {
+  long total = (long)args.M * args.N;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += ws[(long)z * total + i];
+    int row = (int)(i / args.N), col = (int)(i % args.N);
+    store_out<T, OUT>(args, row, col, s);
+  }
+}
+
+}  // namespace vh

@@ -1,0 +1,460 @@
+// vh_kernels.hip -- kernels other than the MFMA implicit GEMM, plus the typed
+// launch helpers the C ABI layer calls.  gfx950 only.
+#include "vh_kernels.hpp"
+
+#include <algorithm>
+
+namespace vh {
+
+static inline int grid_for(long n, int per_block = 256, int cap = 65535 * 8) {
+  long g = (n + per_block - 1) / per_block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (int)g;
+}
+
+// ============================================================== direct conv
+// Volta's direct_conv.wgsl:27-105 assigns one output element per invocation; so
+// does this kernel (consecutive lanes take consecutive ow, so x loads and y
+// stores coalesce).  fp32 accumulation in the reference's order ic -> kh -> kw
+// (conv.rs:1370-1407).
+template <typename T>
+__global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                         const typename Elem<T>::storage* __restrict__ w,
+                                                         typename Elem<T>::storage* __restrict__ y,
+                                                         ConvGeom g, long total) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int q = (int)(i % g.Q);
+    long t = i / g.Q;
+    int p = (int)(t % g.P);
+    t /= g.P;
+    int o = (int)(t % g.O);
+    int n = (int)(t / g.O);
+    float s = 0.f;
+    const auto* xn = x + (long)n * g.C * g.H * g.W;
+    const auto* wo = w + (long)o * g.C * g.R * g.S;
+    for (int c = 0; c < g.C; ++c)
+      for (int r = 0; r < g.R; ++r) {
+        int h = p * g.sh + r - g.ph;
+        if (h < 0 || h >= g.H) continue;
+        for (int k = 0; k < g.S; ++k) {
+          int ww = q * g.sw + k - g.pw;
+          if (ww < 0 || ww >= g.W) continue;
+          s += Elem<T>::to_f32(xn[((long)c * g.H + h) * g.W + ww]) *
+               Elem<T>::to_f32(wo[(c * g.R + r) * g.S + k]);
+        }
+      }
+    y[i] = Elem<T>::from_f32(s);
+  }
+}
+
+// Input gradient, one input element per lane (conv_backward_input.wgsl:26-89),
+// visiting only output positions whose receptive field holds the element.
+template <typename T>
+__global__ __launch_bounds__(256) void direct_dgrad_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                           const typename Elem<T>::storage* __restrict__ w,
+                                                           typename Elem<T>::storage* __restrict__ dx,
+                                                           ConvGeom g, long total) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int iw = (int)(i % g.W);
+    long t = i / g.W;
+    int ih = (int)(t % g.H);
+    t /= g.H;
+    int c = (int)(t % g.C);
+    int n = (int)(t / g.C);
+    int th = ih + g.ph, tw = iw + g.pw;
+    float s = 0.f;
+    for (int o = 0; o < g.O; ++o)
+      for (int r = 0; r < g.R; ++r) {
+        int a = th - r;
+        if (a < 0 || a % g.sh) continue;
+        int p = a / g.sh;
+        if (p >= g.P) continue;
+        for (int k = 0; k < g.S; ++k) {
+          int b = tw - k;
+          if (b < 0 || b % g.sw) continue;
+          int q = b / g.sw;
+          if (q >= g.Q) continue;
+          s += Elem<T>::to_f32(dy[(((long)n * g.O + o) * g.P + p) * g.Q + q]) *
+               Elem<T>::to_f32(w[((o * g.C + c) * g.R + r) * g.S + k]);
+        }
+      }
+    dx[i] = Elem<T>::from_f32(s);
+  }
+}
+
+// Weight gradient: one workgroup per (weight element, position slice); the 256
+// lanes stride over output positions and a wavefront reduction (DPP shuffles)
+// plus an LDS step combine them into one fp32 partial per slice.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void direct_wgrad_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                           const typename Elem<T>::storage* __restrict__ x,
+                                                           float* __restrict__ part, ConvGeom g,
+                                                           int slice) {
+  const int widx = blockIdx.x;  // (o, c, r, s)
+  int k = widx % g.S;
+  int t = widx / g.S;
+  int r = t % g.R;
+  t /= g.R;
+  int c = t % g.C;
+  int o = t / g.C;
+  const long npos = (long)g.N * g.P * g.Q;
+  long b = (long)blockIdx.y * slice, e = min(npos, b + slice);
+  float s = 0.f;
+  for (long i = b + threadIdx.x; i < e; i += 256) {
+    int q = (int)(i % g.Q);
+    long tt = i / g.Q;
+    int p = (int)(tt % g.P);
+    int n = (int)(tt / g.P);
+    int h = p * g.sh + r - g.ph, w = q * g.sw + k - g.pw;
+    if (h < 0 || h >= g.H || w < 0 || w >= g.W) continue;
+    s += Elem<T>::to_f32(x[(((long)n * g.C + c) * g.H + h) * g.W + w]) *
+         Elem<T>::to_f32(dy[(((long)n * g.O + o) * g.P + p) * g.Q + q]);
+  }
+  s = wave_sum(s);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[(long)blockIdx.y * gridDim.x + widx] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Sum of partials [splits][n] -> out[n] (dtype T), fixed order.
+template <typename T>
+__global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restrict__ part, int splits, long n,
+                                                           typename Elem<T>::storage* __restrict__ out) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += part[(long)z * n + i];
+    out[i] = Elem<T>::from_f32(s);
+  }
+}
+
+// ============================================================== pad / im2col / col2im
+template <typename T>
+__global__ __launch_bounds__(256) void pad_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                  typename Elem<T>::storage* __restrict__ xp, int BC, int H,
+                                                  int W, int ph, int pw, long total) {
+  int HP = H + 2 * ph, WP = W + 2 * pw;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int wq = (int)(i % WP);
+    long t = i / WP;
+    int hq = (int)(t % HP);
+    long bc = t / HP;
+    int h = hq - ph, w = wq - pw;
+    typename Elem<T>::storage v = 0;
+    if (h >= 0 && h < H && w >= 0 && w < W) v = x[(bc * H + h) * W + w];
+    xp[i] = v;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void crop_kernel(const typename Elem<T>::storage* __restrict__ xp,
+                                                   typename Elem<T>::storage* __restrict__ x, int H, int W,
+                                                   int ph, int pw, long total) {
+  int HP = H + 2 * ph, WP = W + 2 * pw;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int w = (int)(i % W);
+    long t = i / W;
+    int h = (int)(t % H);
+    long bc = t / H;
+    x[i] = xp[(bc * HP + h + ph) * WP + w + pw];
+  }
+}
+
+// col[(b*HO+oh)*WO+ow][(c*KH+kh)*KW+kw] = x[b][c][oh*sh+kh][ow*sw+kw]  (input pre-padded)
+// Lanes walk the column index fastest, so col stores are coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void im2col_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                     typename Elem<T>::storage* __restrict__ col, int C, int H,
+                                                     int W, int KH, int KW, int SH, int SW, int HO, int WO,
+                                                     long total) {
+  const int cols = C * KH * KW;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int cc = (int)(i % cols);
+    long row = i / cols;
+    int kw = cc % KW;
+    int t = cc / KW;
+    int kh = t % KH;
+    int c = t / KH;
+    int ow = (int)(row % WO);
+    long t2 = row / WO;
+    int oh = (int)(t2 % HO);
+    long b = t2 / HO;
+    col[i] = x[((b * C + c) * H + oh * SH + kh) * W + ow * SW + kw];
+  }
+}
+
+// Gather form of col2im (no atomics): each input element sums every column
+// entry that im2col copied it into.  fp32 accumulation.
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_kernel(const typename Elem<T>::storage* __restrict__ col,
+                                                     typename Elem<T>::storage* __restrict__ x, int C, int H,
+                                                     int W, int KH, int KW, int SH, int SW, int HO, int WO,
+                                                     long total) {
+  const int cols = C * KH * KW;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int w = (int)(i % W);
+    long t = i / W;
+    int h = (int)(t % H);
+    t /= H;
+    int c = (int)(t % C);
+    long b = t / C;
+    float s = 0.f;
+    for (int kh = 0; kh < KH; ++kh) {
+      int a = h - kh;
+      if (a < 0 || a % SH) continue;
+      int oh = a / SH;
+      if (oh >= HO) continue;
+      for (int kw = 0; kw < KW; ++kw) {
+        int bb = w - kw;
+        if (bb < 0 || bb % SW) continue;
+        int ow = bb / SW;
+        if (ow >= WO) continue;
+        s += Elem<T>::to_f32(col[((b * HO + oh) * WO + ow) * cols + (c * KH + kh) * KW + kw]);
+      }
+    }
+    x[i] = Elem<T>::from_f32(s);
+  }
+}
+
+// ============================================================== weight re-layouts
+// src viewed as [A][B][RS]; dst[a][rs][b] (flip_rs: rs -> RS-1-rs) or dst[b][rs][a] (swap).
+template <typename T>
+__global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::storage* __restrict__ src,
+                                                       typename Elem<T>::storage* __restrict__ dst, int A, int B,
+                                                       int RS, int swap) {
+  long total = (long)A * B * RS;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int rs = (int)(i % RS);
+    long t = i / RS;
+    int b = (int)(t % B);
+    int a = (int)(t / B);
+    long d = swap ? ((long)b * RS + rs) * A + a : ((long)a * RS + rs) * B + b;
+    dst[d] = src[i];
+  }
+}
+
+// ============================================================== reductions
+// Per-channel sum of an NCHW tensor [N][C][HW] -> partial[split][C].
+template <typename T>
+__global__ __launch_bounds__(256) void channel_sum_kernel(const typename Elem<T>::storage* __restrict__ x, int N,
+                                                          int C, int HW, float* __restrict__ part, int nslice) {
+  const int c = blockIdx.x;
+  const long len = (long)N * HW;
+  const long per = (len + nslice - 1) / nslice;
+  const long b = (long)blockIdx.y * per, e = min(len, b + per);
+  float s = 0.f;
+  for (long i = b + threadIdx.x; i < e; i += 256) {
+    long n = i / HW, hw = i % HW;
+    s += Elem<T>::to_f32(x[(n * C + c) * HW + hw]);
+  }
+  s = wave_sum(s);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[(long)blockIdx.y * C + c] = red[0] + red[1] + red[2] + red[3];
+}
+
+// Column sums of a row-major [M][N] matrix -> partial[split][N]; lanes walk columns.
+template <typename T>
+__global__ __launch_bounds__(256) void column_sum_kernel(const typename Elem<T>::storage* __restrict__ x, int M,
+                                                         int N, float* __restrict__ part, int rows_per) {
+  int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= N) return;
+  int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
+  float s = 0.f;
+  for (int r = r0; r < r1; ++r) s += Elem<T>::to_f32(x[(long)r * N + col]);
+  part[(long)blockIdx.y * N + col] = s;
+}
+
+// ============================================================== pixel shuffle
+// out[b][c][h*r+i][w*r+j] = in[b][c*r*r+i*r+j][h][w]; forward walks the output
+// (coalesced stores), backward walks the input gradient.
+template <typename T>
+__global__ __launch_bounds__(256) void pixel_shuffle_kernel(const typename Elem<T>::storage* __restrict__ in,
+                                                            typename Elem<T>::storage* __restrict__ out, int C,
+                                                            int H, int W, int r, long total, int backward) {
+  const int HO = H * r, WO = W * r;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    if (!backward) {
+      int wo = (int)(i % WO);
+      long t = i / WO;
+      int ho = (int)(t % HO);
+      long bc = t / HO;  // b*C + c
+      int h = ho / r, ii = ho - h * r, w = wo / r, jj = wo - w * r;
+      out[i] = in[((bc * r + ii) * r + jj) * H * W + (long)h * W + w];
+    } else {
+      int w = (int)(i % W);
+      long t = i / W;
+      int h = (int)(t % H);
+      t /= H;
+      int rr = (int)(t % (r * r));
+      long bc = t / (r * r);
+      int ii = rr / r, jj = rr - ii * r;
+      out[i] = in[(bc * HO + (long)h * r + ii) * WO + (long)w * r + jj];
+    }
+  }
+}
+
+// ============================================================== typed launchers
+template <typename T>
+int run_direct_fwd(const void* x, const void* w, void* y, const ConvGeom& g, hipStream_t st) {
+  long total = (long)g.N * g.O * g.P * g.Q;
+  using S = typename Elem<T>::storage;
+  direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (S*)y, g, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g, hipStream_t st) {
+  long total = (long)g.N * g.C * g.H * g.W;
+  using S = typename Elem<T>::storage;
+  direct_dgrad_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)dy, (const S*)w, (S*)dx, g, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
+  long npos = (long)g.N * g.P * g.Q;
+  long nw = (long)g.O * g.C * g.R * g.S;
+  int sl = (int)std::min<long>(std::max<long>(1, (2048 + nw - 1) / nw), std::max<long>(1, npos / 1024));
+  sl = std::min(sl, 1024);
+  int len = (int)((npos + sl - 1) / sl);
+  *slices = (int)((npos + len - 1) / len);
+  *slice_len = len;
+  return (size_t)(*slices) * nw * sizeof(float);
+}
+
+template <typename T>
+int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g, float* ws, int slices,
+                     int slice_len, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long nw = (long)g.O * g.C * g.R * g.S;
+  dim3 grid((unsigned)nw, (unsigned)slices);
+  direct_wgrad_kernel<T><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+  VH_LAUNCH_CHECK();
+  sum_partials_kernel<T><<<grid_for(nw), 256, 0, st>>>(ws, slices, nw, (S*)dw);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_pad(const void* x, void* xp, int B, int C, int H, int W, int ph, int pw, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * C * (H + 2 * ph) * (W + 2 * pw);
+  pad_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (S*)xp, B * C, H, W, ph, pw, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_crop(const void* xp, void* x, int B, int C, int H, int W, int ph, int pw, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * C * H * W;
+  crop_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)xp, (S*)x, H, W, ph, pw, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_im2col(const void* x, void* col, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int HO,
+               int WO, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * HO * WO * C * KH * KW;
+  im2col_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (S*)col, C, H, W, KH, KW, SH, SW, HO, WO, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int HO,
+               int WO, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * C * H * W;
+  col2im_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)col, (S*)x, C, H, W, KH, KW, SH, SW, HO, WO, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  relayout_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>((const S*)src, (S*)dst, A, B, RS, swap);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+size_t channel_sum_ws(int N, int C, int HW, int* nslice) {
+  long len = (long)N * HW;
+  int s = (int)std::max<long>(1, std::min<long>(std::max<long>(1, 1024 / std::max(C, 1)), len / 4096));
+  *nslice = s;
+  return (size_t)s * C * sizeof(float);
+}
+
+template <typename T>
+int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  channel_sum_kernel<T><<<dim3(C, nslice), 256, 0, st>>>((const S*)x, N, C, HW, ws, nslice);
+  VH_LAUNCH_CHECK();
+  sum_partials_kernel<T><<<grid_for(C), 256, 0, st>>>(ws, nslice, C, (S*)out);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+size_t column_sum_ws(int M, int N, int* nslice, int* rows_per) {
+  int cb = (N + 255) / 256;
+  int s = std::max(1, std::min(M / 64, std::max(1, 1024 / cb)));
+  *rows_per = (M + s - 1) / s;
+  *nslice = (M + *rows_per - 1) / *rows_per;
+  return (size_t)(*nslice) * N * sizeof(float);
+}
+
+template <typename T>
+int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  column_sum_kernel<T><<<dim3((N + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
+  VH_LAUNCH_CHECK();
+  sum_partials_kernel<T><<<grid_for(N), 256, 0, st>>>(ws, nslice, N, (S*)out);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward,
+                      hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * C * H * W * r * r;
+  pixel_shuffle_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)in, (S*)out, C, H, W, r, total, backward);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+#define VH_INST(T)                                                                                      \
+  template int run_direct_fwd<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);        \
+  template int run_direct_dgrad<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);      \
+  template size_t direct_wgrad_ws<T>(const ConvGeom&, int*, int*);                                      \
+  template int run_direct_wgrad<T>(const void*, const void*, void*, const ConvGeom&, float*, int, int,  \
+                                   hipStream_t);                                                        \
+  template int run_pad<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);               \
+  template int run_crop<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);              \
+  template int run_im2col<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \
+                             hipStream_t);                                                              \
+  template int run_col2im<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \
+                             hipStream_t);                                                              \
+  template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t);                    \
+  template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
+  template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
+  template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);
+VH_INST(float)
+VH_INST(bf16)
+#undef VH_INST
+
+}  // namespace vh

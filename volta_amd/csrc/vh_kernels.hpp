@@ -1,0 +1,48 @@
+// vh_kernels.hpp -- internal launch helpers of libvolta_hip (host side).
+#pragma once
+#include "vh_igemm.hpp"
+
+namespace vh {
+
+// ---- implicit GEMM (vh_gemm.hip) ----
+// Describes one GEMM-shaped pass; kinds select the operand gathers and the store.
+struct IgemmPlan {
+  int dtype;                // VH_F32 / VH_BF16
+  int akind, bkind, okind;  // OpndKind x2, OutKind
+  IgemmArgs args;
+  int splits;               // requested split-K factor (1 = none)
+};
+// Fills args.k_chunk / splits and returns the fp32 workspace bytes needed.
+size_t igemm_prepare(IgemmPlan& plan);
+int run_igemm(IgemmPlan& plan, float* ws, hipStream_t st);
+// Heuristic split-K factor for a problem with the given tile grid and K.
+int pick_splits(int M, int N, int K, int dtype);
+ConvGeom make_geom(int N, int C, int H, int W, int O, int R, int S, int P, int Q, int sh, int sw, int ph,
+                   int pw);
+
+// ---- other kernels (vh_kernels.hip) ----
+template <typename T> int run_direct_fwd(const void* x, const void* w, void* y, const ConvGeom& g, hipStream_t st);
+template <typename T> int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g, hipStream_t st);
+template <typename T> size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len);
+template <typename T>
+int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g, float* ws, int slices,
+                     int slice_len, hipStream_t st);
+template <typename T> int run_pad(const void* x, void* xp, int B, int C, int H, int W, int ph, int pw, hipStream_t st);
+template <typename T> int run_crop(const void* xp, void* x, int B, int C, int H, int W, int ph, int pw, hipStream_t st);
+template <typename T>
+int run_im2col(const void* x, void* col, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int HO,
+               int WO, hipStream_t st);
+template <typename T>
+int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int HO,
+               int WO, hipStream_t st);
+template <typename T> int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st);
+size_t channel_sum_ws(int N, int C, int HW, int* nslice);
+template <typename T>
+int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st);
+size_t column_sum_ws(int M, int N, int* nslice, int* rows_per);
+template <typename T>
+int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st);
+template <typename T>
+int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
+
+}  // namespace vh

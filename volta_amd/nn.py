@@ -1,0 +1,217 @@
+"""Layer-level mirror of Volta's Conv2d / ConvTranspose2d / Linear / PixelShuffle.
+
+The composition (algorithm choice, bias add, which gradients are produced)
+runs in C++ inside libvolta_hip.so (``vh_conv2d_forward`` and friends); these
+classes hold parameters as torch device tensors in the reference's layouts
+and call it.  Gradients are explicit (``backward`` returns them) instead of
+going through an autograd graph: the reference's GradFn objects
+(conv.rs:139-1013, conv_transpose.rs:150-353, matmul.rs:374-680) map onto the
+``backward`` methods here.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from ._lib import ALGO_AUTO, ALGO_DIRECT, ALGO_IGEMM, ALGO_IM2COL, check, lib
+from .ops import _same_dtype, ptr, stream_ptr
+
+
+class ConvAlgo(enum.IntEnum):
+    """conv.rs:11-24 -- same variants and order."""
+
+    Direct = ALGO_DIRECT
+    Im2col = ALGO_IM2COL
+    IGEMM = ALGO_IGEMM
+    Auto = ALGO_AUTO
+
+    @staticmethod
+    def auto_select(batch, channels, height, width, kernel_size, has_gpu) -> "ConvAlgo":
+        """conv.rs:29-69, the reference's rule verbatim (computed in C++)."""
+        v = lib().vh_conv_algo_auto_select(batch, channels, height, width, kernel_size, int(bool(has_gpu)))
+        if v < 0:
+            raise ValueError("input smaller than kernel (the reference underflows here)")
+        return ConvAlgo(v)
+
+
+def conv_out(h: int, k: int, s: int, p: int) -> int:
+    return (h + 2 * p - k) // s + 1
+
+
+class Conv2d:
+    """conv.rs:129-135, 1017-1115, 1787-1927.  weight [O, C, K, K] (OIHW), bias [O]."""
+
+    def __init__(self, in_ch: int, out_ch: int, kernel: int, stride: int = 1, padding: int = 0,
+                 use_bias: bool = True, device="cuda", dtype=torch.float32, generator=None):
+        fan_in = in_ch * kernel * kernel
+        # Kaiming (He) normal init like RawTensor::he_initialization (tensor.rs:276-312)
+        w = torch.randn((out_ch, in_ch, kernel, kernel), generator=generator) * math.sqrt(2.0 / fan_in)
+        self.weight = w.to(device=device, dtype=dtype).contiguous()
+        self.bias = torch.zeros(out_ch, device=device, dtype=dtype) if use_bias else None
+        self.stride = (stride, stride)
+        self.padding = (padding, padding)
+        self.algo = ConvAlgo.Auto
+        self.last_algo: Optional[ConvAlgo] = None
+
+    def set_algo(self, algo: ConvAlgo) -> None:
+        self.algo = ConvAlgo(algo)
+
+    def get_algo(self) -> ConvAlgo:
+        return self.algo
+
+    def _dims(self, x: torch.Tensor):
+        B, C, H, W = x.shape
+        O, C2, KH, KW = self.weight.shape
+        if C != C2:
+            raise ValueError("Channel mismatch")
+        return (B, C, O, H, W, KH, KW, self.stride[0], self.stride[1], self.padding[0], self.padding[1])
+
+    def output_shape(self, x: torch.Tensor):
+        B, C, O, H, W, KH, KW, SH, SW, PH, PW = self._dims(x)
+        return (B, O, conv_out(H, KH, SH, PH), conv_out(W, KW, SW, PW))
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        dt = _same_dtype(x, self.weight, self.bias)
+        y = out if out is not None else torch.empty(self.output_shape(x), dtype=x.dtype, device=x.device)
+        used = ctypes.c_int(-1)
+        check(lib().vh_conv2d_forward(dt, int(self.algo), ptr(x), ptr(self.weight), ptr(self.bias), ptr(y),
+                                      *self._dims(x), ctypes.byref(used), stream_ptr(x.device)))
+        self.last_algo = ConvAlgo(used.value)
+        return y
+
+    __call__ = forward
+
+    def backward(self, out_grad: torch.Tensor, x: torch.Tensor, input_grad: bool = True,
+                 weight_grad: bool = True, algo: Optional[ConvAlgo] = None,
+                 outs: Optional[Tuple] = None):
+        """Returns (grad_input, grad_weight, grad_bias); None where not requested."""
+        algo = ConvAlgo(algo if algo is not None else (self.last_algo if self.last_algo is not None else self.algo))
+        if algo == ConvAlgo.Auto:
+            B, C, O, H, W, KH, KW, SH, SW, PH, PW = self._dims(x)
+            algo = ConvAlgo(lib().vh_conv_algo_select_mi355x(B, C, O, H, W, KH, KW, SH, SW, PH, PW))
+        dt = _same_dtype(out_grad, x, self.weight)
+        if outs is not None:
+            dx, dw, db = outs
+        else:
+            dx = torch.empty_like(x) if input_grad else None
+            dw = torch.empty_like(self.weight) if weight_grad else None
+            db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        check(lib().vh_conv2d_backward(dt, int(algo), ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw),
+                                       ptr(db), *self._dims(x), stream_ptr(x.device)))
+        return dx, dw, db
+
+
+class ConvTranspose2d:
+    """conv_transpose.rs:21-58, 356-435.  weight [in, out, K, K] (IOHW), bias [out]."""
+
+    def __init__(self, in_ch: int, out_ch: int, kernel: int, stride: int = 1, padding: int = 0,
+                 use_bias: bool = True, device="cuda", dtype=torch.float32, generator=None):
+        fan_in = out_ch * kernel * kernel  # he_initialization uses prod(shape[1..]) (tensor.rs:283-298)
+        w = torch.randn((in_ch, out_ch, kernel, kernel), generator=generator) * math.sqrt(2.0 / fan_in)
+        self.weight = w.to(device=device, dtype=dtype).contiguous()
+        self.bias = torch.zeros(out_ch, device=device, dtype=dtype) if use_bias else None
+        self.stride = (stride, stride)
+        self.padding = (padding, padding)
+
+    def _dims(self, x):
+        B, CI, H, W = x.shape
+        CI2, CO, KH, KW = self.weight.shape
+        if CI != CI2:
+            raise ValueError(f"Channel mismatch: input has {CI} channels but weight expects {CI2}")
+        return (B, CI, CO, H, W, KH, KW, self.stride[0], self.stride[1], self.padding[0], self.padding[1])
+
+    def output_shape(self, x):
+        B, CI, CO, H, W, KH, KW, SH, SW, PH, PW = self._dims(x)
+        return (B, CO, (H - 1) * SH + KH - 2 * PH, (W - 1) * SW + KW - 2 * PW)
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        dt = _same_dtype(x, self.weight, self.bias)
+        y = out if out is not None else torch.empty(self.output_shape(x), dtype=x.dtype, device=x.device)
+        check(lib().vh_conv_transpose2d_forward(dt, ptr(x), ptr(self.weight), ptr(self.bias), ptr(y),
+                                                *self._dims(x), stream_ptr(x.device)))
+        return y
+
+    __call__ = forward
+
+    def backward(self, out_grad, x, input_grad=True, weight_grad=True, outs=None):
+        dt = _same_dtype(out_grad, x, self.weight)
+        if outs is not None:
+            dx, dw, db = outs
+        else:
+            dx = torch.empty_like(x) if input_grad else None
+            dw = torch.empty_like(self.weight) if weight_grad else None
+            db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        check(lib().vh_conv_transpose2d_backward(dt, ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw),
+                                                 ptr(db), *self._dims(x), stream_ptr(x.device)))
+        return dx, dw, db
+
+
+class Linear:
+    """linear.rs:11-117.  weight [in, out] (xavier-uniform), bias [out]."""
+
+    def __init__(self, in_features: int, out_features: int, use_bias: bool = True, device="cuda",
+                 dtype=torch.float32, generator=None):
+        bound = math.sqrt(6.0 / (in_features + out_features))  # xavier_uniform, tensor.rs:254-265
+        w = (torch.rand((in_features, out_features), generator=generator) * 2 - 1) * bound
+        self.weight = w.to(device=device, dtype=dtype).contiguous()
+        self.bias = torch.zeros(out_features, device=device, dtype=dtype) if use_bias else None
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        dt = _same_dtype(x, self.weight, self.bias)
+        m, i = x.shape
+        o = self.weight.shape[1]
+        y = out if out is not None else torch.empty((m, o), dtype=x.dtype, device=x.device)
+        check(lib().vh_linear_forward(dt, ptr(x), ptr(self.weight), ptr(self.bias), ptr(y), m, i, o,
+                                      stream_ptr(x.device)))
+        return y
+
+    __call__ = forward
+
+    def backward(self, out_grad, x, input_grad=True, weight_grad=True, outs=None):
+        dt = _same_dtype(out_grad, x, self.weight)
+        m, i = x.shape
+        o = self.weight.shape[1]
+        if outs is not None:
+            dx, dw, db = outs
+        else:
+            dx = torch.empty_like(x) if input_grad else None
+            dw = torch.empty_like(self.weight) if weight_grad else None
+            db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        check(lib().vh_linear_backward(dt, ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw), ptr(db),
+                                       m, i, o, stream_ptr(x.device)))
+        return dx, dw, db
+
+
+class PixelShuffle:
+    """pixelshuffle.rs:27-85: (B, C*r^2, H, W) -> (B, C, H*r, W*r)."""
+
+    def __init__(self, upscale_factor: int):
+        if upscale_factor <= 0:
+            raise ValueError(f"PixelShuffle: upscale_factor must be positive, got {upscale_factor}")
+        self.upscale_factor = upscale_factor
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, CR, H, W = x.shape
+        r = self.upscale_factor
+        if CR % (r * r):
+            raise ValueError(f"PixelShuffle: input channels ({CR}) must be divisible by upscale_factor^2 ({r*r})")
+        C = CR // (r * r)
+        y = out if out is not None else torch.empty((B, C, H * r, W * r), dtype=x.dtype, device=x.device)
+        check(lib().vh_pixel_shuffle(_same_dtype(x), ptr(x), ptr(y), B, C, H, W, r, stream_ptr(x.device)))
+        return y
+
+    __call__ = forward
+
+    def backward(self, out_grad: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        B, C, HR, WR = out_grad.shape
+        r = self.upscale_factor
+        H, W = HR // r, WR // r
+        dx = out if out is not None else torch.empty((B, C * r * r, H, W), dtype=out_grad.dtype,
+                                                     device=out_grad.device)
+        check(lib().vh_pixel_shuffle_backward(_same_dtype(out_grad), ptr(out_grad), ptr(dx), B, C, H, W, r,
+                                              stream_ptr(out_grad.device)))
+        return dx

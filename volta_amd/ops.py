@@ -1,0 +1,190 @@
+"""Python mirror of Volta's device-dispatch boundary (src/ops/gpu_ops.rs).
+
+Each ``gpu_*`` function keeps the reference's name and argument order
+(``gpu_ops.rs:151-861``) and calls the matching C-ABI entry of
+libvolta_hip.so on torch device tensors.  Like the reference, the ``gpu_*``
+functions return ``None`` instead of raising when the device path cannot run
+(no GPU / CPU tensor), so a caller can keep a CPU fallback; shape errors
+raise (the reference panics there).  Outputs are allocated by the callee, as
+``GpuBuffer::zeros`` does in the reference.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F32, VoltaHipError, check, lib
+
+_DTYPES = {torch.float32: F32, torch.bfloat16: BF16}
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; libvolta_hip takes float32 or bfloat16") from None
+
+
+def stream_ptr(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("libvolta_hip takes device tensors")
+    if not t.is_contiguous():
+        raise ValueError("libvolta_hip takes contiguous tensors")
+    return t.data_ptr()
+
+
+def _device_ok(*ts: torch.Tensor) -> bool:
+    return all(t is not None and t.is_cuda for t in ts)
+
+
+def _same_dtype(*ts: torch.Tensor) -> int:
+    code = dtype_code(ts[0])
+    for t in ts[1:]:
+        if t is not None and t.dtype != ts[0].dtype:
+            raise TypeError("all tensor arguments of one call must share a dtype")
+    return code
+
+
+def _call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))
+
+
+def _optional(fn):
+    """Reference semantics: Option::None when the device path is unavailable."""
+
+    def wrapper(*args, **kwargs):
+        tensors = [a for a in args if isinstance(a, torch.Tensor)]
+        if not _device_ok(*tensors):
+            return None
+        try:
+            return fn(*args, **kwargs)
+        except VoltaHipError as e:
+            if e.status in (_lib.VH_ERR_NO_DEVICE, _lib.VH_ERR_OOM):
+                return None
+            raise
+
+    wrapper.__name__ = fn.__name__
+    wrapper.__doc__ = fn.__doc__
+    return wrapper
+
+
+# ---------------------------------------------------------------- matmul
+@_optional
+def gpu_matmul(a: torch.Tensor, b: torch.Tensor, m: int, k: int, n: int):
+    """gpu_ops.rs:151 -- c[m,n] = a[m,k] . b[k,n]."""
+    dt = _same_dtype(a, b)
+    c = torch.empty((m, n), dtype=a.dtype, device=a.device)
+    _call("vh_matmul", dt, ptr(a), ptr(b), ptr(c), m, k, n, stream_ptr(a.device))
+    return c
+
+
+@_optional
+def gpu_matmul_backward_a(grad: torch.Tensor, b: torch.Tensor, m: int, k: int, n: int):
+    """gpu_ops.rs:408 -- grad_a[m,k] = grad[m,n] . b[k,n]^T."""
+    dt = _same_dtype(grad, b)
+    out = torch.empty((m, k), dtype=grad.dtype, device=grad.device)
+    _call("vh_matmul_backward_a", dt, ptr(grad), ptr(b), ptr(out), m, k, n, stream_ptr(grad.device))
+    return out
+
+
+@_optional
+def gpu_matmul_backward_b(a: torch.Tensor, grad: torch.Tensor, m: int, k: int, n: int):
+    """gpu_ops.rs:430 -- grad_b[k,n] = a[m,k]^T . grad[m,n]."""
+    dt = _same_dtype(a, grad)
+    out = torch.empty((k, n), dtype=a.dtype, device=a.device)
+    _call("vh_matmul_backward_b", dt, ptr(a), ptr(grad), ptr(out), m, k, n, stream_ptr(a.device))
+    return out
+
+
+# ---------------------------------------------------------------- im2col / col2im
+@_optional
+def gpu_im2col(input, batch_size, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out, w_out):
+    """gpu_ops.rs:515 -- (B,C,H,W) (already padded) -> (B*h_out*w_out, C*kh*kw)."""
+    dt = dtype_code(input)
+    col = torch.empty((batch_size * h_out * w_out, channels * kernel_h * kernel_w), dtype=input.dtype,
+                      device=input.device)
+    _call("vh_im2col", dt, ptr(input), ptr(col), batch_size, channels, height, width, kernel_h, kernel_w,
+          stride_h, stride_w, h_out, w_out, stream_ptr(input.device))
+    return col
+
+
+@_optional
+def gpu_col2im(col, batch_size, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out, w_out):
+    """gpu_ops.rs:546 -- adjoint of gpu_im2col."""
+    dt = dtype_code(col)
+    out = torch.empty((batch_size, channels, height, width), dtype=col.dtype, device=col.device)
+    _call("vh_col2im", dt, ptr(col), ptr(out), batch_size, channels, height, width, kernel_h, kernel_w,
+          stride_h, stride_w, h_out, w_out, stream_ptr(col.device))
+    return out
+
+
+# ---------------------------------------------------------------- conv kernels
+def _conv_call(name, t0, t1, out_shape, dims):
+    dt = _same_dtype(t0, t1)
+    out = torch.empty(out_shape, dtype=t0.dtype, device=t0.device)
+    _call(name, dt, ptr(t0), ptr(t1), ptr(out), *dims, stream_ptr(t0.device))
+    return out
+
+
+@_optional
+def gpu_direct_conv(input, weight, batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w,
+                    stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:574 (stride before pad)."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_direct_conv", input, weight, (batch_size, out_channels, h_out, w_out), dims)
+
+
+@_optional
+def gpu_igemm(input, weight, batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w,
+              stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:622."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_igemm", input, weight, (batch_size, out_channels, h_out, w_out), dims)
+
+
+@_optional
+def gpu_conv_backward_input(out_grad, weight, batch_size, in_channels, out_channels, height, width, kernel_h,
+                            kernel_w, stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:670."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_conv_backward_input", out_grad, weight, (batch_size, in_channels, height, width), dims)
+
+
+@_optional
+def gpu_conv_backward_weight(out_grad, input, batch_size, in_channels, out_channels, height, width, kernel_h,
+                             kernel_w, stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:718 -- note (out_grad, input)."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_conv_backward_weight", out_grad, input, (out_channels, in_channels, kernel_h, kernel_w),
+                      dims)
+
+
+@_optional
+def gpu_igemm_backward_input(out_grad, weight, batch_size, in_channels, out_channels, height, width, kernel_h,
+                             kernel_w, stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:766."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_igemm_backward_input", out_grad, weight, (batch_size, in_channels, height, width), dims)
+
+
+@_optional
+def gpu_igemm_backward_weight(out_grad, input, batch_size, in_channels, out_channels, height, width, kernel_h,
+                              kernel_w, stride_h, stride_w, pad_h, pad_w, h_out, w_out):
+    """gpu_ops.rs:814."""
+    dims = (batch_size, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+            pad_h, pad_w, h_out, w_out)
+    return _conv_call("vh_igemm_backward_weight", out_grad, input,
+                      (out_channels, in_channels, kernel_h, kernel_w), dims)
