@@ -36,6 +36,20 @@ def host(t):
     return t.float().cpu().numpy()
 
 
+def ref_and_scale(fn, *args, **kw):
+    """oracle result and its per-element scale S = fn(|args|) (fn is bilinear)."""
+    ab = [np.abs(a) if isinstance(a, np.ndarray) else a for a in args]
+    return fn(*args, **kw), fn(*ab, **kw)
+
+
+def check(got, fn, args, dt, what, kw=None, extra_ref=None, extra_scale=None):
+    ref, scale = ref_and_scale(fn, *args, **(kw or {}))
+    if extra_ref is not None:
+        ref = ref + extra_ref
+        scale = scale + extra_scale
+    return assert_parity(host(got), ref, scale, dt, what)
+
+
 # ------------------------------------------------------------------ known answers
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_matmul_known_answers(dt):
@@ -94,9 +108,9 @@ def test_matmul_family(mkn, dt):
     a, at = prep(g.standard_normal((m, k)), dt)
     b, bt = prep(g.standard_normal((k, n)), dt)
     gr, grt = prep(g.standard_normal((m, n)), dt)
-    assert_parity(host(ops.gpu_matmul(at, bt, m, k, n)), oracle.matmul(a, b), dt, "matmul")
-    assert_parity(host(ops.gpu_matmul_backward_a(grt, bt, m, k, n)), oracle.matmul_backward_a(gr, b), dt, "dA")
-    assert_parity(host(ops.gpu_matmul_backward_b(at, grt, m, k, n)), oracle.matmul_backward_b(a, gr), dt, "dB")
+    check(ops.gpu_matmul(at, bt, m, k, n), oracle.matmul, (a, b), dt, "matmul")
+    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), dt, "dA")
+    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), dt, "dB")
 
 
 @pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (1, 7, 5)])
@@ -110,12 +124,11 @@ def test_linear_fwd_bwd(shape, dt):
     dy, dyt = prep(g.standard_normal((m, o)), dt)
     lin = vnn.Linear(i, o, device=DEV, dtype=DTYPES[dt])
     lin.weight, lin.bias = wt, bt
-    assert_parity(host(lin.forward(xt)), oracle.linear_forward(x, w, b), dt, "y")
+    check(lin.forward(xt), oracle.linear_forward, (x, w, b), dt, "y")
     dx, dw, db = lin.backward(dyt, xt)
-    rdx, rdw, rdb = oracle.linear_backward(dy, x, w)
-    assert_parity(host(dx), rdx, dt, "dx")
-    assert_parity(host(dw), rdw, dt, "dw")
-    assert_parity(host(db), rdb, dt, "db")
+    check(dx, lambda *a: oracle.linear_backward(*a)[0], (dy, x, w), dt, "dx")
+    check(dw, lambda *a: oracle.linear_backward(*a)[1], (dy, x, w), dt, "dw")
+    check(db, lambda *a: oracle.linear_backward(*a)[2], (dy, x, w), dt, "db")
 
 
 # ------------------------------------------------------------------ Conv2d
@@ -153,13 +166,20 @@ def test_conv2d_fwd_bwd(case, algo, dt):
     conv.set_algo(algo)
     y = conv.forward(xt)
     assert conv.last_algo == algo
-    ref_y = oracle.direct_conv(x, w, (S, S), (P, P)) + b[None, :, None, None]
-    assert_parity(host(y), ref_y, dt, "y")
-    dy, dyt = prep(g.standard_normal(ref_y.shape), dt)
+    bb = b[None, :, None, None]
+    y_shape = (B, O, oracle.conv_out(H, K, S, P), oracle.conv_out(W, K, S, P))
+    check(y, oracle.direct_conv, (x, w), dt, "y", dict(stride=(S, S), pad=(P, P)),
+          extra_ref=bb, extra_scale=np.abs(bb))
+    dy, dyt = prep(g.standard_normal(y_shape), dt)
     dx, dw, db = conv.backward(dyt, xt)
-    assert_parity(host(dx), oracle.direct_conv_backward_input(dy, w, x.shape, (S, S), (P, P)), dt, "dx")
-    assert_parity(host(dw), oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P)), dt, "dw")
-    assert_parity(host(db), oracle.conv_bias_grad(dy), dt, "db")
+    check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", dict(stride=(S, S), pad=(P, P)))
+    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", dict(stride=(S, S), pad=(P, P)))
+    check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+    if algo == vnn.ConvAlgo.Direct and dt == "f32":
+        # the direct kernels keep Volta's CPU summation order and unfused
+        # multiply/add (conv.rs:1370-1407, 458-505): bit-identical results
+        assert np.array_equal(host(y), oracle.direct_conv(x, w, (S, S), (P, P)) + bb)
+        assert np.array_equal(host(dx), oracle.direct_conv_backward_input(dy, w, x.shape, (S, S), (P, P)))
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
@@ -172,15 +192,17 @@ def test_gpu_ops_boundary_functions(dt):
     w, wt = prep(g.standard_normal((O, C, K, K)) * 0.2, dt)
     dy, dyt = prep(g.standard_normal((B, O, HO, WO)), dt)
     dims = (B, C, O, H, W, K, K, S, S, P, P, HO, WO)
-    ry = oracle.direct_conv(x, w, (S, S), (P, P))
-    rdx = oracle.direct_conv_backward_input(dy, w, x.shape, (S, S), (P, P))
-    rdw = oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P))
-    assert_parity(host(ops.gpu_direct_conv(xt, wt, *dims)), ry, dt, "direct")
-    assert_parity(host(ops.gpu_igemm(xt, wt, *dims)), ry, dt, "igemm")
-    assert_parity(host(ops.gpu_conv_backward_input(dyt, wt, *dims)), rdx, dt, "direct dx")
-    assert_parity(host(ops.gpu_igemm_backward_input(dyt, wt, *dims)), rdx, dt, "igemm dx")
-    assert_parity(host(ops.gpu_conv_backward_weight(dyt, xt, *dims)), rdw, dt, "direct dw")
-    assert_parity(host(ops.gpu_igemm_backward_weight(dyt, xt, *dims)), rdw, dt, "igemm dw")
+    kw = dict(stride=(S, S), pad=(P, P))
+    check(ops.gpu_direct_conv(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "direct", kw)
+    check(ops.gpu_igemm(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "igemm", kw)
+    check(ops.gpu_conv_backward_input(dyt, wt, *dims), oracle.direct_conv_backward_input, (dy, w, x.shape), dt,
+          "direct dx", kw)
+    check(ops.gpu_igemm_backward_input(dyt, wt, *dims), oracle.direct_conv_backward_input, (dy, w, x.shape), dt,
+          "igemm dx", kw)
+    check(ops.gpu_conv_backward_weight(dyt, xt, *dims), oracle.direct_conv_backward_weight, (dy, x, w.shape), dt,
+          "direct dw", kw)
+    check(ops.gpu_igemm_backward_weight(dyt, xt, *dims), oracle.direct_conv_backward_weight, (dy, x, w.shape), dt,
+          "igemm dw", kw)
     # im2col / col2im on the padded input, exact copies (sums for col2im)
     xp = oracle.pad(x, P, P)
     xpt = torch.from_numpy(xp).to(DEV, DTYPES[dt])
@@ -189,7 +211,7 @@ def test_gpu_ops_boundary_functions(dt):
     assert np.array_equal(host(col), oracle.im2col(xp, (K, K), (S, S)))
     gcol, gcolt = prep(g.standard_normal(col.shape), dt)
     back = ops.gpu_col2im(gcolt, B, C, HP, WP, K, K, S, S, HO, WO)
-    assert_parity(host(back), oracle.col2im(gcol, xp.shape, (K, K), (S, S)), dt, "col2im")
+    check(back, oracle.col2im, (gcol, xp.shape, (K, K), (S, S)), dt, "col2im")
 
 
 def test_bad_shape_is_an_error_not_a_crash():
@@ -224,14 +246,12 @@ def test_conv_transpose2d_fwd_bwd(case, dt):
     ct = vnn.ConvTranspose2d(CI, CO, K, S, P, device=DEV, dtype=DTYPES[dt])
     ct.weight, ct.bias = wt, bt
     y = ct.forward(xt)
-    ref_y = oracle.conv_transpose_forward(x, w, b, (S, S), (P, P))
-    assert_parity(host(y), ref_y, dt, "y")
-    dy, dyt = prep(g.standard_normal(ref_y.shape), dt)
+    kw = dict(stride=(S, S), pad=(P, P))
+    ref_y = check(y, oracle.conv_transpose_forward, (x, w, b), dt, "y", kw)
+    dy, dyt = prep(g.standard_normal(tuple(y.shape)), dt)
     dx, dw, db = ct.backward(dyt, xt)
-    rdx, rdw, rdb = oracle.conv_transpose_backward(dy, x, w, (S, S), (P, P))
-    assert_parity(host(dx), rdx, dt, "dx")
-    assert_parity(host(dw), rdw, dt, "dw")
-    assert_parity(host(db), rdb, dt, "db")
+    for i, (name, got) in enumerate((("dx", dx), ("dw", dw), ("db", db))):
+        check(got, lambda *a, i=i, **k: oracle.conv_transpose_backward(*a, **k)[i], (dy, x, w), dt, name, kw)
 
 
 # ------------------------------------------------------------------ PixelShuffle

@@ -55,8 +55,8 @@ SIGNATURES = {
     "vh_matmul": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_matmul_backward_a": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_matmul_backward_b": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
-    "vh_im2col": [_INT, _P, _P] + [_I64] * 11 + [_P],
-    "vh_col2im": [_INT, _P, _P] + [_I64] * 11 + [_P],
+    "vh_im2col": [_INT, _P, _P] + [_I64] * 10 + [_P],
+    "vh_col2im": [_INT, _P, _P] + [_I64] * 10 + [_P],
     "vh_direct_conv": [_INT, _P, _P, _P] + _CONV13 + [_P],
     "vh_igemm": [_INT, _P, _P, _P] + _CONV13 + [_P],
     "vh_conv_backward_input": [_INT, _P, _P, _P] + _CONV13 + [_P],

@@ -308,8 +308,10 @@ static int im2col_fwd(int dt, const void* x, const void* w, const void* bias, vo
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
-// Im2col backward: dcol = dY_2d . W (MatMulGradFn, matmul.rs:450-460) ->
-// col2im (conv.rs:1242-1298) -> crop; dW = dY_2d^T . col (matmul.rs:563-574).
+// Im2col backward: dcol = dY_2d . W (MatMulGradFn, matmul.rs:450-460) kept in
+// fp32 in the GEMM's own [C*kh*kw][positions] layout, then col2im
+// (conv.rs:1242-1298) and the pad crop in one gather kernel; dW = dY_2d^T . col
+// (matmul.rs:563-574) over a re-materialised col.
 static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void* dx, void* dw,
                       const ConvDims& d, hipStream_t st) {
   const long HP = d.H + 2 * d.PH, WP = d.W + 2 * d.PW, CKK = d.C * d.KH * d.KW;
@@ -321,21 +323,20 @@ static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void
   ConvGeom g1 = make_geom((int)d.B, (int)d.O, (int)d.HO, (int)d.WO, 1, 1, 1, (int)d.HO, (int)d.WO, 1, 1, 0, 0);
   ConvGeom gw = geom_of(d);
   IgemmPlan pd{}, pw{};
-  size_t ws_d = 0, ws_w = 0;
+  size_t ws_w = 0;
   if (dx) {
     pd.dtype = dt;
     pd.akind = KD_DENSE_MN;
     pd.bkind = KD_CONV_FWD_X;
-    pd.okind = OK_DENSE_T;
+    pd.okind = OK_DENSE_T;  // launched with splits = 1 and an fp32 partial store, see below
     pd.args.M = (int)CKK;
     pd.args.N = (int)M;
     pd.args.K = (int)d.O;
     pd.args.g = g1;
     pd.args.a = Operand{w, (int)CKK, (int)CKK, 0};
     pd.args.b = Operand{dy, 0, (int)M, 0};
-    pd.args.ldd = (int)CKK;
     pd.splits = 1;
-    ws_d = igemm_prepare(pd);
+    igemm_prepare(pd);
   }
   if (dw) {
     pw.dtype = dt;
@@ -352,22 +353,20 @@ static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void
     ws_w = igemm_prepare(pw);
   }
   Carve cv;
-  size_t o_col = cv.take((size_t)M * CKK * es);
-  size_t o_xp = padded ? cv.take((size_t)d.B * d.C * HP * WP * es) : 0;
-  size_t o_g = cv.take(std::max(ws_d, ws_w));
+  size_t o_dcol = dx ? cv.take((size_t)M * CKK * sizeof(float)) : 0;
+  size_t o_col = dw ? cv.take((size_t)M * CKK * es) : 0;
+  size_t o_xp = (dw && padded) ? cv.take((size_t)d.B * d.C * HP * WP * es) : 0;
+  size_t o_g = cv.take(ws_w);
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
-  void* col = at(ws, o_col);
   if (dx) {
-    pd.args.d = col;
-    VH_TRY(run_igemm(pd, (float*)at(ws, o_g), st));
-    void* dxp = padded ? at(ws, o_xp) : dx;
-    VH_TRY(VH_DISPATCH(dt, run_col2im, col, dxp, (int)d.B, (int)d.C, (int)HP, (int)WP, (int)d.KH, (int)d.KW,
-                       (int)d.SH, (int)d.SW, (int)d.HO, (int)d.WO, st));
-    if (padded)
-      VH_TRY(VH_DISPATCH(dt, run_crop, dxp, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.PH, (int)d.PW, st));
+    float* dcolT = (float*)at(ws, o_dcol);
+    VH_TRY(run_igemm_f32out(pd, dcolT, st));
+    VH_TRY(VH_DISPATCH(dt, run_col2im_t, dcolT, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.KH,
+                       (int)d.KW, (int)d.SH, (int)d.SW, (int)d.PH, (int)d.PW, (int)d.HO, (int)d.WO, st));
   }
   if (dw) {
+    void* col = at(ws, o_col);
     const void* xin = x;
     if (padded) {
       VH_TRY(VH_DISPATCH(dt, run_pad, x, at(ws, o_xp), (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.PH,
@@ -392,7 +391,6 @@ static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const C
   return VH_DISPATCH(dt, run_direct_wgrad, dy, x, dw, g, (float*)ws, slices, len, st);
 }
 
-static int add_bias_nchw(int dt, void* y, const void* bias, const ConvDims& d, hipStream_t st);
 
 // ------------------------------------------------------------------ GEMM entry helper
 static int gemm(int dt, int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc,
@@ -589,8 +587,8 @@ int vh_col2im(int dtype, const void* col, void* output, int64_t batch, int64_t c
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w, pad_h, \
              pad_w, h_out, w_out};                                                                          \
   VH_TRY(check_conv(d, true));                                                                              \
-  if (!(p0) || !(p1) || !(p2)) return set_error(VH_ERR_BAD_ARG, "null pointer");                            \
-  if (batch == 0) return VH_OK;
+  if (batch == 0) return VH_OK;                                                                             \
+  if (!(p0) || !(p1) || !(p2)) return set_error(VH_ERR_BAD_ARG, "null pointer");
 
 #define VH_CONV_ARGS                                                                                       \
   int64_t batch, int64_t in_channels, int64_t out_channels, int64_t height, int64_t width, int64_t kernel_h, \
@@ -600,7 +598,7 @@ int vh_col2im(int dtype, const void* col, void* output, int64_t batch, int64_t c
 int vh_direct_conv(int dtype, const void* input, const void* weight, void* output, VH_CONV_ARGS) {
   VH_CONV_PROLOGUE(input, weight, output);
   ConvGeom g = geom_of(d);
-  return VH_DISPATCH(dtype, run_direct_fwd, input, weight, output, g, S(stream));
+  return VH_DISPATCH(dtype, run_direct_fwd, input, weight, nullptr, output, g, S(stream));
 }
 
 int vh_igemm(int dtype, const void* input, const void* weight, void* output, VH_CONV_ARGS) {
@@ -676,19 +674,18 @@ int vh_conv2d_forward(int dtype, int algo, const void* input, const void* weight
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
              pad_h, pad_w, 0, 0};
   VH_TRY(layer_dims(d));
-  if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (algo == VH_ALGO_AUTO)
     algo = vh_conv_algo_select_mi355x(batch, in_channels, out_channels, height, width, kernel_h, kernel_w,
                                       stride_h, stride_w, pad_h, pad_w);
   if (algo < VH_ALGO_DIRECT || algo > VH_ALGO_IGEMM) return set_error(VH_ERR_BAD_ARG, "bad algorithm %d", algo);
   if (algo_used) *algo_used = algo;
   if (batch == 0) return VH_OK;
+  if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   if (algo == VH_ALGO_IGEMM) return igemm_fwd(dtype, input, weight, bias, output, d, st);
   if (algo == VH_ALGO_IM2COL) return im2col_fwd(dtype, input, weight, bias, output, d, st);
   ConvGeom g = geom_of(d);
-  VH_TRY(VH_DISPATCH(dtype, run_direct_fwd, input, weight, output, g, st));
-  return bias ? add_bias_nchw(dtype, output, bias, d, st) : VH_OK;
+  return VH_DISPATCH(dtype, run_direct_fwd, input, weight, bias, output, g, st);
 }
 
 int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
@@ -698,11 +695,11 @@ int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* in
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
              pad_h, pad_w, 0, 0};
   VH_TRY(layer_dims(d));
-  if (!out_grad || (grad_input && !weight) || (grad_weight && !input))
-    return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (algo < VH_ALGO_DIRECT || algo > VH_ALGO_IGEMM) return set_error(VH_ERR_BAD_ARG, "bad algorithm %d", algo);
   hipStream_t st = S(stream);
   if (batch == 0) return VH_OK;
+  if (!out_grad || (grad_input && !weight) || (grad_weight && !input))
+    return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (algo == VH_ALGO_IM2COL) {
     if (grad_input || grad_weight) VH_TRY(im2col_bwd(dtype, out_grad, input, weight, grad_input, grad_weight, d, st));
   } else if (algo == VH_ALGO_IGEMM) {
@@ -736,8 +733,8 @@ int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight
   ConvDims d;
   VH_TRY(convt_dims(d, batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
                     pad_h, pad_w));
-  if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (batch == 0) return VH_OK;
+  if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   // y = dgrad(dy := x; W viewed OIHW with O = in_channels, C = out_channels) + bias
   ConvGeom g = geom_of(d);
@@ -778,9 +775,9 @@ int vh_conv_transpose2d_backward(int dtype, const void* out_grad, const void* in
   ConvDims d;
   VH_TRY(convt_dims(d, batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
                     pad_h, pad_w));
+  if (batch == 0) return VH_OK;
   if (!out_grad || (grad_input && !weight) || (grad_weight && !input))
     return set_error(VH_ERR_BAD_ARG, "null pointer");
-  if (batch == 0) return VH_OK;
   hipStream_t st = S(stream);
   // In conv terms (d): x = out_grad (C = out_channels), dy = input (O = in_channels).
   if (grad_input) VH_TRY(igemm_fwd(dtype, out_grad, weight, nullptr, grad_input, d, st));
@@ -832,8 +829,8 @@ int vh_pixel_shuffle(int dtype, const void* input, void* output, int64_t batch, 
   if (batch < 0 || channels <= 0 || height <= 0 || width <= 0 || upscale <= 0)
     return set_error(VH_ERR_BAD_SHAPE, "bad PixelShuffle geometry");
   VH_TRY(check_sizes({batch * channels * height * width * upscale * upscale}));
-  if (!input || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (batch == 0) return VH_OK;
+  if (!input || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   return VH_DISPATCH(dtype, run_pixel_shuffle, input, output, (int)batch, (int)channels, (int)height, (int)width,
                      (int)upscale, 0, S(stream));
 }
@@ -845,36 +842,10 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
   if (batch < 0 || channels <= 0 || height <= 0 || width <= 0 || upscale <= 0)
     return set_error(VH_ERR_BAD_SHAPE, "bad PixelShuffle geometry");
   VH_TRY(check_sizes({batch * channels * height * width * upscale * upscale}));
-  if (!out_grad || !grad_input) return set_error(VH_ERR_BAD_ARG, "null pointer");
   if (batch == 0) return VH_OK;
+  if (!out_grad || !grad_input) return set_error(VH_ERR_BAD_ARG, "null pointer");
   return VH_DISPATCH(dtype, run_pixel_shuffle, out_grad, grad_input, (int)batch, (int)channels, (int)height,
                      (int)width, (int)upscale, 1, S(stream));
 }
 
 }  // extern "C"
-
-namespace vh {
-template <typename T>
-__global__ __launch_bounds__(256) void bias_add_kernel(typename Elem<T>::storage* y,
-                                                       const typename Elem<T>::storage* b, int C, int HW,
-                                                       long total) {
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    int c = (int)((i / HW) % C);
-    y[i] = Elem<T>::from_f32(Elem<T>::to_f32(y[i]) + Elem<T>::to_f32(b[c]));
-  }
-}
-
-template <typename T>
-static int run_bias_add(void* y, const void* b, int C, int HW, long total, hipStream_t st) {
-  using Sx = typename Elem<T>::storage;
-  long g = std::min<long>((total + 255) / 256, 65535L * 8);
-  bias_add_kernel<T><<<(int)std::max<long>(g, 1), 256, 0, st>>>((Sx*)y, (const Sx*)b, C, HW, total);
-  VH_LAUNCH_CHECK();
-  return VH_OK;
-}
-
-static int add_bias_nchw(int dt, void* y, const void* bias, const ConvDims& d, hipStream_t st) {
-  long total = d.B * d.O * d.HO * d.WO;
-  return VH_DISPATCH(dt, run_bias_add, y, bias, (int)d.O, (int)(d.HO * d.WO), total, st);
-}
-}  // namespace vh

@@ -41,6 +41,13 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
   IgemmArgs a = p.args;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   dim3 grid((unsigned)tiles, 1, (unsigned)p.splits);
+  if (p.f32_out) {  // fp32 row-major result, one split
+    IgemmArgs pa = a;
+    pa.d = ws;
+    igemm_kernel<T, AK, BKIND, OK_PARTIAL, BM, BN, BK><<<dim3((unsigned)tiles, 1, 1), 256, 0, st>>>(pa);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   if (p.splits > 1) {
     IgemmArgs pa = a;
     pa.d = ws;
@@ -105,6 +112,16 @@ size_t igemm_prepare(IgemmPlan& p) {
   p.args.k_chunk = chunk;
   p.splits = (K + chunk - 1) / chunk;
   return p.splits > 1 ? (size_t)p.splits * p.args.M * p.args.N * sizeof(float) : 0;
+}
+
+int run_igemm_f32out(IgemmPlan& p, float* out, hipStream_t st) {
+  if (p.args.M <= 0 || p.args.N <= 0) return VH_OK;
+  p.splits = 1;
+  p.args.k_chunk = p.args.K;
+  p.f32_out = 1;
+  int r = p.dtype == VH_BF16 ? launch_typed<bf16>(p, out, st) : launch_typed<float>(p, out, st);
+  p.f32_out = 0;
+  return r;
 }
 
 int run_igemm(IgemmPlan& p, float* ws, hipStream_t st) {

@@ -16,13 +16,17 @@ static inline int grid_for(long n, int per_block = 256, int cap = 65535 * 8) {
 // ============================================================== direct conv
 // Volta's direct_conv.wgsl:27-105 assigns one output element per invocation; so
 // does this kernel (consecutive lanes take consecutive ow, so x loads and y
-// stores coalesce).  fp32 accumulation in the reference's order ic -> kh -> kw
-// (conv.rs:1370-1407).
+// stores coalesce).  The f32 sum runs in the reference's CPU order
+// ic -> kh -> kw (conv.rs:1370-1407) with separate multiply and add roundings
+// (Rust never contracts a*b+c), so f32 results equal Volta's CPU Direct loop
+// bit for bit.  The bias is added in fp32 before the single output rounding.
 template <typename T>
 __global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>::storage* __restrict__ x,
                                                          const typename Elem<T>::storage* __restrict__ w,
+                                                         const typename Elem<T>::storage* __restrict__ bias,
                                                          typename Elem<T>::storage* __restrict__ y,
                                                          ConvGeom g, long total) {
+#pragma clang fp contract(off)
   for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
     int q = (int)(i % g.Q);
     long t = i / g.Q;
@@ -40,21 +44,26 @@ __global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>:
         for (int k = 0; k < g.S; ++k) {
           int ww = q * g.sw + k - g.pw;
           if (ww < 0 || ww >= g.W) continue;
-          s += Elem<T>::to_f32(xn[((long)c * g.H + h) * g.W + ww]) *
-               Elem<T>::to_f32(wo[(c * g.R + r) * g.S + k]);
+          float prod = Elem<T>::to_f32(xn[((long)c * g.H + h) * g.W + ww]) *
+                       Elem<T>::to_f32(wo[(c * g.R + r) * g.S + k]);
+          s += prod;
         }
       }
+    if (bias) s += Elem<T>::to_f32(bias[o]);
     y[i] = Elem<T>::from_f32(s);
   }
 }
 
-// Input gradient, one input element per lane (conv_backward_input.wgsl:26-89),
-// visiting only output positions whose receptive field holds the element.
+// Input gradient, one input element per lane (conv_backward_input.wgsl:26-89).
+// Terms are visited in the reference's order oc -> oh -> ow (conv.rs:458-505),
+// skipping the output positions whose receptive field misses the element, with
+// unfused multiply/add: f32 results equal Volta's CPU loop bit for bit.
 template <typename T>
 __global__ __launch_bounds__(256) void direct_dgrad_kernel(const typename Elem<T>::storage* __restrict__ dy,
                                                            const typename Elem<T>::storage* __restrict__ w,
                                                            typename Elem<T>::storage* __restrict__ dx,
                                                            ConvGeom g, long total) {
+#pragma clang fp contract(off)
   for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
     int iw = (int)(i % g.W);
     long t = i / g.W;
@@ -62,23 +71,23 @@ __global__ __launch_bounds__(256) void direct_dgrad_kernel(const typename Elem<T
     t /= g.H;
     int c = (int)(t % g.C);
     int n = (int)(t / g.C);
-    int th = ih + g.ph, tw = iw + g.pw;
+    const int th = ih + g.ph, tw = iw + g.pw;
+    // first output row/col whose window reaches this element: oh*sh > th - R
+    const int oh0 = th - g.R + 1 <= 0 ? 0 : (th - g.R + 1 + g.sh - 1) / g.sh;
+    const int ow0 = tw - g.S + 1 <= 0 ? 0 : (tw - g.S + 1 + g.sw - 1) / g.sw;
     float s = 0.f;
-    for (int o = 0; o < g.O; ++o)
-      for (int r = 0; r < g.R; ++r) {
-        int a = th - r;
-        if (a < 0 || a % g.sh) continue;
-        int p = a / g.sh;
-        if (p >= g.P) continue;
-        for (int k = 0; k < g.S; ++k) {
-          int b = tw - k;
-          if (b < 0 || b % g.sw) continue;
-          int q = b / g.sw;
-          if (q >= g.Q) continue;
-          s += Elem<T>::to_f32(dy[(((long)n * g.O + o) * g.P + p) * g.Q + q]) *
-               Elem<T>::to_f32(w[((o * g.C + c) * g.R + r) * g.S + k]);
+    for (int o = 0; o < g.O; ++o) {
+      const auto* dyo = dy + (((long)n * g.O + o) * g.P) * g.Q;
+      const auto* wo = w + ((long)o * g.C + c) * g.R * g.S;
+      for (int oh = oh0; oh < g.P && oh * g.sh <= th; ++oh) {
+        const int r = th - oh * g.sh;
+        for (int ow = ow0; ow < g.Q && ow * g.sw <= tw; ++ow) {
+          const int k = tw - ow * g.sw;
+          float prod = Elem<T>::to_f32(dyo[(long)oh * g.Q + ow]) * Elem<T>::to_f32(wo[r * g.S + k]);
+          s += prod;
         }
       }
+    }
     dx[i] = Elem<T>::from_f32(s);
   }
 }
@@ -223,6 +232,41 @@ __global__ __launch_bounds__(256) void col2im_kernel(const typename Elem<T>::sto
   }
 }
 
+// Input gradient of the Im2col path straight from the fp32 column gradient
+// stored transposed, dcolT[(c*KH+kh)*KW+kw][(b*HO+oh)*WO+ow] (the GEMM's own
+// output layout, so it is never rounded to bf16), cropping the padding:
+// x[b][c][h][w] sums the entries whose padded position (h+ph, w+pw) they copy.
+template <typename T>
+__global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__ dcolT,
+                                                       typename Elem<T>::storage* __restrict__ x, int C, int H,
+                                                       int W, int KH, int KW, int SH, int SW, int PH, int PW,
+                                                       int HO, int WO, long M, long total) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    int w = (int)(i % W);
+    long t = i / W;
+    int h = (int)(t % H);
+    t /= H;
+    int c = (int)(t % C);
+    long b = t / C;
+    const int hp = h + PH, wp = w + PW;
+    float s = 0.f;
+    for (int kh = 0; kh < KH; ++kh) {
+      int a = hp - kh;
+      if (a < 0 || a % SH) continue;
+      int oh = a / SH;
+      if (oh >= HO) continue;
+      for (int kw = 0; kw < KW; ++kw) {
+        int bb = wp - kw;
+        if (bb < 0 || bb % SW) continue;
+        int ow = bb / SW;
+        if (ow >= WO) continue;
+        s += dcolT[(long)((c * KH + kh) * KW + kw) * M + (b * HO + oh) * WO + ow];
+      }
+    }
+    x[i] = Elem<T>::from_f32(s);
+  }
+}
+
 // ============================================================== weight re-layouts
 // src viewed as [A][B][RS]; dst[a][rs][b] (flip_rs: rs -> RS-1-rs) or dst[b][rs][a] (swap).
 template <typename T>
@@ -304,10 +348,10 @@ __global__ __launch_bounds__(256) void pixel_shuffle_kernel(const typename Elem<
 
 // ============================================================== typed launchers
 template <typename T>
-int run_direct_fwd(const void* x, const void* w, void* y, const ConvGeom& g, hipStream_t st) {
+int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st) {
   long total = (long)g.N * g.O * g.P * g.Q;
   using S = typename Elem<T>::storage;
-  direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (S*)y, g, total);
+  direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, total);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -385,6 +429,17 @@ int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int
 }
 
 template <typename T>
+int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int PH,
+                 int PW, int HO, int WO, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  long total = (long)B * C * H * W;
+  col2im_t_kernel<T><<<grid_for(total), 256, 0, st>>>(dcolT, (S*)x, C, H, W, KH, KW, SH, SW, PH, PW, HO, WO,
+                                                      (long)B * HO * WO, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
 int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st) {
   using S = typename Elem<T>::storage;
   relayout_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>((const S*)src, (S*)dst, A, B, RS, swap);
@@ -438,7 +493,9 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
 }
 
 #define VH_INST(T)                                                                                      \
-  template int run_direct_fwd<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);        \
+  template int run_direct_fwd<T>(const void*, const void*, const void*, void*, const ConvGeom&, hipStream_t); \
+  template int run_col2im_t<T>(const float*, void*, int, int, int, int, int, int, int, int, int, int, int, int,  \
+                               hipStream_t);                                                            \
   template int run_direct_dgrad<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);      \
   template size_t direct_wgrad_ws<T>(const ConvGeom&, int*, int*);                                      \
   template int run_direct_wgrad<T>(const void*, const void*, void*, const ConvGeom&, float*, int, int,  \

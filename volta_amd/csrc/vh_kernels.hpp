@@ -11,17 +11,24 @@ struct IgemmPlan {
   int akind, bkind, okind;  // OpndKind x2, OutKind
   IgemmArgs args;
   int splits;               // requested split-K factor (1 = none)
+  int f32_out;              // internal: store fp32 row-major D (run_igemm_f32out)
 };
 // Fills args.k_chunk / splits and returns the fp32 workspace bytes needed.
 size_t igemm_prepare(IgemmPlan& plan);
 int run_igemm(IgemmPlan& plan, float* ws, hipStream_t st);
+// Runs the plan with splits = 1 and stores D[M][N] row-major in fp32 to `out`.
+int run_igemm_f32out(IgemmPlan& plan, float* out, hipStream_t st);
 // Heuristic split-K factor for a problem with the given tile grid and K.
 int pick_splits(int M, int N, int K, int dtype);
 ConvGeom make_geom(int N, int C, int H, int W, int O, int R, int S, int P, int Q, int sh, int sw, int ph,
                    int pw);
 
 // ---- other kernels (vh_kernels.hip) ----
-template <typename T> int run_direct_fwd(const void* x, const void* w, void* y, const ConvGeom& g, hipStream_t st);
+template <typename T>
+int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st);
+template <typename T>
+int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int PH,
+                 int PW, int HO, int WO, hipStream_t st);
 template <typename T> int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g, hipStream_t st);
 template <typename T> size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len);
 template <typename T>
