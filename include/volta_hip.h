@@ -69,6 +69,12 @@ int vh_download(void* dst_host, const void* src_dev, size_t bytes, void* stream)
 int vh_stream_sync(void* stream);
 /* Releases cached workspace and pooled buffers (pool.rs clear). */
 int vh_release_cache(void);
+/* Kernel choice inside an algorithm (no reference counterpart: Volta has one
+ * shader per op).  VH_POLICY_FASTEST (default) uses specialised kernels where
+ * their shape envelope allows; VH_POLICY_GENERIC forces the generic MFMA
+ * implicit GEMM, so both can be checked against the same oracle. */
+typedef enum { VH_POLICY_FASTEST = 0, VH_POLICY_GENERIC = 1 } vh_kernel_policy;
+int vh_set_kernel_policy(int policy);
 
 /* ------------------------------------------------------------------ matmul */
 /* RawTensor::gpu_matmul, src/ops/gpu_ops.rs:151-169 (GpuKernels::matmul,

@@ -224,6 +224,46 @@ def test_bad_shape_is_an_error_not_a_crash():
     assert y.shape == (0, 3, 5, 5)
 
 
+# ------------------------------------------------------------------ stride-1 fast path vs generic
+HALO_CASES = [
+    # (B, C, O, H, W, K, S, P): shapes inside the bf16 halo kernel's envelope
+    (3, 16, 32, 14, 14, 3, 1, 1),    # blocks span 2-3 images
+    (2, 32, 128, 28, 28, 3, 1, 1),   # 128-channel tile (two wave rows)
+    (2, 64, 64, 56, 56, 3, 1, 1),    # config 3 first layer, batch 2
+    (1, 16, 48, 20, 24, 5, 1, 2),    # 5x5 pad 2, O not a tile multiple
+    (2, 16, 16, 9, 10, 3, 1, 0),     # no padding (P = H - 2)
+    (5, 32, 16, 4, 4, 3, 1, 1),      # tiny images, many per block
+    (2, 48, 80, 16, 18, 1, 1, 0),    # 1x1 stride 1
+]
+
+
+@pytest.mark.parametrize("case", HALO_CASES, ids=_conv_ids)
+@pytest.mark.parametrize("policy", [volta_amd._lib.POLICY_FASTEST, volta_amd._lib.POLICY_GENERIC])
+def test_conv2d_bf16_fast_and_generic_paths(case, policy):
+    B, C, O, H, W, K, S, P = case
+    dt = "bf16"
+    volta_amd.check(volta_amd.lib().vh_set_kernel_policy(policy))
+    try:
+        g = rng(sum(case) + 7)
+        x, xt = prep(g.standard_normal((B, C, H, W)), dt)
+        w, wt = prep(g.standard_normal((O, C, K, K)) * np.sqrt(2.0 / (C * K * K)), dt)
+        b, bt = prep(g.uniform(-1, 1, (O,)), dt)
+        conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=DEV, dtype=DTYPES[dt])
+        conv.weight, conv.bias = wt, bt
+        conv.set_algo(vnn.ConvAlgo.IGEMM)
+        y = conv.forward(xt)
+        bb = b[None, :, None, None]
+        kw = dict(stride=(S, S), pad=(P, P))
+        check(y, oracle.direct_conv, (x, w), dt, "y", kw, extra_ref=bb, extra_scale=np.abs(bb))
+        dy, dyt = prep(g.standard_normal(tuple(y.shape)), dt)
+        dx, dw, db = conv.backward(dyt, xt)
+        check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", kw)
+        check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw)
+        check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+    finally:
+        volta_amd.check(volta_amd.lib().vh_set_kernel_policy(volta_amd._lib.POLICY_FASTEST))
+
+
 # ------------------------------------------------------------------ ConvTranspose2d
 CT_CASES = [
     # (B, CI, CO, H, W, K, S, P)

@@ -26,6 +26,7 @@ F32 = 0
 BF16 = 1
 
 ALGO_DIRECT, ALGO_IM2COL, ALGO_IGEMM, ALGO_AUTO = 0, 1, 2, 3
+POLICY_FASTEST, POLICY_GENERIC = 0, 1
 
 
 class VoltaHipError(RuntimeError):
@@ -52,6 +53,7 @@ SIGNATURES = {
     "vh_download": [_P, _P, _SZ, _P],
     "vh_stream_sync": [_P],
     "vh_release_cache": [],
+    "vh_set_kernel_policy": [_INT],
     "vh_matmul": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_matmul_backward_a": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_matmul_backward_b": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],

@@ -5,6 +5,7 @@
 // src/nn/layers/{conv,conv_transpose,linear}.rs.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <algorithm>
 #include <map>
@@ -25,6 +26,14 @@ int set_error(int status, const char* fmt, ...) {
   va_end(ap);
   return status;
 }
+
+// Specialised kernels (halo conv, ...) are used where their envelope allows
+// unless the policy says otherwise (vh_set_kernel_policy; the environment
+// variable VOLTA_HIP_GENERIC=1 sets the initial policy to generic).
+static bool g_fast_paths = [] {
+  const char* e = getenv("VOLTA_HIP_GENERIC");
+  return !(e && e[0] == '1');
+}();
 
 // ------------------------------------------------------------------ device init
 static std::once_flag g_init_once;
@@ -190,6 +199,11 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wt = at(ws, o_w);
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wt, (int)d.O, (int)d.C, (int)RS, 0, st));
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
+    int r = halo_conv_bf16(x, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
+                           (int)d.KW, (int)d.PH, (int)d.PW, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wt, (int)(RS * d.C), (int)d.O, ((RS * d.C) % vec) == 0};
   p.args.b = Operand{x, 0, p.args.N, 0};
@@ -221,7 +235,14 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wd = at(ws, o_w);
-  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st));
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && d.PH <= d.KH - 1 && d.PW <= d.KW - 1 && g_fast_paths) {
+    // stride 1: dX = conv(dY, W rotated 180 degrees with O and C swapped), pad K-1-p
+    VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 1));
+    int r = halo_conv_bf16(dy, wd, nullptr, dx, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C, (int)d.KH,
+                           (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
+  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wd, (int)(RS * d.O), (int)d.C, ((RS * d.O) % vec) == 0};
   p.args.b = Operand{dy, 0, p.args.N, 0};
@@ -433,6 +454,13 @@ static hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 extern "C" {
 
 int vh_init(void) { return ensure_init(); }
+
+int vh_set_kernel_policy(int policy) {
+  if (policy != VH_POLICY_FASTEST && policy != VH_POLICY_GENERIC)
+    return set_error(VH_ERR_BAD_ARG, "unknown kernel policy %d", policy);
+  g_fast_paths = policy == VH_POLICY_FASTEST;
+  return VH_OK;
+}
 
 const char* vh_last_error(void) { return g_err; }
 

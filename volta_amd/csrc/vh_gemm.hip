@@ -97,7 +97,9 @@ int pick_splits(int M, int N, int K, int dtype) {
   Tile t = pick_tile(M, N);
   const int bk = dtype == VH_BF16 ? 32 : 16;
   long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
-  if (tiles >= 512) return 1;
+  // Split K only when the tile grid leaves most of the 256 CUs idle and K is
+  // long: partial sums cost 2 x splits x M x N x 4 bytes of HBM traffic.
+  if (tiles >= 192 || K < 1024) return 1;
   long want = (512 + tiles - 1) / tiles;
   long maxk = std::max<long>(1, K / (bk * 8));
   return (int)std::max<long>(1, std::min<long>(std::min(want, maxk), 256));

@@ -1,0 +1,331 @@
+// vh_halo.hip -- bf16 implicit-GEMM convolution for stride-1 layers on NCHW
+// tensors, gfx950 MFMA (v_mfma_f32_32x32x16_bf16).  Serves the forward pass
+// and, with a flipped/transposed weight, the input gradient.
+//
+// GEMM view: rows = output channels o, columns = output positions m = (n,p,q)
+// (flattened over the batch), K = (input channel c, tap r, tap s).
+//
+// A block owns BM output channels x BN consecutive positions.  For every group
+// of 16 input channels it stages in LDS
+//   * the weights  W[o][tap][c16]          (K-packed per (o, tap)), and
+//   * the input "halo": every padded input row the BN positions touch, stored
+//     channel-packed, cell = (ext row, padded column) -> 16 channels,
+// then runs all R*S taps against that one copy of the input: tap (r,s) of
+// position (n,p,q) is the cell (n*Hp + p + r, q + s), i.e. a fixed LDS address
+// shift.  x is read from HBM once per block (plus the halo rows), with dword
+// loads along rows that are transposed to channel-packed cells in registers.
+//
+// LDS is split into two half-planes (channels 0-7, 8-15) so that the 64 lanes
+// of one fragment read walk consecutive 16-byte cells: lanes 0-31 read plane 0,
+// lanes 32-63 plane 1, each at consecutive positions / output channels.
+#include <algorithm>
+
+#include "vh_kernels.hpp"
+
+namespace vh {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct HaloArgs {
+  const uint16_t* x;     // [N][C][H][W]
+  const uint16_t* wt;    // [O][R*S][C]
+  const uint16_t* bias;  // [O] or nullptr
+  uint16_t* y;           // [N][O][P][Q]
+  int N, C, H, W, O, P, Q, ph, pw;
+  int Hp, Wp;            // padded input extents
+  int M;                 // N*P*Q
+  int rows_max;          // max ext rows any block needs
+  FastDiv fPQ, fQ;
+};
+
+template <int R, int S, int WM, int XI>
+struct HaloCfg {
+  static constexpr int RS = R * S;
+  static constexpr int FM = 2, FN = 2;            // 32x32 tiles per wave
+  static constexpr int WN = 4 / WM;               // waves along positions
+  static constexpr int BM = WM * FM * 32;
+  static constexpr int BN = WN * FN * 32;
+  static constexpr int WUNITS = BM * RS * 2;      // 16-byte weight units per stage
+  static constexpr int WITER = (WUNITS + 255) / 256;
+  static constexpr int XITER = XI;                // x items per thread per stage (8 dwords each)
+};
+
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+  // low bf16 of a, low bf16 of b -> (a.lo | b.lo << 16)
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+template <int R, int S, int WM, int XI>
+__global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
+  using Cfg = HaloCfg<R, S, WM, XI>;
+  constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
+  extern __shared__ __attribute__((aligned(16))) u32x4 lds[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = (wave / Cfg::WN) * FM * 32;  // wave's first output channel in the tile
+  const int wn = (wave % Cfg::WN) * FN * 32;  // wave's first position in the tile
+
+  const int m0 = blockIdx.x * BN;
+  const int o0 = blockIdx.y * BM;
+  const int Wp = a.Wp;
+  const int cells = a.rows_max * Wp;       // cells per half-plane
+  const int w_units = 2 * RS * BM;         // uint4 per weight stage
+  const int stage = w_units + 2 * cells;   // uint4 per stage
+  // stage st: weights at lds + st*stage, x halo right after them
+#define WSM(st) (lds + (st) * stage)
+#define XSM(st) (lds + (st) * stage + w_units)
+
+  // first ext row this block needs: output row of its first position
+  uint32_t n_a, pq_a, p_a, q_a;
+  a.fPQ.divmod((uint32_t)m0, n_a, pq_a);
+  a.fQ.divmod(pq_a, p_a, q_a);
+  const int e_start = (int)n_a * a.Hp + (int)p_a;
+  const int m_last = min(m0 + BN, a.M) - 1;
+  uint32_t n_b, pq_b, p_b, q_b;
+  a.fPQ.divmod((uint32_t)m_last, n_b, pq_b);
+  a.fQ.divmod(pq_b, p_b, q_b);
+  const int rows = (int)n_b * a.Hp + (int)p_b + R - e_start;  // ext rows used by this block
+
+  // zero the padding columns once (never written by the loader)
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  const int padc = Wp - a.W;  // = 2*pw for stride 1 'same'-style padding, general otherwise
+  for (int i = tid; i < 2 * 2 * a.rows_max * padc; i += 256) {
+    int st = i / (2 * a.rows_max * padc);
+    int rem = i % (2 * a.rows_max * padc);
+    int half = rem / (a.rows_max * padc);
+    int r2 = rem % (a.rows_max * padc);
+    int e = r2 / padc, pc = r2 % padc;
+    int u = pc < a.pw ? pc : a.W + pc;  // columns [0,pw) and [W+pw, Wp)
+    XSM(st)[half * cells + e * Wp + u] = z;
+  }
+
+  // per-lane cell index of each B fragment column (fixed for the whole block)
+  int bcell[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int m = m0 + wn + j * 32 + (lane & 31);
+    int cidx = 0;
+    if (m < a.M) {
+      uint32_t n, pq, p, q;
+      a.fPQ.divmod((uint32_t)m, n, pq);
+      a.fQ.divmod(pq, p, q);
+      cidx = ((int)n * a.Hp + (int)p - e_start) * Wp + (int)q;
+    }
+    bcell[j] = cidx;
+  }
+
+  const int HW = a.H * a.W;
+  const int W2 = a.W >> 1;
+  const int x_items = 2 * rows * W2;
+  const long RSC = (long)RS * a.C;
+
+  u32x4 wreg[Cfg::WITER];
+  uint32_t xreg[Cfg::XITER][8];
+
+  auto gload = [&](int c0) {
+#pragma unroll
+    for (int it = 0; it < Cfg::WITER; ++it) {
+      int u = tid + it * 256;
+      if (u < Cfg::WUNITS) {
+        int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
+        int og = o0 + o;
+        wreg[it] = og < a.O ? *reinterpret_cast<const u32x4*>(a.wt + og * RSC + (long)tap * a.C + c0 + half * 8) : z;
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < Cfg::XITER; ++it) {
+      int i = tid + it * 256;
+      if (i < x_items) {
+        int wi = i % W2, t = i / W2;
+        int e = t % rows, half = t / rows;
+        int eg = e_start + e;
+        int n = eg / a.Hp, h = eg - n * a.Hp - a.ph;
+        if (h >= 0 && h < a.H && n < a.N) {
+          const uint32_t* src = reinterpret_cast<const uint32_t*>(
+              a.x + ((long)n * a.C + c0 + half * 8) * HW + (long)h * a.W + 2 * wi);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xreg[it][j] = src[(long)j * (HW >> 1)];
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xreg[it][j] = 0u;
+        }
+      }
+    }
+  };
+  auto sstore = [&](int st) {
+#pragma unroll
+    for (int it = 0; it < Cfg::WITER; ++it) {
+      int u = tid + it * 256;
+      if (u < Cfg::WUNITS) {
+        int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
+        WSM(st)[(half * RS + tap) * BM + o] = wreg[it];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < Cfg::XITER; ++it) {
+      int i = tid + it * 256;
+      if (i < x_items) {
+        int wi = i % W2, t = i / W2;
+        int e = t % rows, half = t / rows;
+        u32x4 c0v, c1v;
+        c0v.x = pack_lo(xreg[it][0], xreg[it][1]); c0v.y = pack_lo(xreg[it][2], xreg[it][3]);
+        c0v.z = pack_lo(xreg[it][4], xreg[it][5]); c0v.w = pack_lo(xreg[it][6], xreg[it][7]);
+        c1v.x = pack_hi(xreg[it][0], xreg[it][1]); c1v.y = pack_hi(xreg[it][2], xreg[it][3]);
+        c1v.z = pack_hi(xreg[it][4], xreg[it][5]); c1v.w = pack_hi(xreg[it][6], xreg[it][7]);
+        u32x4* base = XSM(st) + half * cells + e * Wp + a.pw + 2 * wi;
+        base[0] = c0v;
+        base[1] = c1v;
+      }
+    }
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int nk = a.C / 16;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int half_l = lane >> 5, row_l = lane & 31;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * 16);
+    const u32x4* Wp_ = WSM(st) + half_l * RS * BM + wm + row_l;
+    const u32x4* Xp_ = XSM(st) + half_l * cells;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int tap = r * S + s;
+        const int toff = r * Wp + s;
+        bf16x8 af[FM], bfr[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          af[i] = __builtin_bit_cast(bf16x8, Wp_[tap * BM + i * 32]);
+        }
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          bfr[j] = __builtin_bit_cast(bf16x8, Xp_[bcell[j] + toff]);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < nk) sstore(st ^ 1);
+    __syncthreads();
+  }
+
+#undef WSM
+#undef XSM
+  // epilogue: rows = o (acc_row), cols = positions (lane & 31); fp32 bias add,
+  // one rounding to bf16, NCHW store (lanes walk consecutive q).
+  const long PQ = (long)a.P * a.Q;
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    int m = m0 + wn + j * 32 + (lane & 31);
+    if (m >= a.M) continue;
+    uint32_t n, pq;
+    a.fPQ.divmod((uint32_t)m, n, pq);
+    uint16_t* yb = a.y + (long)n * a.O * PQ + pq;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        if (o < a.O) {
+          float val = acc[i][j][v];
+          if (a.bias) val += bf16_to_f32(a.bias[o]);
+          yb[(long)o * PQ] = f32_to_bf16(val);
+        }
+      }
+  }
+}
+
+// ---------------------------------------------------------------- host side
+namespace {
+
+template <int R, int S, int WM, int XI>
+int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
+  using Cfg = HaloCfg<R, S, WM, XI>;
+  auto kern = conv_halo_bf16_kernel<R, S, WM, XI>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    attr_set = true;
+  }
+  dim3 grid((unsigned)((a.M + Cfg::BN - 1) / Cfg::BN), (unsigned)((a.O + Cfg::BM - 1) / Cfg::BM));
+  kern<<<grid, 256, lds_bytes, st>>>(a);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <int R, int S, int WM>
+int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
+  const int items = 2 * a.rows_max * (a.W / 2);
+  const int xi = (items + 255) / 256;
+  if (xi <= 2) return launch_halo<R, S, WM, 2>(a, lds_bytes, st);
+  if (xi <= 4) return launch_halo<R, S, WM, 4>(a, lds_bytes, st);
+  if (xi <= 6) return launch_halo<R, S, WM, 6>(a, lds_bytes, st);
+  return launch_halo<R, S, WM, 8>(a, lds_bytes, st);
+}
+
+}  // namespace
+
+// Returns VH_ERR_UNSUPPORTED (without launching) when the shape is outside what
+// the halo kernel handles; the caller then uses the generic implicit GEMM.
+int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int N, int C, int H, int W, int O,
+                   int R, int S, int ph, int pw, hipStream_t st) {
+  const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
+  if (P <= 0 || Q <= 0) return VH_ERR_UNSUPPORTED;
+  if ((C % 16) != 0 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
+  if (!((R == 3 && S == 3) || (R == 5 && S == 5) || (R == 1 && S == 1))) return VH_ERR_UNSUPPORTED;
+  HaloArgs a;
+  a.x = (const uint16_t*)x;
+  a.wt = (const uint16_t*)wt;
+  a.bias = (const uint16_t*)bias;
+  a.y = (uint16_t*)y;
+  a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph; a.pw = pw;
+  a.Hp = H + 2 * ph;  // = P + R - 1
+  a.Wp = W + 2 * pw;  // = Q + S - 1
+  a.M = N * P * Q;
+  a.fPQ = FastDiv((uint32_t)(P * Q));
+  a.fQ = FastDiv((uint32_t)Q);
+  const int WM = O > 64 ? 2 : 1;
+  const int BN = (4 / WM) * 64;
+  const int BM = WM * 64;
+  // exact maximum number of ext rows over all blocks
+  int rows_max = 0;
+  for (int m0 = 0; m0 < a.M; m0 += BN) {
+    int ml = std::min(m0 + BN, a.M) - 1;
+    int na = m0 / (P * Q), pa = (m0 % (P * Q)) / Q;
+    int nb = ml / (P * Q), pb = (ml % (P * Q)) / Q;
+    rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
+  }
+  a.rows_max = rows_max;
+  const size_t stage = (size_t)(2 * R * S * BM + 2 * rows_max * a.Wp) * 16;
+  const size_t lds = 2 * stage;
+  if (lds > 160 * 1024 || (2 * rows_max * (W / 2) + 255) / 256 > 8) return VH_ERR_UNSUPPORTED;
+#define VH_HALO(RR, SS)                                           \
+  if (R == RR && S == SS) {                                       \
+    return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \
+  }
+  VH_HALO(3, 3)
+  VH_HALO(5, 5)
+  VH_HALO(1, 1)
+#undef VH_HALO
+  return VH_ERR_UNSUPPORTED;
+}
+
+}  // namespace vh

@@ -268,18 +268,21 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
 }
 
 // ============================================================== weight re-layouts
-// src viewed as [A][B][RS]; dst[a][rs][b] (flip_rs: rs -> RS-1-rs) or dst[b][rs][a] (swap).
+// src viewed as [A][B][RS]; dst[a][rs'][b] (swap = 0) or dst[b][rs'][a] (swap = 1)
+// with rs' = rs, or rs' = RS-1-rs (flip = 1: the 180-degree kernel rotation that
+// turns a stride-1 input gradient into a forward convolution).
 template <typename T>
 __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::storage* __restrict__ src,
                                                        typename Elem<T>::storage* __restrict__ dst, int A, int B,
-                                                       int RS, int swap) {
+                                                       int RS, int swap, int flip) {
   long total = (long)A * B * RS;
   for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
     int rs = (int)(i % RS);
     long t = i / RS;
     int b = (int)(t % B);
     int a = (int)(t / B);
-    long d = swap ? ((long)b * RS + rs) * A + a : ((long)a * RS + rs) * B + b;
+    int rd = flip ? RS - 1 - rs : rs;
+    long d = swap ? ((long)b * RS + rd) * A + a : ((long)a * RS + rd) * B + b;
     dst[d] = src[i];
   }
 }
@@ -440,9 +443,9 @@ int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH
 }
 
 template <typename T>
-int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st) {
+int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip) {
   using S = typename Elem<T>::storage;
-  relayout_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>((const S*)src, (S*)dst, A, B, RS, swap);
+  relayout_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>((const S*)src, (S*)dst, A, B, RS, swap, flip);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -506,7 +509,7 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
                              hipStream_t);                                                              \
   template int run_col2im<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \
                              hipStream_t);                                                              \
-  template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t);                    \
+  template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t, int);               \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
   template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);

@@ -42,7 +42,8 @@ int run_im2col(const void* x, void* col, int B, int C, int H, int W, int KH, int
 template <typename T>
 int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int HO,
                int WO, hipStream_t st);
-template <typename T> int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st);
+template <typename T>
+int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip = 0);
 size_t channel_sum_ws(int N, int C, int HW, int* nslice);
 template <typename T>
 int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st);
@@ -51,5 +52,11 @@ template <typename T>
 int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st);
 template <typename T>
 int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
+
+// ---- stride-1 bf16 halo convolution (vh_halo.hip) ----
+// wt is [O][R*S][C]; returns VH_ERR_UNSUPPORTED without launching when the shape
+// is outside the kernel's envelope.
+int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int N, int C, int H, int W, int O,
+                   int R, int S, int ph, int pw, hipStream_t st);
 
 }  // namespace vh
