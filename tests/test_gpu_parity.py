@@ -234,6 +234,9 @@ HALO_CASES = [
     (2, 16, 16, 9, 10, 3, 1, 0),     # no padding (P = H - 2)
     (5, 32, 16, 4, 4, 3, 1, 1),      # tiny images, many per block
     (2, 48, 80, 16, 18, 1, 1, 0),    # 1x1 stride 1
+    (2, 16, 16, 8, 8, 3, 1, 2),      # even padding wider than 1 (P = H + 2)
+    (4, 64, 96, 12, 12, 3, 1, 1),    # O and C not multiples of the 64-wide tiles
+    (2, 128, 64, 9, 9, 3, 1, 1),     # odd image size (W odd: generic fallback)
 ]
 
 

@@ -249,9 +249,28 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
-// Weight gradient as implicit GEMM with split-K over output positions:
-// rows = O (A = dY), columns = (kh, kw, c) (B = gather of x), stored OIHW.
-static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, const ConvDims& d, hipStream_t st) {
+// Weight gradient.  bf16 stride-1 layers use the row-streaming kernel
+// (vh_wgrad.hip), which can also produce the bias gradient from the same pass
+// (*db_done = true then); everything else runs the generic implicit GEMM with
+// split-K over output positions: rows = O (A = dY), columns = (kh, kw, c)
+// (B = gather of x), stored OIHW.
+static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db, bool* db_done,
+                       const ConvDims& d, hipStream_t st) {
+  if (db_done) *db_done = false;
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
+    size_t need = wgrad_rows_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH, (int)d.KW,
+                                (int)d.PH, (int)d.PW, db != nullptr);
+    if (need) {
+      void* ws;
+      VH_TRY(ws_get(st, need, &ws));
+      int r = wgrad_rows_bf16(dy, x, dw, db, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
+                              (int)d.KW, (int)d.PH, (int)d.PW, (float*)ws, need, st);
+      if (r != VH_ERR_UNSUPPORTED) {
+        if (r == VH_OK && db_done) *db_done = db != nullptr;
+        return r;
+      }
+    }
+  }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   IgemmPlan p{};
@@ -652,7 +671,7 @@ int vh_igemm_backward_input(int dtype, const void* out_grad, const void* weight,
 
 int vh_igemm_backward_weight(int dtype, const void* out_grad, const void* input, void* grad_weight, VH_CONV_ARGS) {
   VH_CONV_PROLOGUE(out_grad, input, grad_weight);
-  return igemm_wgrad(dtype, out_grad, input, grad_weight, d, S(stream));
+  return igemm_wgrad(dtype, out_grad, input, grad_weight, nullptr, nullptr, d, S(stream));
 }
 
 // ------------------------------------------------------------------ algorithm selection
@@ -732,7 +751,11 @@ int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* in
     if (grad_input || grad_weight) VH_TRY(im2col_bwd(dtype, out_grad, input, weight, grad_input, grad_weight, d, st));
   } else if (algo == VH_ALGO_IGEMM) {
     if (grad_input) VH_TRY(igemm_dgrad(dtype, out_grad, weight, grad_input, d, st));
-    if (grad_weight) VH_TRY(igemm_wgrad(dtype, out_grad, input, grad_weight, d, st));
+    if (grad_weight) {
+      bool db_done = false;
+      VH_TRY(igemm_wgrad(dtype, out_grad, input, grad_weight, grad_bias, &db_done, d, st));
+      if (db_done) grad_bias = nullptr;
+    }
   } else {
     ConvGeom g = geom_of(d);
     if (grad_input) VH_TRY(VH_DISPATCH(dtype, run_direct_dgrad, out_grad, weight, grad_input, g, st));
@@ -809,7 +832,7 @@ int vh_conv_transpose2d_backward(int dtype, const void* out_grad, const void* in
   hipStream_t st = S(stream);
   // In conv terms (d): x = out_grad (C = out_channels), dy = input (O = in_channels).
   if (grad_input) VH_TRY(igemm_fwd(dtype, out_grad, weight, nullptr, grad_input, d, st));
-  if (grad_weight) VH_TRY(igemm_wgrad(dtype, input, out_grad, grad_weight, d, st));
+  if (grad_weight) VH_TRY(igemm_wgrad(dtype, input, out_grad, grad_weight, nullptr, nullptr, d, st));
   if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.C, d.H * d.W, st));
   return VH_OK;
 }

@@ -59,4 +59,12 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
 int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int N, int C, int H, int W, int O,
                    int R, int S, int ph, int pw, hipStream_t st);
 
+// ---- stride-1 bf16 weight gradient (vh_wgrad.hip) ----
+// Workspace bytes needed (0 if the shape is outside the kernel's envelope).
+size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, int pw, bool bias);
+// dW (OIHW, bf16) and optionally db; VH_ERR_UNSUPPORTED without launching if the
+// shape is outside the envelope.
+int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, int C, int H, int W, int O, int R,
+                    int S, int ph, int pw, float* ws, size_t ws_bytes, hipStream_t st);
+
 }  // namespace vh
