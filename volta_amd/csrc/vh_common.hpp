@@ -24,7 +24,11 @@ __host__ __device__ inline float bf16_to_f32(uint16_t b) {
 }
 
 // Round-to-nearest-even, NaN kept quiet (same rule as half::bf16::from_f32).
+// On the device this is gfx950's v_cvt_pk_bf16_f32 (RNE in hardware).
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+#endif
   uint32_t u;
   __builtin_memcpy(&u, &f, 4);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);

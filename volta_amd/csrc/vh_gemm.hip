@@ -54,7 +54,7 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
     igemm_kernel<T, AK, BKIND, OK_PARTIAL, BM, BN, BK><<<grid, 256, 0, st>>>(pa);
     VH_LAUNCH_CHECK();
     long total = (long)a.M * a.N;
-    int g = (int)std::min<long>((total + 255) / 256, 4096);
+    int g = (int)std::min<long>((total + 15) / 16, 65535L * 4);
     splitk_reduce_kernel<T, OUT><<<g, 256, 0, st>>>(a, ws, p.splits);
     VH_LAUNCH_CHECK();
   } else {

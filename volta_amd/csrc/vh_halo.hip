@@ -35,6 +35,7 @@ struct HaloArgs {
   int Hp, Wp;            // padded input extents
   int M;                 // N*P*Q
   int rows_max;          // max ext rows any block needs
+  int x_bytes;           // size of x in bytes (< 2^31: buffer-load range)
   FastDiv fPQ, fQ;
 };
 
@@ -46,6 +47,7 @@ struct HaloCfg {
   static constexpr int BM = WM * FM * 32;
   static constexpr int BN = WN * FN * 32;
   static constexpr int WUNITS = BM * RS * 2;      // 16-byte weight units per stage
+  static constexpr int WPU = 2 * RS + 1;          // LDS pitch per output channel (odd: conflict-free)
   static constexpr int WITER = (WUNITS + 255) / 256;
   static constexpr int XITER = XI;                // x items per thread per stage (8 dwords each)
 };
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   const int o0 = blockIdx.y * BM;
   const int Wp = a.Wp;
   const int cells = a.rows_max * Wp;       // cells per half-plane
-  const int w_units = 2 * RS * BM;         // uint4 per weight stage
+  const int w_units = BM * Cfg::WPU;       // 16-byte units per weight stage
   const int stage = w_units + 2 * cells;   // uint4 per stage
   // stage st: weights at lds + st*stage, x halo right after them
 #define WSM(st) (lds + (st) * stage)
@@ -122,6 +124,30 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   const int x_items = 2 * rows * W2;
   const long RSC = (long)RS * a.C;
 
+  // x load items (fixed for the whole block; only the channel group moves):
+  // item -> (half, ext row e, column pair wi).  x_voff is the byte offset of the
+  // item's first element at channel 0 (+8 channels for the upper half), or an
+  // offset past the end of the buffer for rows outside the image.
+  const int HW2 = HW * 2;  // bytes per channel plane
+  const __amdgpu_buffer_rsrc_t xrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  int x_voff[Cfg::XITER], x_loff[Cfg::XITER];
+#pragma unroll
+  for (int it = 0; it < Cfg::XITER; ++it) {
+    int i = tid + it * 256;
+    int voff = (int)0x80000000u, loff = -1;
+    if (i < x_items) {
+      int wi = i % W2, t = i / W2;
+      int e = t % rows, half = t / rows;
+      int eg = e_start + e;
+      int n = eg / a.Hp, h = eg - n * a.Hp - a.ph;
+      if (h >= 0 && h < a.H && n < a.N) voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + 2 * wi) * 2);
+      loff = half * cells + e * Wp + a.pw + 2 * wi;
+    }
+    x_voff[it] = voff;
+    x_loff[it] = loff;
+  }
+
   u32x4 wreg[Cfg::WITER];
   uint32_t xreg[Cfg::XITER][8];
 
@@ -133,26 +159,15 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
         int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
         int og = o0 + o;
         wreg[it] = og < a.O ? *reinterpret_cast<const u32x4*>(a.wt + og * RSC + (long)tap * a.C + c0 + half * 8) : z;
+        (void)og;
       }
     }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
-      int i = tid + it * 256;
-      if (i < x_items) {
-        int wi = i % W2, t = i / W2;
-        int e = t % rows, half = t / rows;
-        int eg = e_start + e;
-        int n = eg / a.Hp, h = eg - n * a.Hp - a.ph;
-        if (h >= 0 && h < a.H && n < a.N) {
-          const uint32_t* src = reinterpret_cast<const uint32_t*>(
-              a.x + ((long)n * a.C + c0 + half * 8) * HW + (long)h * a.W + 2 * wi);
+      // invalid items carry an out-of-range offset: the buffer load returns 0
 #pragma unroll
-          for (int j = 0; j < 8; ++j) xreg[it][j] = src[(long)j * (HW >> 1)];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 8; ++j) xreg[it][j] = 0u;
-        }
-      }
+      for (int j = 0; j < 8; ++j)
+        xreg[it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
     }
   };
   auto sstore = [&](int st) {
@@ -160,22 +175,19 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
     for (int it = 0; it < Cfg::WITER; ++it) {
       int u = tid + it * 256;
       if (u < Cfg::WUNITS) {
-        int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
-        WSM(st)[(half * RS + tap) * BM + o] = wreg[it];
+        int o = u / (RS * 2), rem = u % (RS * 2);
+        WSM(st)[o * Cfg::WPU + rem] = wreg[it];
       }
     }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
-      int i = tid + it * 256;
-      if (i < x_items) {
-        int wi = i % W2, t = i / W2;
-        int e = t % rows, half = t / rows;
+      if (x_loff[it] >= 0) {
         u32x4 c0v, c1v;
         c0v.x = pack_lo(xreg[it][0], xreg[it][1]); c0v.y = pack_lo(xreg[it][2], xreg[it][3]);
         c0v.z = pack_lo(xreg[it][4], xreg[it][5]); c0v.w = pack_lo(xreg[it][6], xreg[it][7]);
         c1v.x = pack_hi(xreg[it][0], xreg[it][1]); c1v.y = pack_hi(xreg[it][2], xreg[it][3]);
         c1v.z = pack_hi(xreg[it][4], xreg[it][5]); c1v.w = pack_hi(xreg[it][6], xreg[it][7]);
-        u32x4* base = XSM(st) + half * cells + e * Wp + a.pw + 2 * wi;
+        u32x4* base = XSM(st) + x_loff[it];
         base[0] = c0v;
         base[1] = c1v;
       }
@@ -198,7 +210,7 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & 1;
     if (kt + 1 < nk) gload((kt + 1) * 16);
-    const u32x4* Wp_ = WSM(st) + half_l * RS * BM + wm + row_l;
+    const u32x4* Wp_ = WSM(st) + (wm + row_l) * Cfg::WPU + half_l;
     const u32x4* Xp_ = XSM(st) + half_l * cells;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
         bf16x8 af[FM], bfr[FN];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-          af[i] = __builtin_bit_cast(bf16x8, Wp_[tap * BM + i * 32]);
+          af[i] = __builtin_bit_cast(bf16x8, Wp_[i * 32 * Cfg::WPU + tap * 2]);
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
         if (o < a.O) {
           float val = acc[i][j][v];
           if (a.bias) val += bf16_to_f32(a.bias[o]);
-          yb[(long)o * PQ] = f32_to_bf16(val);
+          yb[(long)o * PQ] = __builtin_bit_cast(uint16_t, (__bf16)val);
         }
       }
   }
@@ -302,6 +314,9 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
   a.M = N * P * Q;
   a.fPQ = FastDiv((uint32_t)(P * Q));
   a.fQ = FastDiv((uint32_t)Q);
+  const long xb = (long)N * C * H * W * 2;
+  if (xb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;  // 32-bit buffer offsets
+  a.x_bytes = (int)xb;
   const int WM = O > 64 ? 2 : 1;
   const int BN = (4 / WM) * 64;
   const int BM = WM * 64;
@@ -314,7 +329,7 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
     rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
   }
   a.rows_max = rows_max;
-  const size_t stage = (size_t)(2 * R * S * BM + 2 * rows_max * a.Wp) * 16;
+  const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp) * 16;
   const size_t lds = 2 * stage;
   if (lds > 160 * 1024 || (2 * rows_max * (W / 2) + 255) / 256 > 8) return VH_ERR_UNSUPPORTED;
 #define VH_HALO(RR, SS)                                           \

@@ -208,7 +208,12 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     if (ks + 1 < nsteps) gload(step_b + ks + 1);
     const uint16_t* dl = DYS(st) + (wo + rl) * OS;
     const uint16_t* xl = XS(st) + (wc + rl) * CS;
-    int g = 0, k0 = grp * 8;  // this lane group's chunk: t = kk + grp
+    // this lane group's chunk t = kk + grp as (row g, column k0); rows hold QP/8 chunks
+    int g = 0, k0 = grp * 8;
+    if (k0 >= QP) {
+      k0 -= QP;
+      g = 1;
+    }
     for (int kk = 0; kk < nchunk; kk += 2) {
       const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4w*>(dl + g * QP + k0));
 #pragma unroll
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
         }
       }
       k0 += 16;
-      if (k0 >= QP) {
+      while (k0 >= QP) {  // QP = 8 advances two rows per 16 positions
         k0 -= QP;
         ++g;
       }
@@ -265,13 +270,20 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   }
 }
 
-// dW[o][c][tap] = sum_z part[z][tap][o][c]  (fixed order), bf16 out.
+// dW[o][c][tap] = sum_z part[z][tap][o][c], bf16 out.  16 lanes share one output
+// element: lane g adds the splits z = g, g+16, ... and the 16 partial sums are
+// combined in a fixed butterfly order, so the result does not depend on timing.
 __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __restrict__ part, int splits,
                                                                 int RS, int O, int C, uint16_t* __restrict__ dw) {
   const long total = (long)RS * O * C;
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += part[(long)z * total + i];
+  const int g = threadIdx.x & 15;
+  const long i = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
+  float s = 0.f;
+  if (i < total)
+    for (int z = g; z < splits; z += 16) s += part[(long)z * total + i];
+#pragma unroll
+  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  if (g == 0 && i < total) {
     int c = (int)(i % C);
     long t = i / C;
     int o = (int)(t % O);
@@ -322,12 +334,12 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
     if (((a.G * a.QP / 8) & 1) != 0) a.QP += 8;
   }
   a.XP = std::max(a.QP + 16, (W + 2 * pw + 7) / 8 * 8);
-  // LDS row strides: 16-byte aligned, and not a multiple of 128 bytes so that the
-  // 32 rows read by one fragment spread over the banks
+  // LDS row strides: an ODD number of 16-byte units, so the 16 lanes that one
+  // LDS cycle serves (16 rows, 16 bytes each) land on 16 distinct bank groups
   a.OS = a.G * a.QP;
-  if ((a.OS * 2) % 128 == 0) a.OS += 8;
+  if (((a.OS / 8) & 1) == 0) a.OS += 8;
   a.CS = (a.G + R - 1) * a.XP;
-  if ((a.CS * 2) % 128 == 0) a.CS += 8;
+  if (((a.CS / 8) & 1) == 0) a.CS += 8;
   const size_t stage = (size_t)(64 * a.OS + 64 * a.CS) * 2;
   pl.lds = 2 * stage;
   if (pl.lds > 160 * 1024) return false;
@@ -395,8 +407,7 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   int rc = pl.a.V == 8 ? launch_v<8>(pl, st) : pl.a.V == 4 ? launch_v<4>(pl, st) : launch_v<2>(pl, st);
   if (rc) return rc;
   const long total = (long)R * S * O * C;
-  wgrad_reduce_bf16_kernel<<<(int)std::min<long>((total + 255) / 256, 2048), 256, 0, st>>>(
-      ws, pl.splits, R * S, O, C, (uint16_t*)dw);
+  wgrad_reduce_bf16_kernel<<<(int)((total + 15) / 16), 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw);
   VH_LAUNCH_CHECK();
   if (db) {
     bias_reduce_bf16_kernel<<<(O + 255) / 256, 256, 0, st>>>(pl.a.dbias_part, pl.splits, O, (uint16_t*)db);
