@@ -36,7 +36,9 @@ struct HaloArgs {
   int M;                 // N*P*Q
   int rows_max;          // max ext rows any block needs
   int x_bytes;           // size of x in bytes (< 2^31: buffer-load range)
+  int y_bytes;           // size of y in bytes (< 2^31)
   FastDiv fPQ, fQ;
+  FastDiv fW2, fRowsMax, fHp;  // item decomposition (W/2, rows_max, Hp)
 };
 
 template <int R, int S, int WM, int XI>
@@ -134,20 +136,24 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   int x_voff[Cfg::XITER], x_loff[Cfg::XITER];
 #pragma unroll
   for (int it = 0; it < Cfg::XITER; ++it) {
-    int i = tid + it * 256;
+    // item -> (half, e, wi) over a rows_max-row grid; rows e >= rows are skipped
+    uint32_t i = (uint32_t)(tid + it * 256);
+    uint32_t wi, t, e, half;
+    a.fW2.divmod(i, t, wi);
+    a.fRowsMax.divmod(t, half, e);
     int voff = (int)0x80000000u, loff = -1;
-    if (i < x_items) {
-      int wi = i % W2, t = i / W2;
-      int e = t % rows, half = t / rows;
-      int eg = e_start + e;
-      int n = eg / a.Hp, h = eg - n * a.Hp - a.ph;
-      if (h >= 0 && h < a.H && n < a.N) voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + 2 * wi) * 2);
-      loff = half * cells + e * Wp + a.pw + 2 * wi;
+    if (half < 2u && (int)e < rows) {
+      uint32_t eg = (uint32_t)(e_start + (int)e), n, hr;
+      a.fHp.divmod(eg, n, hr);
+      int h = (int)hr - a.ph;
+      if (h >= 0 && h < a.H) voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + 2 * wi) * 2);
+      loff = (int)half * cells + (int)e * Wp + a.pw + 2 * (int)wi;
     }
     x_voff[it] = voff;
     x_loff[it] = loff;
   }
 
+  const bool full_o = o0 + BM <= a.O;  // uniform: no per-row checks needed
   u32x4 wreg[Cfg::WITER];
   uint32_t xreg[Cfg::XITER][8];
 
@@ -158,8 +164,10 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
       if (u < Cfg::WUNITS) {
         int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
         int og = o0 + o;
-        wreg[it] = og < a.O ? *reinterpret_cast<const u32x4*>(a.wt + og * RSC + (long)tap * a.C + c0 + half * 8) : z;
-        (void)og;
+        if (full_o || og < a.O)
+          wreg[it] = *reinterpret_cast<const u32x4*>(a.wt + og * RSC + (long)tap * a.C + c0 + half * 8);
+        else
+          wreg[it] = z;
       }
     }
 #pragma unroll
@@ -241,25 +249,52 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
 #undef WSM
 #undef XSM
   // epilogue: rows = o (acc_row), cols = positions (lane & 31); fp32 bias add,
-  // one rounding to bf16, NCHW store (lanes walk consecutive q).
-  const long PQ = (long)a.P * a.Q;
+  // one rounding to bf16, NCHW store (lanes walk consecutive q).  Buffer stores:
+  // the per-lane offset is the position (plus 4 rows for the upper half-wave),
+  // the output-channel row is a scalar offset; positions past the end carry an
+  // out-of-range offset and their stores are dropped.
+  const int PQ = a.P * a.Q;
+  const int PQ2 = PQ * 2;
+  const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.y, (short)0, a.y_bytes, 0x00020000);
+  int yoff[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    int m = m0 + wn + j * 32 + (lane & 31);
-    if (m >= a.M) continue;
-    uint32_t n, pq;
-    a.fPQ.divmod((uint32_t)m, n, pq);
-    uint16_t* yb = a.y + (long)n * a.O * PQ + pq;
+    uint32_t m = (uint32_t)(m0 + wn + j * 32 + (lane & 31)), n, pq;
+    a.fPQ.divmod(m, n, pq);
+    yoff[j] = (int)m < a.M ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + pq) * 2u) + (lane >> 5) * 4 * PQ2
+                           : (int)0x80000000u;
+  }
+  float bv[FM][16];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+      bv[i][v] = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
+    }
+  if (full_o) {
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (o < a.O) {
-          float val = acc[i][j][v];
-          if (a.bias) val += bf16_to_f32(a.bias[o]);
-          yb[(long)o * PQ] = __builtin_bit_cast(uint16_t, (__bf16)val);
-        }
+        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);  // wave-uniform part of o
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][v] + bv[i][v])),
+                                                yrsrc, yoff[j], orow * PQ2, 0);
+      }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);
+        const bool ok = orow + (lane >> 5) * 4 < a.O;
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          if (ok)
+            __builtin_amdgcn_raw_buffer_store_b16(
+                __builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][v] + bv[i][v])), yrsrc, yoff[j], orow * PQ2, 0);
       }
   }
 }
@@ -317,6 +352,11 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
   const long xb = (long)N * C * H * W * 2;
   if (xb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   a.x_bytes = (int)xb;
+  const long yb_ = (long)N * O * P * Q * 2;
+  if (yb_ >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
+  a.y_bytes = (int)yb_;
+  a.fW2 = FastDiv((uint32_t)(W / 2));
+  a.fHp = FastDiv((uint32_t)a.Hp);
   const int WM = O > 64 ? 2 : 1;
   const int BN = (4 / WM) * 64;
   const int BM = WM * 64;
@@ -329,6 +369,7 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
     rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
   }
   a.rows_max = rows_max;
+  a.fRowsMax = FastDiv((uint32_t)rows_max);
   const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp) * 16;
   const size_t lds = 2 * stage;
   if (lds > 160 * 1024 || (2 * rows_max * (W / 2) + 255) / 256 > 8) return VH_ERR_UNSUPPORTED;

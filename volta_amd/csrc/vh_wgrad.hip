@@ -43,6 +43,24 @@ struct WgradArgs {
   int steps_per_split;
   int V;               // elements per global load (8, 4 or 2): divides Q, W and the row pitch
   int cpr_dy, cpr_x;   // chunks of V elements per dY row / per x row
+  int dy_bytes, x_bytes, part_bytes;  // buffer ranges (< 2^31)
+};
+
+template <int V> struct BufLoad;
+template <> struct BufLoad<8> {
+  __device__ static u32x4w ld(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x4w, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+  }
+};
+template <> struct BufLoad<4> {
+  __device__ static u32x2w ld(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_bit_cast(u32x2w, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
+  }
+};
+template <> struct BufLoad<2> {
+  __device__ static uint32_t ld(__amdgpu_buffer_rsrc_t r, int vo, int so) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
+  }
 };
 
 __device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
@@ -140,7 +158,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     int ch = i % a.cpr_dy, t = i / a.cpr_dy, g = t % G, o = t / G;
     bool ok = i < dy_items && o0 + o < a.O;
     dy_g[it] = ok ? g : 1 << 20;  // invalid items never load
-    dy_goff[it] = ok ? (int)((o0 + o) * PQ) + g * a.Q + ch * V : 0;
+    dy_goff[it] = ok ? (int)(((o0 + o) * PQ + g * a.Q + ch * V) * 2) : 0;
     dy_loff[it] = i < dy_items ? o * OS + g * QP + ch * V : -1;
   }
 #pragma unroll
@@ -149,30 +167,31 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     int ch = i % a.cpr_x, t = i / a.cpr_x, j = t % XR, c = t / XR;
     bool ok = i < x_items && c0 + c < a.C;
     x_j[it] = ok ? j : 1 << 20;
-    x_goff[it] = ok ? (int)((c0 + c) * HW) + j * a.W + ch * V : 0;
+    x_goff[it] = ok ? (int)(((c0 + c) * HW + j * a.W + ch * V) * 2) : 0;
     x_loff[it] = i < x_items ? c * CS + j * XP + a.pw + ch * V : -1;
   }
   const int x_mode = (a.pw % V) == 0 ? 0 : (a.pw % 2) == 0 ? 1 : 2;
+  const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
   VT rdy[ND], rx[NX];
   auto gload = [&](int step) {
     const int n = step / a.steps_per_img;
     const int p0 = (step - n * a.steps_per_img) * G;
-    const uint16_t* dyb = a.dy + (long)n * a.O * PQ + (long)p0 * a.Q;
-    const uint16_t* xb = a.x + (long)n * a.C * HW + (long)(p0 - a.ph) * a.W;
-    const int gmax = a.P - p0;           // rows g < gmax exist
+    // scalar byte offsets of this step's image / first row; per-item parts are in VGPRs
+    const int dys = (int)(((long)n * a.O * PQ + (long)p0 * a.Q) * 2);
+    const int xso = (int)(((long)n * a.C * HW + (long)(p0 - a.ph) * a.W) * 2);
+    const int gmax = a.P - p0;                           // rows g < gmax exist
     const int jmin = a.ph - p0, jmax = a.H + a.ph - p0;  // rows j in [jmin, jmax) exist
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      VT v = VT{};
-      if (dy_g[it] < gmax) v = *reinterpret_cast<const VT*>(dyb + dy_goff[it]);
-      rdy[it] = v;
+      const bool ok = dy_g[it] < gmax;
+      rdy[it] = BufLoad<V>::ld(dyr, ok ? dy_goff[it] + dys : (int)0x80000000u, 0);
     }
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      VT v = VT{};
-      if (x_j[it] >= jmin && x_j[it] < jmax) v = *reinterpret_cast<const VT*>(xb + x_goff[it]);
-      rx[it] = v;
+      const bool ok = x_j[it] >= jmin && x_j[it] < jmax;
+      rx[it] = BufLoad<V>::ld(xrr, ok ? x_goff[it] + xso : (int)0x80000000u, 0);
     }
   };
   auto sstore = [&](int st) {
@@ -252,15 +271,24 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #undef DYS
 #undef XS
 
-  // partial tile store: part[split][tap][o][c], lanes walk c
+  // partial tile store: part[split][tap][o][c], lanes walk c.  Per-lane offset:
+  // column c and the half-wave's 4-row shift; scalar offset: (split, tap, row).
+  {
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.part, (short)0, a.part_bytes, 0x00020000);
+    const int c = c0 + wc + rl;
+    const int ohalf = (lane >> 5) * 4;
+    const int voff = c < a.C ? (ohalf * a.C + c) * 4 : (int)0x80000000u;
 #pragma unroll
-  for (int t = 0; t < RS; ++t)
+    for (int t = 0; t < RS; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      int o = o0 + wo + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      int c = c0 + wc + rl;
-      if (o < a.O && c < a.C) a.part[(((long)split * RS + t) * a.O + o) * a.C + c] = acc[t][v];
-    }
+      for (int v = 0; v < 16; ++v) {
+        const int orow = o0 + wo + (v >> 2) * 8 + (v & 3);
+        if (orow + ohalf < a.O)
+          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[t][v]), pr, voff,
+                                                (((split * RS + t) * a.O) + orow) * a.C * 4, 0);
+      }
+  }
   if (do_bias) {
     // combine the 4 quarter sums of each o (adjacent lanes)
     dbias += __shfl_xor(dbias, 1, 64);
@@ -399,6 +427,14 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return VH_ERR_UNSUPPORTED;
   const size_t need = wgrad_rows_ws(N, C, H, W, O, R, S, ph, pw, db != nullptr);
   if (need > ws_bytes) return set_error(VH_ERR_BAD_ARG, "wgrad workspace too small");
+  {
+    const long dyb = (long)N * O * pl.a.P * pl.a.Q * 2, xb = (long)N * C * H * W * 2;
+    const long pb = (long)pl.splits * R * S * O * C * 4;
+    if (dyb >= (1L << 31) - 16 || xb >= (1L << 31) - 16 || pb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
+    pl.a.dy_bytes = (int)dyb;
+    pl.a.x_bytes = (int)xb;
+    pl.a.part_bytes = (int)pb;
+  }
   pl.a.dy = (const uint16_t*)dy;
   pl.a.x = (const uint16_t*)x;
   pl.a.part = ws;
