@@ -68,7 +68,8 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   extern __shared__ __attribute__((aligned(16))) u32x4 lds[];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wm = (wave / Cfg::WN) * FM * 32;  // wave's first output channel in the tile
   const int wn = (wave % Cfg::WN) * FN * 32;  // wave's first position in the tile
 

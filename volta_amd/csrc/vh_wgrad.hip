@@ -128,7 +128,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   constexpr int TO = 64, TC = 64;  // block tile (o, c)
   using VT = typename VecT<V>::t;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wo = (wave >> 1) * 32, wc = (wave & 1) * 32;
   const int o0 = blockIdx.x * TO, c0 = blockIdx.y * TC;
   const int split = blockIdx.z;
@@ -285,8 +286,11 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
       for (int v = 0; v < 16; ++v) {
         const int orow = o0 + wo + (v >> 2) * 8 + (v & 3);
         if (orow + ohalf < a.O)
-          __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, acc[t][v]), pr, voff,
+        {
+          const float val = acc[t][v];  // (a bit_cast of the vector element itself reads element 0)
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), pr, voff,
                                                 (((split * RS + t) * a.O) + orow) * a.C * 4, 0);
+        }
       }
   }
   if (do_bias) {
