@@ -237,6 +237,9 @@ HALO_CASES = [
     (2, 16, 16, 8, 8, 3, 1, 2),      # even padding wider than 1 (P = H + 2)
     (4, 64, 96, 12, 12, 3, 1, 1),    # O and C not multiples of the 64-wide tiles
     (2, 128, 64, 9, 9, 3, 1, 1),     # odd image size (W odd: generic fallback)
+    (2, 64, 128, 56, 56, 1, 2, 0),   # config 3 projection: subsampled 1x1 path
+    (3, 32, 48, 13, 11, 1, 2, 0),    # strided 1x1, odd sizes (scatter edges)
+    (2, 16, 32, 12, 12, 1, 3, 0),    # stride 3
 ]
 
 
