@@ -170,25 +170,13 @@ static ConvGeom geom_of(const ConvDims& d) {
   ((dtype) == VH_BF16 ? FN<bf16>(__VA_ARGS__) : FN<float>(__VA_ARGS__))
 
 // ------------------------------------------------------------------ conv passes
-// A 1x1, pad-0 convolution with stride s reads only the input positions
-// (p*s, q*s).  In bf16 such layers run as stride-1 1x1 convolutions on the
-// subsampled input (one HBM pass builds it), the input gradient as a stride-1
-// 1x1 convolution of dY scattered back with zeros in between, and the weight
-// gradient as a dense GEMM over the (subsampled) channel planes.
-static bool is_1x1_p0(const ConvDims& d) { return d.KH == 1 && d.KW == 1 && d.PH == 0 && d.PW == 0; }
-
-// Forward pass.  bf16 stride-1 layers (and strided 1x1 ones, see above) use the
-// halo kernel (vh_halo.hip); everything else the generic implicit GEMM: rows =
-// output channels (A = weight in [O][kh][kw][C] order), columns = output
-// positions (B = im2col gather of x).
+// Forward pass as implicit GEMM: rows = output channels (A = weight in
+// [O][kh][kw][C] order), columns = output positions (B = im2col gather of x).
 static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, void* y, const ConvDims& d,
                      hipStream_t st) {
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   const size_t wbytes = (size_t)d.O * d.C * RS * elem_size(dt);
-  const bool fast = dt == VH_BF16 && g_fast_paths;
-  const bool s1 = d.SH == 1 && d.SW == 1;
-  const bool sub = fast && !s1 && is_1x1_p0(d);
   IgemmPlan p{};
   p.dtype = dt;
   p.akind = KD_DENSE_K;
@@ -207,23 +195,13 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   size_t ws_gemm = igemm_prepare(p);
   Carve cv;
   size_t o_w = cv.take(wbytes), o_g = cv.take(ws_gemm);
-  size_t o_xs = sub ? cv.take((size_t)d.B * d.C * d.HO * d.WO * 2) : 0;
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wt = at(ws, o_w);
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wt, (int)d.O, (int)d.C, (int)RS, 0, st));
-  if (fast && (s1 || sub)) {
-    const void* xin = x;
-    long H = d.H, W = d.W;
-    if (sub) {
-      VH_TRY(run_subsample<bf16>(x, at(ws, o_xs), (int)(d.B * d.C), (int)d.H, (int)d.W, (int)d.HO, (int)d.WO,
-                                 (int)d.SH, (int)d.SW, st));
-      xin = at(ws, o_xs);
-      H = d.HO;
-      W = d.WO;
-    }
-    int r = halo_conv_bf16(xin, wt, bias, y, (int)d.B, (int)d.C, (int)H, (int)W, (int)d.O, (int)d.KH, (int)d.KW,
-                           sub ? 0 : (int)d.PH, sub ? 0 : (int)d.PW, st);
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
+    int r = halo_conv_bf16(x, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
+                           (int)d.KW, (int)d.PH, (int)d.PW, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   const int vec = dt == VH_BF16 ? 8 : 4;
@@ -232,18 +210,12 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
-// Input gradient.  bf16 stride-1 layers: dX = conv(dY, W rotated 180 degrees
-// with O and C swapped, pad K-1-p) on the halo kernel; strided 1x1 layers: the
-// same on the compact grid, then a zero-filling scatter.  Otherwise the generic
-// implicit GEMM: rows = input channels (A = weight in [C][kh][kw][O] order),
-// columns = input positions (B = gather of dY).
+// Input gradient as implicit GEMM: rows = input channels (A = weight in
+// [C][kh][kw][O] order), columns = input positions (B = gather of dY).
 static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st) {
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   const size_t wbytes = (size_t)d.O * d.C * RS * elem_size(dt);
-  const bool fast = dt == VH_BF16 && g_fast_paths;
-  const bool s1 = d.SH == 1 && d.SW == 1 && d.PH <= d.KH - 1 && d.PW <= d.KW - 1;
-  const bool sub = fast && (d.SH != 1 || d.SW != 1) && is_1x1_p0(d);
   IgemmPlan p{};
   p.dtype = dt;
   p.akind = KD_DENSE_K;
@@ -260,18 +232,14 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   size_t ws_gemm = igemm_prepare(p);
   Carve cv;
   size_t o_w = cv.take(wbytes), o_g = cv.take(ws_gemm);
-  size_t o_dxs = sub ? cv.take((size_t)d.B * d.C * d.HO * d.WO * 2) : 0;
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wd = at(ws, o_w);
-  if (fast && (s1 || sub)) {
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && d.PH <= d.KH - 1 && d.PW <= d.KW - 1 && g_fast_paths) {
+    // stride 1: dX = conv(dY, W rotated 180 degrees with O and C swapped), pad K-1-p
     VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 1));
-    void* out = sub ? at(ws, o_dxs) : dx;
-    int r = halo_conv_bf16(dy, wd, nullptr, out, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C, (int)d.KH,
-                           (int)d.KW, sub ? 0 : (int)(d.KH - 1 - d.PH), sub ? 0 : (int)(d.KW - 1 - d.PW), st);
-    if (r == VH_OK && sub)
-      r = run_upsample_scatter<bf16>(out, dx, (int)(d.B * d.C), (int)d.H, (int)d.W, (int)d.HO, (int)d.WO,
-                                     (int)d.SH, (int)d.SW, st);
+    int r = halo_conv_bf16(dy, wd, nullptr, dx, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C, (int)d.KH,
+                           (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
@@ -305,37 +273,6 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
-  if (dt == VH_BF16 && g_fast_paths && is_1x1_p0(d)) {
-    // dW[o][c] = sum over (n, p, q) of dY[n][o][p][q] * xs[n][c][p][q]: both
-    // operands are channel-major planes read with 16-byte loads
-    const bool sub = d.SH != 1 || d.SW != 1;
-    IgemmPlan p{};
-    p.dtype = dt;
-    p.akind = KD_CONV_WGRAD_DY;
-    p.bkind = KD_CONV_WGRAD_DY;
-    p.okind = OK_DENSE;
-    p.args.M = (int)d.O;
-    p.args.N = (int)d.C;
-    p.args.K = (int)(d.B * d.HO * d.WO);
-    p.args.g = g;
-    p.args.ldd = (int)d.C;
-    p.args.d = dw;
-    p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
-    size_t ws_gemm = igemm_prepare(p);
-    Carve cv;
-    size_t o_g = cv.take(ws_gemm), o_xs = sub ? cv.take((size_t)d.B * d.C * d.HO * d.WO * 2) : 0;
-    void* ws;
-    VH_TRY(ws_get(st, cv.off, &ws));
-    const void* xin = x;
-    if (sub) {
-      VH_TRY(run_subsample<bf16>(x, at(ws, o_xs), (int)(d.B * d.C), (int)d.H, (int)d.W, (int)d.HO, (int)d.WO,
-                                 (int)d.SH, (int)d.SW, st));
-      xin = at(ws, o_xs);
-    }
-    p.args.a = Operand{dy, (int)d.O, (int)d.O, aligned16(dy)};
-    p.args.b = Operand{xin, (int)d.C, (int)d.C, aligned16(xin)};
-    return run_igemm(p, (float*)at(ws, o_g), st);
-  }
   IgemmPlan p{};
   p.dtype = dt;
   p.akind = KD_CONV_WGRAD_DY;

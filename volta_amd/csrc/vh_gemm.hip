@@ -86,7 +86,6 @@ int launch_typed(IgemmPlan& p, float* ws, hipStream_t st) {
   VH_COMBO(KD_DENSE_K, KD_DENSE_K, OK_NCHW)              // im2col conv fwd
   VH_COMBO(KD_DENSE_MN, KD_CONV_FWD_X, OK_DENSE_T)       // im2col conv dcol
   VH_COMBO(KD_CONV_WGRAD_DY, KD_DENSE_MN, OK_DENSE)      // im2col conv dW
-  VH_COMBO(KD_CONV_WGRAD_DY, KD_CONV_WGRAD_DY, OK_DENSE) // 1x1 conv dW over channel-major planes
 #undef VH_COMBO
   return set_error(VH_ERR_BAD_ARG, "unsupported implicit-GEMM operand combination %d/%d/%d", p.akind,
                    p.bkind, p.okind);

@@ -22,7 +22,7 @@ enum OpndKind : int {
   KD_DENSE_MN = 1,      // elem(r,k) = p[k*ld + r]
   KD_CONV_FWD_X = 2,    // r = out position (n,p,q); k = (kh,kw,c): x[n][c][p*sh+kh-ph][q*sw+kw-pw]
   KD_CONV_DGRAD_DY = 3, // r = in position (n,h,w); k = (kh,kw,o): dy[n][o][(h+ph-kh)/sh][(w+pw-kw)/sw]
-  KD_CONV_WGRAD_DY = 4, // r = o; k = out position (n,p,q): dy[n][o][p][q] (o range = ld if ld > 0)
+  KD_CONV_WGRAD_DY = 4, // r = o; k = out position (n,p,q): dy[n][o][p][q]
   KD_CONV_WGRAD_X = 5,  // r = (kh,kw,c); k = out position (n,p,q): x[n][c][p*sh+kh-ph][q*sw+kw-pw]
 };
 
@@ -98,7 +98,6 @@ struct Loader {
       s2 = (int)n * g.O * g.P * g.Q;
     } else if (KIND == KD_CONV_WGRAD_DY) {
       s0 = r * g.P * g.Q;
-      s1 = op.ld > 0 ? op.ld : g.O;  // channels of this [N][channels][P*Q] operand
     } else if (KIND == KD_CONV_WGRAD_X) {
       uint32_t rs, c, kh, kw;
       g.fC.divmod((uint32_t)r, rs, c);
@@ -190,7 +189,7 @@ struct Loader {
       const int PQ = g.P * g.Q;
       uint32_t n, pq;
       g.fPQ.divmod((uint32_t)k0, n, pq);
-      const S* src = base + (int)n * s1 * PQ + s0 + (int)pq;
+      const S* src = base + (int)n * g.O * PQ + s0 + (int)pq;
       if ((PQ % VEC) == 0 && op.vec_ok && k0 + VEC <= K) {
         *reinterpret_cast<uint4*>(out) = *reinterpret_cast<const uint4*>(src);
       } else {
@@ -203,7 +202,7 @@ struct Loader {
           ++src;
           if ((int)pq == PQ) {  // next image: skip the other channels
             pq = 0;
-            src += (s1 - 1) * PQ;
+            src += (g.O - 1) * PQ;
           }
         }
       }

@@ -267,57 +267,6 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
   }
 }
 
-// ============================================================== strided 1x1 support
-// xs[b][c][p][q] = x[b][c][p*sh][q*sw]  (the input a 1x1, pad-0, stride-s conv
-// actually reads), and the adjoint: dx[b][c][h][w] = dxs[b][c][h/sh][w/sw] where
-// both divide, else 0.
-template <typename T>
-__global__ __launch_bounds__(256) void subsample_kernel(const typename Elem<T>::storage* __restrict__ x,
-                                                        typename Elem<T>::storage* __restrict__ xs, int H, int W,
-                                                        int P, int Q, int sh, int sw, long total) {
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    int q = (int)(i % Q);
-    long t = i / Q;
-    int p = (int)(t % P);
-    long bc = t / P;
-    xs[i] = x[(bc * H + (long)p * sh) * W + (long)q * sw];
-  }
-}
-
-template <typename T>
-__global__ __launch_bounds__(256) void upsample_scatter_kernel(const typename Elem<T>::storage* __restrict__ dxs,
-                                                               typename Elem<T>::storage* __restrict__ dx, int H,
-                                                               int W, int P, int Q, int sh, int sw, long total) {
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    int w = (int)(i % W);
-    long t = i / W;
-    int h = (int)(t % H);
-    long bc = t / H;
-    typename Elem<T>::storage v = 0;
-    if (h % sh == 0 && w % sw == 0 && h / sh < P && w / sw < Q) v = dxs[(bc * P + h / sh) * Q + w / sw];
-    dx[i] = v;
-  }
-}
-
-template <typename T>
-int run_subsample(const void* x, void* xs, int BC, int H, int W, int P, int Q, int sh, int sw, hipStream_t st) {
-  using S = typename Elem<T>::storage;
-  long total = (long)BC * P * Q;
-  subsample_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (S*)xs, H, W, P, Q, sh, sw, total);
-  VH_LAUNCH_CHECK();
-  return VH_OK;
-}
-
-template <typename T>
-int run_upsample_scatter(const void* dxs, void* dx, int BC, int H, int W, int P, int Q, int sh, int sw,
-                         hipStream_t st) {
-  using S = typename Elem<T>::storage;
-  long total = (long)BC * H * W;
-  upsample_scatter_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)dxs, (S*)dx, H, W, P, Q, sh, sw, total);
-  VH_LAUNCH_CHECK();
-  return VH_OK;
-}
-
 // ============================================================== weight re-layouts
 // src viewed as [A][B][RS]; dst[a][rs'][b] (swap = 0) or dst[b][rs'][a] (swap = 1)
 // with rs' = rs, or rs' = RS-1-rs (flip = 1: the 180-degree kernel rotation that
@@ -563,9 +512,7 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
   template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t, int);               \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
-  template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);         \
-  template int run_subsample<T>(const void*, void*, int, int, int, int, int, int, int, hipStream_t);       \
-  template int run_upsample_scatter<T>(const void*, void*, int, int, int, int, int, int, int, hipStream_t);
+  template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);
 VH_INST(float)
 VH_INST(bf16)
 #undef VH_INST

@@ -51,11 +51,6 @@ size_t column_sum_ws(int M, int N, int* nslice, int* rows_per);
 template <typename T>
 int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st);
 template <typename T>
-int run_subsample(const void* x, void* xs, int BC, int H, int W, int P, int Q, int sh, int sw, hipStream_t st);
-template <typename T>
-int run_upsample_scatter(const void* dxs, void* dx, int BC, int H, int W, int P, int Q, int sh, int sw,
-                         hipStream_t st);
-template <typename T>
 int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
 
 // ---- stride-1 bf16 halo convolution (vh_halo.hip) ----
