@@ -95,6 +95,54 @@ def run_step(layers, timers=None):
             t["wgrad"][1].record()
 
 
+def gemm_secondary(torch, vnn, dev, reps=5):
+    """Linear 4096x1024 -> 4096 fwd + dX + dW (+ bias) in f32 and bf16, and the
+    8192^3 bf16 product; reported beside the headline (same HIP-event timing)."""
+    out = {}
+    g = torch.Generator().manual_seed(1)
+    for dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        lin = vnn.Linear(1024, 4096, device=dev, dtype=dt, generator=g)
+        x = torch.randn((4096, 1024), generator=g).to(dev, dt)
+        dy = torch.randn((4096, 4096), generator=g).to(dev, dt)
+        y = torch.empty((4096, 4096), device=dev, dtype=dt)
+        outs = (torch.empty_like(x), torch.empty_like(lin.weight), torch.empty_like(lin.bias))
+
+        def step():
+            lin.forward(x, out=y)
+            lin.backward(dy, x, outs=outs)
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        fl = 3 * 2.0 * 4096 * 1024 * 4096
+        out[f"linear_4096x1024x4096_fwd_bwd_{name}_tflops"] = round(fl / ms / 1e9, 2)
+    import volta_amd
+    from volta_amd import ops
+    a = torch.randn((8192, 8192), generator=g).to(dev, torch.bfloat16)
+    b = torch.randn((8192, 8192), generator=g).to(dev, torch.bfloat16)
+    c = torch.empty_like(a)
+    st = torch.cuda.current_stream().cuda_stream
+    lib = volta_amd.lib()
+    for _ in range(2):
+        volta_amd.check(lib.vh_matmul(volta_amd.BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), 8192, 8192, 8192, st))
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        volta_amd.check(lib.vh_matmul(volta_amd.BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), 8192, 8192, 8192, st))
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    out["matmul_8192cubed_bf16_tflops"] = round(2.0 * 8192 ** 3 / ms / 1e9, 2)
+    return out
+
+
 def cpu_baseline(sample_budget_s=20.0):
     """Time the oracle's restatement of Volta's CPU Direct loops (what Volta's
     CPU auto-select picks for every C3 layer, conv.rs:55-57) on a sample of
@@ -112,17 +160,18 @@ def cpu_baseline(sample_budget_s=20.0):
     used = 0.0
     for name, C, O, H, K, S, P in C3_LAYERS:
         HO = conv_out(H, K, S, P)
-        # forward (conv.rs:1359-1419): one image, extrapolated x N
-        x = rng.standard_normal((1, C, H, H)).astype(np.float32)
+        # forward (conv.rs:1359-1419): NS images, extrapolated x N/NS
+        NS = 2
+        x = rng.standard_normal((NS, C, H, H)).astype(np.float32)
         w = rng.standard_normal((O, C, K, K)).astype(np.float32)
         t0 = time.perf_counter()
         oracle.direct_conv(x, w, (S, S), (P, P))
-        tf = (time.perf_counter() - t0) * C3_BATCH
-        # weight grad (conv.rs:544-606): one image, x N
-        dy = rng.standard_normal((1, O, HO, HO)).astype(np.float32)
+        tf = (time.perf_counter() - t0) * C3_BATCH / NS
+        # weight grad (conv.rs:544-606): NS images, x N/NS
+        dy = rng.standard_normal((NS, O, HO, HO)).astype(np.float32)
         t0 = time.perf_counter()
         oracle.direct_conv_backward_weight(dy, x, w.shape, (S, S), (P, P))
-        tw = (time.perf_counter() - t0) * C3_BATCH
+        tw = (time.perf_counter() - t0) * C3_BATCH / NS
         # input grad, literal O(B*C*H*W*O*HO*WO) scan (conv.rs:450-515): run it on
         # a 4-row strip of one input channel of one image, take the cost per
         # (input element x output position) iteration, scale to the full scan
@@ -139,14 +188,14 @@ def cpu_baseline(sample_budget_s=20.0):
         t1 = time.perf_counter() - t0
         per_iter = t1 / (rows * H * O * HO_s * HO)
         td = per_iter * C3_BATCH * C * H * H * O * HO * HO
-        used += tf / C3_BATCH + tw / C3_BATCH + t1
+        used += (tf + tw) * NS / C3_BATCH + t1
         detail.append((name, tf, td, tw))
         total_s += tf + td + tw
     flops = sum(2.0 * C3_BATCH * O * C * K * K * conv_out(H, K, S, P) ** 2 * 3 for _, C, O, H, K, S, P in C3_LAYERS)
     return dict(value=flops / total_s / 1e12, unit="TFLOP/s", cores=1, kind="port",
-                sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on 1 of "
-                        "128 images, literal dX scan on 1 row of 1 input channel; extrapolated linearly to the full "
-                        f"step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
+                sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on 2 of "
+                        "128 images, literal dX scan on a 4-row strip of 1 input channel; extrapolated linearly to "
+                        f"the full step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
                 seconds_per_step_extrapolated=total_s)
 
 
@@ -205,6 +254,8 @@ def main():
     roof["kernel"] = f"{dom['layer']} {dom['op']}"
     roof["launch_ms"] = round(dom["ms"], 4)
 
+    secondary = gemm_secondary(torch, vnn, dev)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline()
@@ -229,6 +280,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
+        "secondary": secondary,
     }
     print(json.dumps(out), flush=True)
 
