@@ -143,7 +143,7 @@ def gemm_secondary(torch, vnn, dev, reps=5):
     return out
 
 
-def cpu_baseline(sample_budget_s=20.0):
+def cpu_baseline(images=32, strip_rows=8):
     """Time the oracle's restatement of Volta's CPU Direct loops (what Volta's
     CPU auto-select picks for every C3 layer, conv.rs:55-57) on a sample of
     each loop nest's outer iterations and extrapolate to the full step."""
@@ -161,7 +161,7 @@ def cpu_baseline(sample_budget_s=20.0):
     for name, C, O, H, K, S, P in C3_LAYERS:
         HO = conv_out(H, K, S, P)
         # forward (conv.rs:1359-1419): NS images, extrapolated x N/NS
-        NS = 2
+        NS = images
         x = rng.standard_normal((NS, C, H, H)).astype(np.float32)
         w = rng.standard_normal((O, C, K, K)).astype(np.float32)
         t0 = time.perf_counter()
@@ -175,7 +175,7 @@ def cpu_baseline(sample_budget_s=20.0):
         # input grad, literal O(B*C*H*W*O*HO*WO) scan (conv.rs:450-515): run it on
         # a 4-row strip of one input channel of one image, take the cost per
         # (input element x output position) iteration, scale to the full scan
-        rows = 4
+        rows = strip_rows
         HO_s = conv_out(rows, K, S, P)
         ws = np.ascontiguousarray(w[:, :1])
         dys = np.ascontiguousarray(dy[:, :, :HO_s, :])
@@ -193,9 +193,9 @@ def cpu_baseline(sample_budget_s=20.0):
         total_s += tf + td + tw
     flops = sum(2.0 * C3_BATCH * O * C * K * K * conv_out(H, K, S, P) ** 2 * 3 for _, C, O, H, K, S, P in C3_LAYERS)
     return dict(value=flops / total_s / 1e12, unit="TFLOP/s", cores=1, kind="port",
-                sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on 2 of "
-                        "128 images, literal dX scan on a 4-row strip of 1 input channel; extrapolated linearly to "
-                        f"the full step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
+                sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on "
+                        f"{images} of 128 images, literal dX scan on a {strip_rows}-row strip of 1 input channel of "
+                        f"1 image; extrapolated linearly to the full step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
                 seconds_per_step_extrapolated=total_s)
 
 
