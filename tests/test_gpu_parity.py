@@ -143,6 +143,7 @@ CONV_CASES = [
     (1, 3, 64, 32, 32, 5, 1, 2),     # config 5 conv1 shape, smaller image
     (2, 8, 4, 9, 9, 4, 2, 1),
     (3, 5, 7, 6, 5, 2, 3, 0),
+    (1, 2, 3, 12, 12, 9, 1, 4),      # 81-tap window (element-wise weight relayout)
 ]
 
 
@@ -240,6 +241,8 @@ HALO_CASES = [
     (2, 64, 128, 56, 56, 1, 2, 0),   # config 3 projection: subsampled 1x1 path
     (3, 32, 48, 13, 11, 1, 2, 0),    # strided 1x1, odd sizes (scatter edges)
     (2, 16, 32, 12, 12, 1, 3, 0),    # stride 3
+    (3, 48, 80, 16, 16, 1, 2, 0),    # strided 1x1: O, C not tile multiples
+    (2, 32, 64, 15, 16, 1, 2, 0),    # strided 1x1: odd H (last cell row clipped)
 ]
 
 

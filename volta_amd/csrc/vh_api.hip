@@ -170,10 +170,19 @@ static ConvGeom geom_of(const ConvDims& d) {
   ((dtype) == VH_BF16 ? FN<bf16>(__VA_ARGS__) : FN<float>(__VA_ARGS__))
 
 // ------------------------------------------------------------------ conv passes
+// 1x1 kernel, no padding, equal strides >= 2 (the ResNet projection shortcut).
+static bool is_strided_pointwise(const ConvDims& d) {
+  return d.KH == 1 && d.KW == 1 && d.PH == 0 && d.PW == 0 && d.SH == d.SW && d.SH >= 2;
+}
+
 // Forward pass as implicit GEMM: rows = output channels (A = weight in
 // [O][kh][kw][C] order), columns = output positions (B = im2col gather of x).
 static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, void* y, const ConvDims& d,
                      hipStream_t st) {
+  if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths) {
+    int r = pw_conv_bf16_fwd(x, w, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   const size_t wbytes = (size_t)d.O * d.C * RS * elem_size(dt);
@@ -243,6 +252,10 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
+  if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths && ((uintptr_t)dx & 3) == 0) {
+    int r = pw_conv_bf16_dgrad(dy, wd, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wd, (int)(RS * d.O), (int)d.C, ((RS * d.O) % vec) == 0};
   p.args.b = Operand{dy, 0, p.args.N, 0};
@@ -269,6 +282,16 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
         if (r == VH_OK && db_done) *db_done = db != nullptr;
         return r;
       }
+    }
+  }
+  if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths) {
+    size_t need = pw_conv_bf16_wgrad_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH);
+    if (need) {
+      void* ws;
+      VH_TRY(ws_get(st, need, &ws));
+      int r = pw_conv_bf16_wgrad(dy, x, dw, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH,
+                                 (float*)ws, need, st);
+      if (r != VH_ERR_UNSUPPORTED) return r;
     }
   }
   ConvGeom g = geom_of(d);

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "../../include/volta_hip.h"
 
 namespace vh {
@@ -70,6 +72,32 @@ struct FastDiv {
     r = n - q * d;
   }
 };
+
+// Deterministic reduction of split-K partial sums part[z][i] (z < splits,
+// i < total) by a 256-thread block: 64 consecutive outputs per pass, wave w
+// adds z = w, w+4, w+8, ... in order and the four wave sums are added in wave
+// order.  Every load of a wave covers 64 consecutive floats of one slab.
+// store(i, sum) writes the result.
+template <typename Store>
+__device__ __forceinline__ void reduce_splits_block(const float* __restrict__ part, int splits, long total,
+                                                    Store store) {
+  __shared__ float red[4][64];
+  const int j = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (long base = (long)blockIdx.x * 64; base < total; base += (long)gridDim.x * 64) {
+    const long i = base + j;
+    float s = 0.f;
+    if (i < total) {
+#pragma unroll 4
+      for (int z = w; z < splits; z += 4) s += part[(size_t)z * total + i];
+    }
+    red[w][j] = s;
+    __syncthreads();
+    if (w == 0 && i < total) store(i, ((red[0][j] + red[1][j]) + red[2][j]) + red[3][j]);
+    __syncthreads();
+  }
+}
+
+inline int reduce_splits_grid(long total) { return (int)std::min<long>((total + 63) / 64, 1L << 20); }
 
 // Record an error message for vh_last_error(); returns the status.
 int set_error(int status, const char* fmt, ...);

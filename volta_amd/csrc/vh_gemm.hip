@@ -53,9 +53,7 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
     pa.d = ws;
     igemm_kernel<T, AK, BKIND, OK_PARTIAL, BM, BN, BK><<<grid, 256, 0, st>>>(pa);
     VH_LAUNCH_CHECK();
-    long total = (long)a.M * a.N;
-    int g = (int)std::min<long>((total + 15) / 16, 65535L * 4);
-    splitk_reduce_kernel<T, OUT><<<g, 256, 0, st>>>(a, ws, p.splits);
+    splitk_reduce_kernel<T, OUT><<<reduce_splits_grid((long)a.M * a.N), 256, 0, st>>>(a, ws, p.splits);
     VH_LAUNCH_CHECK();
   } else {
     igemm_kernel<T, AK, BKIND, OUT, BM, BN, BK><<<grid, 256, 0, st>>>(a);

@@ -123,8 +123,6 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   }
 
   const int HW = a.H * a.W;
-  const int W2 = a.W >> 1;
-  const int x_items = 2 * rows * W2;
   const long RSC = (long)RS * a.C;
 
   // x load items (fixed for the whole block; only the channel group moves):
@@ -358,22 +356,30 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
   a.y_bytes = (int)yb_;
   a.fW2 = FastDiv((uint32_t)(W / 2));
   a.fHp = FastDiv((uint32_t)a.Hp);
-  const int WM = O > 64 ? 2 : 1;
-  const int BN = (4 / WM) * 64;
-  const int BM = WM * 64;
-  // exact maximum number of ext rows over all blocks
+  // 64 output channels x 256 positions per block (two blocks per CU fit in
+  // LDS for the config-3 layers); 128 x 128 only when the wider tile does not fit.
+  int WM = 1;
   int rows_max = 0;
-  for (int m0 = 0; m0 < a.M; m0 += BN) {
-    int ml = std::min(m0 + BN, a.M) - 1;
-    int na = m0 / (P * Q), pa = (m0 % (P * Q)) / Q;
-    int nb = ml / (P * Q), pb = (ml % (P * Q)) / Q;
-    rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
+  size_t lds = 0;
+  for (;; WM = 2) {
+    const int BN = (4 / WM) * 64;
+    const int BM = WM * 64;
+    // exact maximum number of ext rows over all blocks
+    rows_max = 0;
+    for (int m0 = 0; m0 < a.M; m0 += BN) {
+      int ml = std::min(m0 + BN, a.M) - 1;
+      int na = m0 / (P * Q), pa = (m0 % (P * Q)) / Q;
+      int nb = ml / (P * Q), pb = (ml % (P * Q)) / Q;
+      rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
+    }
+    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp) * 16;
+    lds = 2 * stage;
+    const bool fits = lds <= 160 * 1024 && (2 * rows_max * (W / 2) + 255) / 256 <= 8;
+    if (fits) break;
+    if (WM == 2 || O <= 64) return VH_ERR_UNSUPPORTED;
   }
   a.rows_max = rows_max;
   a.fRowsMax = FastDiv((uint32_t)rows_max);
-  const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp) * 16;
-  const size_t lds = 2 * stage;
-  if (lds > 160 * 1024 || (2 * rows_max * (W / 2) + 255) / 256 > 8) return VH_ERR_UNSUPPORTED;
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
     return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \

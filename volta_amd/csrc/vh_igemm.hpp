@@ -410,22 +410,14 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
                           n0 + wn + j * MM::TN + MM::acc_col(lane), acc[i][j][v]);
 }
 
-// Split-K reduction: out(row, col) = bias + sum_z ws[z][row][col], stored by OUT.
-// 16 lanes share one output element (lane g adds z = g, g+16, ...) and their
-// partial sums are combined in a fixed butterfly order: deterministic results.
+// Split-K reduction: out(row, col) = sum_z ws[z][row][col] (+ bias), stored by
+// OUT; fixed summation order (reduce_splits_block).
 template <typename T, int OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(IgemmArgs args, const float* ws, int splits) {
   const long total = (long)args.M * args.N;
-  const int g = threadIdx.x & 15;
-  for (long i = (long)blockIdx.x * 16 + (threadIdx.x >> 4); i - (threadIdx.x >> 4) < total;
-       i += (long)gridDim.x * 16) {
-    float s = 0.f;
-    if (i < total)
-      for (int z = g; z < splits; z += 16) s += ws[(long)z * total + i];
-#pragma unroll
-    for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (g == 0 && i < total) store_out<T, OUT>(args, (int)(i / args.N), (int)(i % args.N), s);
-  }
+  reduce_splits_block(ws, splits, total, [&](long i, float s) {
+    store_out<T, OUT>(args, (int)(i / args.N), (int)(i % args.N), s);
+  });
 }
 
 }  // namespace vh

@@ -271,19 +271,61 @@ __global__ __launch_bounds__(256) void col2im_t_kernel(const float* __restrict__
 // src viewed as [A][B][RS]; dst[a][rs'][b] (swap = 0) or dst[b][rs'][a] (swap = 1)
 // with rs' = rs, or rs' = RS-1-rs (flip = 1: the 180-degree kernel rotation that
 // turns a stride-1 input gradient into a forward convolution).
-template <typename T>
+//
+// Both are batched transposes through an LDS tile: batch t holds a source
+// matrix [R1][R2] and dst[t][j][i] = src[t][i][colmap(j)], where colmap keeps
+// groups of RS columns together and flips inside a group.  swap = 0: batch a,
+// R1 = B, R2 = RS; swap = 1: one batch, R1 = A, R2 = B*RS.  Loads walk source
+// rows, stores walk destination rows (both coalesced); a tile holds whole
+// column groups (TJ <= 64 is a multiple of RS), so colmap never leaves the tile.
+template <int TI, typename T>
 __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::storage* __restrict__ src,
-                                                       typename Elem<T>::storage* __restrict__ dst, int A, int B,
-                                                       int RS, int swap, int flip) {
-  long total = (long)A * B * RS;
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
-    int rs = (int)(i % RS);
-    long t = i / RS;
-    int b = (int)(t % B);
-    int a = (int)(t / B);
-    int rd = flip ? RS - 1 - rs : rs;
-    long d = swap ? ((long)b * RS + rd) * A + a : ((long)a * RS + rd) * B + b;
-    dst[d] = src[i];
+                                                       typename Elem<T>::storage* __restrict__ dst, int R1, int R2,
+                                                       int RS, int flip, int TJ) {
+  using S = typename Elem<T>::storage;
+  __shared__ S tile[TI][65];
+  const size_t bofs = (size_t)blockIdx.z * R1 * R2;
+  const int j0 = blockIdx.x * TJ, i0 = blockIdx.y * TI;
+  // every thread issues all of its loads before the first LDS store
+  constexpr int NE = TI * 64 / 256;
+  S v[NE];
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = threadIdx.x + k * 256;
+    const int i = e / TJ, jj = e - i * TJ;
+    v[k] = (e < TI * TJ && i0 + i < R1 && j0 + jj < R2) ? src[bofs + (size_t)(i0 + i) * R2 + j0 + jj] : S{};
+  }
+#pragma unroll
+  for (int k = 0; k < NE; ++k) {
+    const int e = threadIdx.x + k * 256;
+    const int i = e / TJ, jj = e - i * TJ;
+    if (e < TI * TJ) tile[i][jj] = v[k];
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < TI * TJ; e += 256) {
+    const int jj = e / TI, i = e - jj * TI;
+    const int j = j0 + jj;
+    if (i0 + i < R1 && j < R2) {
+      const int g = jj / RS, r = jj - g * RS;
+      dst[bofs + (size_t)j * R1 + i0 + i] = tile[i][g * RS + (flip ? RS - 1 - r : r)];
+    }
+  }
+}
+
+// Element-wise form of the same map for windows of more than 64 taps.
+template <typename T>
+__global__ __launch_bounds__(256) void relayout_simple_kernel(const typename Elem<T>::storage* __restrict__ src,
+                                                              typename Elem<T>::storage* __restrict__ dst, int A,
+                                                              int B, int RS, int swap, int flip, FastDiv fRS,
+                                                              FastDiv fInner) {
+  const uint32_t total = (uint32_t)A * B * RS;
+  for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < total; d += gridDim.x * 256u) {
+    uint32_t t, inner, outer, rd;
+    fInner.divmod(d, t, inner);  // inner = a (swap) or b
+    fRS.divmod(t, outer, rd);    // outer = b (swap) or a
+    const uint32_t rs = flip ? (uint32_t)RS - 1u - rd : rd;
+    const uint32_t s = swap ? (inner * (uint32_t)B + outer) * RS + rs : (outer * (uint32_t)B + inner) * RS + rs;
+    dst[d] = src[s];
   }
 }
 
@@ -445,7 +487,23 @@ int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH
 template <typename T>
 int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip) {
   using S = typename Elem<T>::storage;
-  relayout_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>((const S*)src, (S*)dst, A, B, RS, swap, flip);
+  if (RS > 64) {
+    relayout_simple_kernel<T><<<grid_for((long)A * B * RS), 256, 0, st>>>(
+        (const S*)src, (S*)dst, A, B, RS, swap, flip, FastDiv((uint32_t)RS), FastDiv((uint32_t)(swap ? A : B)));
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
+  const int R1 = swap ? A : B, R2 = swap ? B * RS : RS, batch = swap ? 1 : A;
+  const int TJ = std::min(R2, (64 / RS) * RS);
+  dim3 grid((unsigned)((R2 + TJ - 1) / TJ), (unsigned)((R1 + 15) / 16), (unsigned)batch);
+  if (grid.z > 65535u) return set_error(VH_ERR_UNSUPPORTED, "too many weight rows for the relayout");
+  if (R1 <= 16) {
+    relayout_kernel<16, T><<<grid, 256, 0, st>>>((const S*)src, (S*)dst, R1, R2, RS, flip, TJ);
+  } else {
+    // 32-row tiles: enough blocks for the single-batch (swap) form
+    grid.y = (unsigned)((R1 + 31) / 32);
+    relayout_kernel<32, T><<<grid, 256, 0, st>>>((const S*)src, (S*)dst, R1, R2, RS, flip, TJ);
+  }
   VH_LAUNCH_CHECK();
   return VH_OK;
 }

@@ -1,0 +1,463 @@
+// vh_pointwise.hip -- strided 1x1 convolutions (pad 0), bf16 storage, fp32
+// accumulation: the ResNet projection shortcut (1x1, stride 2).
+//
+// All three passes are GEMMs over output positions with a short contraction
+// (C or O channels, or the positions themselves for the weight gradient).
+// They are HBM-bound (about 21 FLOP per byte at the config-3 shape), so the
+// kernels read each operand once, straight from NCHW into MFMA fragments
+// (v_mfma_f32_32x32x16_bf16), with no LDS staging and no workspace besides
+// the weight-gradient partial sums:
+//
+//  forward   y[n,o,p,q]   = sum_c W[o,c] x[n,c,p*s,q*s]          (+ bias[o])
+//  dgrad     dx[n,c,h,w]  = sum_o W[o,c] dy[n,o,h/s,w/s]  if s | h and s | w, else 0
+//  wgrad     dW[o,c]      = sum_{n,p,q} dy[n,o,p,q] x[n,c,p*s,q*s]
+//
+// Fragment layout of the 32x32x16 MFMA: lane l supplies row / column (l & 31)
+// and contraction indices 8*(l >> 5) .. +7; the result element v of lane l is
+// row (v >> 2) * 8 + (l >> 5) * 4 + (v & 3), column (l & 31).
+#include <algorithm>
+
+#include "vh_common.hpp"
+#include "vh_kernels.hpp"
+
+namespace vh {
+
+typedef unsigned int u32x4p __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2p __attribute__((ext_vector_type(2)));
+
+namespace {
+
+constexpr int kOutOfRange = (int)0x80000000u;  // buffer offset past every range: loads 0, stores dropped
+
+struct PwArgs {
+  const void* x;      // [B][C][H][W]
+  const void* w;      // forward [O][C]; dgrad [C][O] (transposed copy)
+  const void* dy;     // [B][O][P][Q]
+  const uint16_t* bias;
+  void* out;          // forward y; dgrad dx
+  float* part;        // wgrad partial sums [blocks][O][C]
+  int B, C, H, W, O, P, Q, S;
+  int npos;           // B*P*Q
+  FastDiv fPQ, fQ;
+  int x_bytes, w_bytes, dy_bytes, out_bytes;
+  int quads_per_block;  // wgrad: stages (4 output rows) per block
+  FastDiv fPQ4;         // wgrad: P/4
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const uint16_t (&v)[8]) {
+  u32x4p u;
+  u[0] = v[0] | ((uint32_t)v[1] << 16);
+  u[1] = v[2] | ((uint32_t)v[3] << 16);
+  u[2] = v[4] | ((uint32_t)v[5] << 16);
+  u[3] = v[6] | ((uint32_t)v[7] << 16);
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// even bf16 elements of 8 consecutive ones (x at stride 2 along a row)
+__device__ __forceinline__ u32x2p evens(u32x4p v) {
+  u32x2p r;
+  r[0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);
+  return r;
+}
+
+// ------------------------------------------------------------------ forward
+// Block: 4 waves x 32 output positions; each wave computes MT*32 output
+// channels for its 32 positions.  B fragment: 8 channels of one position
+// (8 two-byte loads, channel planes apart); A fragment: 16 bytes of a weight row.
+template <int MT>
+__global__ __launch_bounds__(256) void pw_fwd_bf16_kernel(PwArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const uint32_t pos = ((uint32_t)blockIdx.x * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+  const int o0 = blockIdx.y * MT * 32;
+  const bool valid = pos < (uint32_t)a.npos;
+  uint32_t n, pq, p, q;
+  a.fPQ.divmod(valid ? pos : 0u, n, pq);
+  a.fQ.divmod(pq, p, q);
+  const int HW2 = a.H * a.W * 2;
+  const int xbase = (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + p * (uint32_t)(a.S * a.W) +
+                           q * (uint32_t)a.S) * 2u) + half * 8 * HW2;
+  int xo[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) xo[j] = valid ? xbase + j * HW2 : kOutOfRange;
+  int wo[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int o = o0 + mt * 32 + col;
+    wo[mt] = o < a.O ? (o * a.C + 8 * half) * 2 : kOutOfRange;
+  }
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+  for (int c0 = 0; c0 < a.C; c0 += 16) {
+    const int so = c0 * HW2;
+    uint16_t xv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xv[j] = __builtin_amdgcn_raw_buffer_load_b16(xr, xo[j], so, 0);
+    bf16x8 af[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      af[mt] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[mt], c0 * 2, 0));
+    const bf16x8 bf = pack8(xv);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
+  }
+
+  // epilogue: fp32 bias add, one rounding, NCHW store (lanes walk consecutive positions)
+  const int PQ = a.P * a.Q;
+  const int PQ2 = PQ * 2;
+  const __amdgpu_buffer_rsrc_t yr = rsrc(a.out, a.out_bytes);
+  const int yo = valid ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + pq) * 2u) + half * 4 * PQ2 : kOutOfRange;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int orow = o0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+      const int o = orow + half * 4;
+      if (o < a.O) {
+        const float b = a.bias ? bf16_to_f32(a.bias[o]) : 0.f;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)(acc[mt][v] + b)), yr, yo,
+                                              orow * PQ2, 0);
+      }
+    }
+}
+
+// ------------------------------------------------------------------ input gradient
+// Same GEMM shape with rows = input channels (A = W^T [C][O]) and contraction
+// over output channels (B = 8 channels of dY at one position).  Each result
+// is written with the zeros of its s x s cell of dX, so dX is covered exactly
+// once (the cells tile [0,H) x [0,W) because (P-1)*s <= H-1 < P*s).
+template <int MT, bool S2>
+__global__ __launch_bounds__(256) void pw_dgrad_bf16_kernel(PwArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const uint32_t pos = ((uint32_t)blockIdx.x * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+  const int c0 = blockIdx.y * MT * 32;
+  const bool valid = pos < (uint32_t)a.npos;
+  uint32_t n, pq, p, q;
+  a.fPQ.divmod(valid ? pos : 0u, n, pq);
+  a.fQ.divmod(pq, p, q);
+  const int PQ2 = a.P * a.Q * 2;
+  const int dbase = (int)((n * (uint32_t)a.O * (uint32_t)(a.P * a.Q) + pq) * 2u) + half * 8 * PQ2;
+  int dyo[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dyo[j] = valid ? dbase + j * PQ2 : kOutOfRange;
+  int wo[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int c = c0 + mt * 32 + col;
+    wo[mt] = c < a.C ? (c * a.O + 8 * half) * 2 : kOutOfRange;
+  }
+  const __amdgpu_buffer_rsrc_t dr = rsrc(a.dy, a.dy_bytes);
+  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
+
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+  for (int k0 = 0; k0 < a.O; k0 += 16) {
+    const int so = k0 * PQ2;
+    uint16_t dv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dv[j] = __builtin_amdgcn_raw_buffer_load_b16(dr, dyo[j], so, 0);
+    bf16x8 af[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      af[mt] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[mt], k0 * 2, 0));
+    const bf16x8 bf = pack8(dv);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
+  }
+
+  const int HW2 = a.H * a.W * 2;
+  const int h0 = (int)p * a.S, w0 = (int)q * a.S;
+  const int xo = valid ? (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + (uint32_t)(h0 * a.W + w0)) * 2u) +
+                             half * 4 * HW2
+                       : kOutOfRange;
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.out, a.out_bytes);
+  if (S2) {
+    // s = 2, W even: (value, 0) as one 4-byte store on row h0, (0, 0) on row h0 + 1
+    const int xo1 = (valid && h0 + 1 < a.H) ? xo + a.W * 2 : kOutOfRange;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+        if (crow + half * 4 < a.C) {
+          const uint32_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
+          __builtin_amdgcn_raw_buffer_store_b32(val, xr, xo, crow * HW2, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(0u, xr, xo1, crow * HW2, 0);
+        }
+      }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+        if (crow + half * 4 < a.C) {
+          const uint16_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
+          for (int dh = 0; dh < a.S; ++dh)
+            for (int dw = 0; dw < a.S; ++dw) {
+              const bool in = valid && h0 + dh < a.H && w0 + dw < a.W;
+              __builtin_amdgcn_raw_buffer_store_b16((dh | dw) ? (uint16_t)0 : val, xr,
+                                                    in ? xo + (dh * a.W + dw) * 2 : kOutOfRange, crow * HW2, 0);
+            }
+        }
+      }
+  }
+}
+
+// ------------------------------------------------------------------ weight gradient
+// s = 2, W % 8 == 0, P % 4 == 0.  The contraction runs over output positions,
+// four output rows (4Q positions, never crossing an image) per stage.  A block
+// owns 128 output channels x 64 input channels and a range of stages; per
+// stage it copies into LDS
+//   dY rows  [o][4Q]   (one contiguous 8Q-byte run per o: 16-byte loads), and
+//   x rows   [c][4Q]   (the even elements of input rows 2p, 2p+2, ..: 16-byte
+//                       loads, 8 bytes kept),
+// both K-contiguous with an odd pitch in 16-byte units, so every MFMA fragment
+// is one ds_read_b128.  Wave w computes o0 + 32w .. +31 x the block's 64 c.
+// The next stage is loaded into registers while the current one is consumed.
+// Each block writes one fp32 partial tile [O][C]; a second kernel adds them.
+template <int IT>
+__global__ __launch_bounds__(256) void pw_wgrad_s2_bf16_kernel(PwArgs a) {
+  extern __shared__ __attribute__((aligned(16))) u32x4p lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int o0 = blockIdx.y * 128, c0 = blockIdx.z * 64;
+  const int Q = a.Q, PQ = a.P * a.Q, HW = a.H * a.W;
+  const int KU = Q / 2;                 // 16-byte units per LDS row (4Q elements)
+  const int PU = KU | 1;                // odd pitch
+  u32x4p* dys = lds;                    // [128][PU]
+  u32x4p* xs = lds + 128 * PU;          // [64][PU]
+
+  // load items, fixed for the block: dY item i -> (o = i / KU, unit u = i % KU);
+  // x item i -> (c = i / Q, row g = (i % Q) / (W/8), unit u), W/8 = Q/4 units per row
+  const int WU = Q / 4;
+  int dy_g[IT], dy_l[IT], x_g[IT], x_l[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int i = tid + it * 256;
+    const int o = i / KU, u = i % KU;
+    const bool ok = o < 128 && o0 + o < a.O;
+    dy_g[it] = ok ? ((o0 + o) * PQ * 2 + u * 16) : kOutOfRange;
+    dy_l[it] = o < 128 ? o * PU + u : -1;
+    const int c = i / Q, r = i % Q, g = r / WU, xu = r % WU;
+    const bool okx = c < 64 && c0 + c < a.C;
+    x_g[it] = okx ? ((c0 + c) * HW * 2 + g * 2 * a.W * 2 + xu * 16) : kOutOfRange;
+    x_l[it] = c < 64 ? c * PU * 2 + g * WU + xu : -1;  // in 8-byte units (4 positions each)
+  }
+  const __amdgpu_buffer_rsrc_t dr = rsrc(a.dy, a.dy_bytes);
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, a.x_bytes);
+
+  const int stages = a.B * a.P / 4;
+  const int s_begin = blockIdx.x * a.quads_per_block;
+  const int s_end = min(s_begin + a.quads_per_block, stages);
+
+  u32x4p rdy[IT], rx[IT];
+  auto gload = [&](int sidx) {
+    uint32_t n, p4;
+    a.fPQ4.divmod((uint32_t)sidx, n, p4);  // fPQ4 holds P/4 here
+    const int p0 = (int)p4 * 4;
+    const int dso = (int)((n * (uint32_t)a.O * (uint32_t)PQ + (uint32_t)(p0 * Q)) * 2u);
+    const int xso = (int)((n * (uint32_t)a.C * (uint32_t)HW + (uint32_t)(2 * p0 * a.W)) * 2u);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      rdy[it] = __builtin_bit_cast(u32x4p, __builtin_amdgcn_raw_buffer_load_b128(
+                                              dr, dy_g[it] == kOutOfRange ? kOutOfRange : dy_g[it] + dso, 0, 0));
+      rx[it] = __builtin_bit_cast(u32x4p, __builtin_amdgcn_raw_buffer_load_b128(
+                                             xr, x_g[it] == kOutOfRange ? kOutOfRange : x_g[it] + xso, 0, 0));
+    }
+  };
+  auto sstore = [&]() {
+    u32x2p* xs8 = reinterpret_cast<u32x2p*>(xs);
+#pragma unroll
+    for (int it = 0; it < IT; ++it) {
+      if (dy_l[it] >= 0) dys[dy_l[it]] = rdy[it];
+      if (x_l[it] >= 0) xs8[x_l[it]] = evens(rx[it]);
+    }
+  };
+
+  const int row = lane & 31, half = lane >> 5;
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  if (s_begin < s_end) gload(s_begin);
+  for (int sidx = s_begin; sidx < s_end; ++sidx) {
+    sstore();
+    __syncthreads();
+    if (sidx + 1 < s_end) gload(sidx + 1);
+    const u32x4p* ap = dys + (wave * 32 + row) * PU + half;
+    const u32x4p* bp = xs + row * PU + half;
+    for (int k = 0; k < KU; k += 2) {
+      const bf16x8 af = __builtin_bit_cast(bf16x8, ap[k]);
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, bp[k]);
+      const bf16x8 b1 = __builtin_bit_cast(bf16x8, bp[32 * PU + k]);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, b0, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, b1, acc[1], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // partial tile of this block: part[blockIdx.x][o][c]
+  float* part = a.part + (size_t)blockIdx.x * a.O * a.C;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int c = c0 + nt * 32 + row;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int o = o0 + wave * 32 + (v >> 2) * 8 + half * 4 + (v & 3);
+      if (o < a.O && c < a.C) part[(size_t)o * a.C + c] = acc[nt][v];
+    }
+  }
+}
+
+// dW[o][c] = sum over blocks z of part[z][o][c], fixed order
+__global__ __launch_bounds__(256) void pw_wgrad_reduce_kernel(const float* __restrict__ part, int splits,
+                                                              int total, uint16_t* __restrict__ dw) {
+  reduce_splits_block(part, splits, total, [&](long i, float s) { dw[i] = f32_to_bf16(s); });
+}
+
+bool fits_i32(long v) { return v > 0 && v < (1L << 31) - 16; }
+
+PwArgs base_args(int B, int C, int H, int W, int O, int S) {
+  PwArgs a{};
+  a.B = B;
+  a.C = C;
+  a.H = H;
+  a.W = W;
+  a.O = O;
+  a.S = S;
+  a.P = (H - 1) / S + 1;
+  a.Q = (W - 1) / S + 1;
+  a.npos = B * a.P * a.Q;
+  a.fPQ = FastDiv((uint32_t)(a.P * a.Q));
+  a.fQ = FastDiv((uint32_t)a.Q);
+  a.x_bytes = (int)((long)B * C * H * W * 2);
+  a.dy_bytes = (int)((long)B * O * a.P * a.Q * 2);
+  a.w_bytes = O * C * 2;
+  return a;
+}
+
+bool envelope(int B, int C, int H, int W, int O, int S) {
+  if (S < 2 || B <= 0 || C <= 0 || O <= 0 || H <= 0 || W <= 0) return false;
+  const long P = (H - 1) / S + 1, Q = (W - 1) / S + 1;
+  return fits_i32((long)B * C * H * W * 2) && fits_i32((long)B * O * P * Q * 2) && fits_i32((long)O * C * 2);
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ host entry points
+int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, int B, int C, int H, int W, int O,
+                     int S, hipStream_t st) {
+  if (!envelope(B, C, H, W, O, S) || C % 16 != 0) return VH_ERR_UNSUPPORTED;
+  PwArgs a = base_args(B, C, H, W, O, S);
+  a.x = x;
+  a.w = w;
+  a.bias = (const uint16_t*)bias;
+  a.out = y;
+  a.out_bytes = a.dy_bytes;
+  dim3 grid((a.npos + 127) / 128, (O + 127) / 128);
+  if (O <= 64) {
+    grid.y = (O + 63) / 64;
+    pw_fwd_bf16_kernel<2><<<grid, 256, 0, st>>>(a);
+  } else {
+    pw_fwd_bf16_kernel<4><<<grid, 256, 0, st>>>(a);
+  }
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, int H, int W, int O, int S,
+                       hipStream_t st) {
+  if (!envelope(B, C, H, W, O, S) || O % 16 != 0) return VH_ERR_UNSUPPORTED;
+  PwArgs a = base_args(B, C, H, W, O, S);
+  a.dy = dy;
+  a.w = wt;
+  a.out = dx;
+  a.out_bytes = a.x_bytes;
+  const bool s2 = S == 2 && W % 2 == 0;
+  dim3 grid((a.npos + 127) / 128, (C + 127) / 128);
+  if (C <= 64) {
+    grid.y = (C + 63) / 64;
+    if (s2) pw_dgrad_bf16_kernel<2, true><<<grid, 256, 0, st>>>(a);
+    else pw_dgrad_bf16_kernel<2, false><<<grid, 256, 0, st>>>(a);
+  } else {
+    if (s2) pw_dgrad_bf16_kernel<4, true><<<grid, 256, 0, st>>>(a);
+    else pw_dgrad_bf16_kernel<4, false><<<grid, 256, 0, st>>>(a);
+  }
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+static int pw_wgrad_plan(int B, int C, int H, int W, int O, int S, PwArgs* out) {
+  if (!envelope(B, C, H, W, O, S) || S != 2 || W % 8 != 0) return 0;
+  PwArgs a = base_args(B, C, H, W, O, S);
+  if (a.P % 4 != 0 || a.Q > 64) return 0;  // Q = W/2 is a multiple of 4
+  const int stages = B * a.P / 4;
+  const int tiles = ((O + 127) / 128) * ((C + 63) / 64);
+  // about 256 blocks in all, each walking a range of stages
+  const int blocks = std::max(1, 256 / tiles);
+  a.quads_per_block = std::max(1, (stages + blocks - 1) / blocks);  // stages per block
+  a.fPQ4 = FastDiv((uint32_t)(a.P / 4));
+  *out = a;
+  return (stages + a.quads_per_block - 1) / a.quads_per_block;
+}
+
+static size_t pw_wgrad_lds(int Q) { return (size_t)(128 + 64) * ((Q / 2) | 1) * 16; }
+
+size_t pw_conv_bf16_wgrad_ws(int B, int C, int H, int W, int O, int S) {
+  PwArgs a;
+  const int splits = pw_wgrad_plan(B, C, H, W, O, S, &a);
+  return splits ? (size_t)splits * O * C * sizeof(float) : 0;
+}
+
+template <int IT>
+static int launch_pw_wgrad(const PwArgs& a, dim3 grid, hipStream_t st) {
+  auto kern = pw_wgrad_s2_bf16_kernel<IT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    attr_set = true;
+  }
+  kern<<<grid, 256, pw_wgrad_lds(a.Q), st>>>(a);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+int pw_conv_bf16_wgrad(const void* dy, const void* x, void* dw, int B, int C, int H, int W, int O, int S,
+                       float* ws, size_t ws_bytes, hipStream_t st) {
+  PwArgs a;
+  const int splits = pw_wgrad_plan(B, C, H, W, O, S, &a);
+  if (!splits) return VH_ERR_UNSUPPORTED;
+  if (ws_bytes < (size_t)splits * O * C * sizeof(float))
+    return set_error(VH_ERR_BAD_ARG, "pointwise wgrad: workspace too small");
+  if (((uintptr_t)x & 15) || ((uintptr_t)dy & 15)) return VH_ERR_UNSUPPORTED;
+  a.dy = dy;
+  a.x = x;
+  a.part = ws;
+  dim3 grid(splits, (O + 127) / 128, (C + 63) / 64);
+  // load items per thread: 128 * Q/2 dY units and 64 * Q x units over 256 threads
+  const int it = (64 * a.Q + 255) / 256;
+  int r;
+  if (it <= 4) r = launch_pw_wgrad<4>(a, grid, st);
+  else if (it <= 8) r = launch_pw_wgrad<8>(a, grid, st);
+  else if (it <= 12) r = launch_pw_wgrad<12>(a, grid, st);
+  else r = launch_pw_wgrad<16>(a, grid, st);
+  if (r != VH_OK) return r;
+  const int total = O * C;
+  pw_wgrad_reduce_kernel<<<reduce_splits_grid(total), 256, 0, st>>>(ws, splits, total, (uint16_t*)dw);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+}  // namespace vh

@@ -1,25 +1,28 @@
-// vh_wgrad.hip -- bf16 weight gradient of stride-1 convolutions on NCHW
+// vh_wgrad.hip -- bf16 weight gradient of stride-1 3x3 convolutions on NCHW
 // tensors, gfx950 MFMA (v_mfma_f32_32x32x16_bf16).
 //
 //   dW[o][c][r][s] = sum_{n,p,q} dY[n][o][p][q] * x[n][c][p+r-ph][q+s-pw]
 //
-// GEMM view: rows = o, columns = (c, tap), K = output positions.  Both operands
-// are K-contiguous in NCHW memory (positions run along rows), so rows of dY and
-// x are copied to LDS as they are -- no transposition.  A K step covers G
-// output rows of one image; the block stages
-//   * dY rows  [64 o][G][QP]       (QP = Q rounded up to 8, zero padded), and
-//   * x rows   [64 c][G+R-1][XP]   (padded input columns u = w + pw),
-// and every lane reads 8 consecutive positions per fragment.  Tap (r, s) of the
-// x operand is row g+r, columns k+s..k+s+7: two aligned 16-byte reads and a
-// byte-align funnel shift give all S horizontal taps of one row r, so x is read
-// from LDS 2*R times per 16 positions instead of R*S times.
+// GEMM view: rows = o, columns = (c, tap), K = positions.  Both operands are
+// K-contiguous in NCHW memory (positions run along rows), so rows of dY and x
+// are copied to LDS as they are -- no transposition, aligned vector stores.
+// The K walk runs over the x columns v of G output rows: with q = v + pw - s,
+//   dW[o][c][r][s] = sum_{g,v} dY[o][g][v + pw - s] * x[c][g + r][v],
+// so one aligned 16-byte read of an x row serves all three s taps of a row r,
+// and the three dY windows (shifts pw - s = +1, 0, -1 for pw = 1) are built
+// from three aligned 16-byte reads of the dY row and a byte-align funnel shift.
+// dY rows sit in LDS with at least 8 zero elements between them (and before the
+// first), so windows that run past a row end read zeros.
 //
-// Each wave accumulates a 32(o) x 32(c) x R*S tile in AGPRs.  Split-K: the grid's
-// z dimension walks disjoint ranges of K steps; partial sums go to an fp32
-// workspace [split][tap][O][C] (lanes store consecutive c) and a second kernel
-// adds them in a fixed order and writes dW (OIHW).  Optional bias gradient
-// (sum of dY over positions) is accumulated by the c-tile-0 blocks from the
-// same LDS copy of dY.
+// A block stages, per K step,
+//   * dY rows [64 o][8 + G*DP]   (row g of o at 8 + g*DP, zero gaps), and
+//   * x rows  [64 c][(G+2)*XP]   (input rows p0-ph .. p0+G+1-ph, zero past W),
+// in two LDS buffers (loads for step k+1 are in flight while step k runs).
+// Each wave accumulates a 32(o) x 32(c) x 9-tap tile in AGPRs.  Split-K: the
+// grid's z dimension walks disjoint ranges of K steps; partial sums go to an
+// fp32 workspace [split][tap][O][C] and a second kernel adds them in a fixed
+// order and writes dW (OIHW).  The optional bias gradient (sum of dY over
+// positions) is accumulated by the c-tile-0 blocks from the same LDS copy of dY.
 #include <algorithm>
 
 #include "vh_kernels.hpp"
@@ -35,14 +38,18 @@ struct WgradArgs {
   float* part;         // [splits][RS][O][C]
   float* dbias_part;   // [splits][O] or nullptr
   int N, C, H, W, O, P, Q, ph, pw;
-  int G;               // output rows per K step
-  int QP, XP;          // padded row lengths in LDS (elements)
-  int OS, CS;          // LDS row strides per o / per c (elements)
-  int steps_per_img;   // ceil(P / G)
+  int G;               // output rows per K step (divides P)
+  int XV;              // x columns walked per row: W rounded up so G*XV/8 is even
+  int DP;              // LDS pitch of a dY row (elements): >= max(XV, Q) + 8
+  int XP;              // LDS pitch of an x row (elements): XV
+  int OS, CS;          // LDS strides per o / per c (elements)
+  int steps_per_img;   // P / G
   int total_steps;     // N * steps_per_img
   int steps_per_split;
-  int V;               // elements per global load (8, 4 or 2): divides Q, W and the row pitch
+  int V;               // elements per global load (8, 4 or 2): divides Q and W
   int cpr_dy, cpr_x;   // chunks of V elements per dY row / per x row
+  int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < Q
+  int xadv, xcadv;     // the same for x rows (columns < W)
   int dy_bytes, x_bytes, part_bytes;  // buffer ranges (< 2^31)
 };
 
@@ -63,67 +70,47 @@ template <> struct BufLoad<2> {
   }
 };
 
-__device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
-  // bytes 2..5 of (hi:lo): upper bf16 of lo, lower bf16 of hi
-  return __builtin_amdgcn_alignbyte(hi, lo, 2);
-}
-
-// 8 consecutive bf16 starting s elements into the 16-element window (c0, c1)
-template <int SH>
-__device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1) {
-  u32x4w r;
-  if constexpr (SH == 0) {
-    r = c0;
-  } else if constexpr (SH == 2) {
-    r = u32x4w{c0.y, c0.z, c0.w, c1.x};
-  } else if constexpr (SH == 4) {
-    r = u32x4w{c0.z, c0.w, c1.x, c1.y};
-  } else if constexpr (SH == 6) {
-    r = u32x4w{c0.w, c1.x, c1.y, c1.z};
-  } else if constexpr (SH == 8) {
-    r = c1;
-  } else if constexpr (SH == 1) {
-    r = u32x4w{funnel16(c0.x, c0.y), funnel16(c0.y, c0.z), funnel16(c0.z, c0.w), funnel16(c0.w, c1.x)};
-  } else if constexpr (SH == 3) {
-    r = u32x4w{funnel16(c0.y, c0.z), funnel16(c0.z, c0.w), funnel16(c0.w, c1.x), funnel16(c1.x, c1.y)};
-  } else if constexpr (SH == 5) {
-    r = u32x4w{funnel16(c0.z, c0.w), funnel16(c0.w, c1.x), funnel16(c1.x, c1.y), funnel16(c1.y, c1.z)};
-  } else {  // 7
-    r = u32x4w{funnel16(c0.w, c1.x), funnel16(c1.x, c1.y), funnel16(c1.y, c1.z), funnel16(c1.z, c1.w)};
-  }
-  return r;
-}
-
 template <int V>
 struct VecT;
 template <> struct VecT<8> { using t = u32x4w; };
 template <> struct VecT<4> { using t = u32x2w; };
 template <> struct VecT<2> { using t = uint32_t; };
 
-// Stores V bf16 elements at LDS element offset `off`.  mode 0: off is V-aligned
-// (one vector store); mode 1: off is even (dword stores); mode 2: off is odd
-// (the odd horizontal padding case: one element, shifted pairs, one element).
-template <int V>
-__device__ __forceinline__ void lds_put(uint16_t* base, int off, const typename VecT<V>::t& v, int mode) {
-  if (mode == 0) {
-    *reinterpret_cast<typename VecT<V>::t*>(base + off) = v;
-    return;
-  }
-  const uint32_t* d = reinterpret_cast<const uint32_t*>(&v);
-  if (mode == 1) {
-#pragma unroll
-    for (int i = 0; i < V / 2; ++i) *reinterpret_cast<uint32_t*>(base + off + 2 * i) = d[i];
-    return;
-  }
-  base[off] = (uint16_t)(d[0] & 0xffffu);
-#pragma unroll
-  for (int i = 0; i < V / 2 - 1; ++i)
-    *reinterpret_cast<uint32_t*>(base + off + 1 + 2 * i) = __builtin_amdgcn_alignbyte(d[i + 1], d[i], 2);
-  base[off + V - 1] = (uint16_t)(d[V / 2 - 1] >> 16);
+__device__ __forceinline__ uint32_t funnel16(uint32_t lo, uint32_t hi) {
+  // bytes 2..5 of (hi:lo): upper bf16 of lo, lower bf16 of hi
+  return __builtin_amdgcn_alignbyte(hi, lo, 2);
 }
 
-template <int R, int S, int V, int ND, int NX>
+// 8 consecutive bf16 starting SH elements into the 24-element window (c0, c1, c2)
+template <int SH>
+__device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, const u32x4w& c2) {
+  if constexpr (SH >= 8) {
+    return window8<SH - 8>(c1, c2, c2);
+  } else if constexpr (SH == 0) {
+    return c0;
+  } else if constexpr (SH == 2) {
+    return u32x4w{c0.y, c0.z, c0.w, c1.x};
+  } else if constexpr (SH == 4) {
+    return u32x4w{c0.z, c0.w, c1.x, c1.y};
+  } else if constexpr (SH == 6) {
+    return u32x4w{c0.w, c1.x, c1.y, c1.z};
+  } else if constexpr (SH == 1) {
+    return u32x4w{funnel16(c0.x, c0.y), funnel16(c0.y, c0.z), funnel16(c0.z, c0.w), funnel16(c0.w, c1.x)};
+  } else if constexpr (SH == 3) {
+    return u32x4w{funnel16(c0.y, c0.z), funnel16(c0.z, c0.w), funnel16(c0.w, c1.x), funnel16(c1.x, c1.y)};
+  } else if constexpr (SH == 5) {
+    return u32x4w{funnel16(c0.z, c0.w), funnel16(c0.w, c1.x), funnel16(c1.x, c1.y), funnel16(c1.y, c1.z)};
+  } else {  // 7
+    return u32x4w{funnel16(c0.w, c1.x), funnel16(c1.x, c1.y), funnel16(c1.y, c1.z), funnel16(c1.z, c1.w)};
+  }
+}
+
+// Load items: thread t serves row owner t/4 (an o of the dY tile, a c of the x
+// tile) and takes that owner's chunks t%4, t%4 + 4, ...; chunk k of a dY owner
+// is row k / cpr, column (k % cpr) * V.  Offsets advance incrementally.
+template <int R, int S, int PW, int V, int ND, int NX>
 __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
+  static_assert(R == 3 && S == 3, "3x3 windows");
   constexpr int RS = R * S;
   constexpr int TO = 64, TC = 64;  // block tile (o, c)
   using VT = typename VecT<V>::t;
@@ -133,7 +120,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int wo = (wave >> 1) * 32, wc = (wave & 1) * 32;
   const int o0 = blockIdx.x * TO, c0 = blockIdx.y * TC;
   const int split = blockIdx.z;
-  const int G = a.G, QP = a.QP, XP = a.XP, OS = a.OS, CS = a.CS;
+  const int G = a.G, DP = a.DP, XP = a.XP, OS = a.OS, CS = a.CS;
   const int XR = G + R - 1;
   const int dy_elems = TO * OS, x_elems = TC * CS;
   const int stage = dy_elems + x_elems;  // elements per stage
@@ -144,34 +131,23 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int step_e = min(a.total_steps, step_b + a.steps_per_split);
   const int nsteps = max(0, step_e - step_b);
 
-  // zero both stages once: padding columns/rows are never written by the loader
+  // zero both stages once: gaps and padding are never written by the loader
   for (int i = tid; i < 2 * stage / 8; i += 256) reinterpret_cast<u32x4w*>(smem)[i] = u32x4w{0u, 0u, 0u, 0u};
 
-  // Per-thread load items, fixed for the whole kernel: (row, chunk) of the dY
-  // tile and of the x tile.  Only the (image, first row) base moves per step.
-  const long PQ = (long)a.P * a.Q, HW = (long)a.H * a.W;
-  const int dy_items = TO * G * a.cpr_dy, x_items = TC * XR * a.cpr_x;
-  int dy_goff[ND], dy_loff[ND], dy_g[ND];
-  int x_goff[NX], x_loff[NX], x_j[NX];
-#pragma unroll
-  for (int it = 0; it < ND; ++it) {
-    int i = tid + it * 256;
-    int ch = i % a.cpr_dy, t = i / a.cpr_dy, g = t % G, o = t / G;
-    bool ok = i < dy_items && o0 + o < a.O;
-    dy_g[it] = ok ? g : 1 << 20;  // invalid items never load
-    dy_goff[it] = ok ? (int)(((o0 + o) * PQ + g * a.Q + ch * V) * 2) : 0;
-    dy_loff[it] = i < dy_items ? o * OS + g * QP + ch * V : -1;
-  }
-#pragma unroll
-  for (int it = 0; it < NX; ++it) {
-    int i = tid + it * 256;
-    int ch = i % a.cpr_x, t = i / a.cpr_x, j = t % XR, c = t / XR;
-    bool ok = i < x_items && c0 + c < a.C;
-    x_j[it] = ok ? j : 1 << 20;
-    x_goff[it] = ok ? (int)(((c0 + c) * HW + j * a.W + ch * V) * 2) : 0;
-    x_loff[it] = i < x_items ? c * CS + j * XP + a.pw + ch * V : -1;
-  }
-  const int x_mode = (a.pw % V) == 0 ? 0 : (a.pw % 2) == 0 ? 1 : 2;
+  const int PQ = a.P * a.Q, HW = a.H * a.W;
+  const int own = tid >> 2, sub = tid & 3;
+  // dY owner o = own: chunk k = sub + 4*it -> (row g, column) ; x owner c = own likewise
+  const bool dy_own_ok = o0 + own < a.O, x_own_ok = c0 + own < a.C;
+  const int dy_base_g = dy_own_ok ? (o0 + own) * PQ * 2 : 0;  // bytes, plane of o at image 0
+  const int x_base_g = x_own_ok ? (c0 + own) * HW * 2 : 0;
+  const int dy_chunks = G * a.cpr_dy, x_chunks = XR * a.cpr_x;
+  // item it of this thread is chunk sub + 4*it of its owner: (row, column) start
+  // at (g0, col0) and advance by 4V elements per item (a.dadv rows + a.cadv
+  // columns, with one carry); recomputed per step instead of kept in registers
+  int dg0 = 0, dc0 = sub * V;
+  while (dc0 >= a.Q) { dc0 -= a.Q; ++dg0; }
+  int xj0 = 0, xc0 = sub * V;
+  while (xc0 >= a.W) { xc0 -= a.W; ++xj0; }
   const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
@@ -179,31 +155,50 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   auto gload = [&](int step) {
     const int n = step / a.steps_per_img;
     const int p0 = (step - n * a.steps_per_img) * G;
-    // scalar byte offsets of this step's image / first row; per-item parts are in VGPRs
-    const int dys = (int)(((long)n * a.O * PQ + (long)p0 * a.Q) * 2);
-    const int xso = (int)(((long)n * a.C * HW + (long)(p0 - a.ph) * a.W) * 2);
-    const int gmax = a.P - p0;                           // rows g < gmax exist
-    const int jmin = a.ph - p0, jmax = a.H + a.ph - p0;  // rows j in [jmin, jmax) exist
+    // byte offsets of this step's image / first row (G divides P: all G dY rows exist)
+    const int dys = dy_base_g + (n * a.O * PQ + p0 * a.Q) * 2;
+    const int xso = x_base_g + (n * a.C * HW + (p0 - a.ph) * a.W) * 2;
+    const int jmin = a.ph - p0, jmax = a.H + a.ph - p0;  // x rows j in [jmin, jmax) exist
+    int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      const bool ok = dy_g[it] < gmax;
-      rdy[it] = BufLoad<V>::ld(dyr, ok ? dy_goff[it] + dys : (int)0x80000000u, 0);
+      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks;
+      rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + col) * 2 : (int)0x80000000u, 0);
+      g += a.dadv;
+      col += a.cadv;
+      if (col >= a.Q) { col -= a.Q; ++g; }
     }
+    int j = xj0;
+    col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      const bool ok = x_j[it] >= jmin && x_j[it] < jmax;
-      rx[it] = BufLoad<V>::ld(xrr, ok ? x_goff[it] + xso : (int)0x80000000u, 0);
+      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax;
+      rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + col) * 2 : (int)0x80000000u, 0);
+      j += a.xadv;
+      col += a.xcadv;
+      if (col >= a.W) { col -= a.W; ++j; }
     }
   };
   auto sstore = [&](int st) {
-    uint16_t* d = DYS(st);
-    uint16_t* xs = XS(st);
+    uint16_t* d = DYS(st) + own * OS + 8;
+    uint16_t* xs = XS(st) + own * CS;
+    int g = dg0, col = dc0;
 #pragma unroll
-    for (int it = 0; it < ND; ++it)
-      if (dy_loff[it] >= 0) *reinterpret_cast<VT*>(d + dy_loff[it]) = rdy[it];
+    for (int it = 0; it < ND; ++it) {
+      if (sub + 4 * it < dy_chunks) *reinterpret_cast<VT*>(d + g * DP + col) = rdy[it];
+      g += a.dadv;
+      col += a.cadv;
+      if (col >= a.Q) { col -= a.Q; ++g; }
+    }
+    int j = xj0;
+    col = xc0;
 #pragma unroll
-    for (int it = 0; it < NX; ++it)
-      if (x_loff[it] >= 0) lds_put<V>(xs, x_loff[it], rx[it], x_mode);
+    for (int it = 0; it < NX; ++it) {
+      if (sub + 4 * it < x_chunks) *reinterpret_cast<VT*>(xs + j * XP + col) = rx[it];
+      j += a.xadv;
+      col += a.xcadv;
+      if (col >= a.W) { col -= a.W; ++j; }
+    }
   };
 
   f32x16 acc[RS];
@@ -214,7 +209,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   float dbias = 0.f;
   const bool do_bias = a.dbias_part != nullptr && blockIdx.y == 0;
 
-  const int nchunk = G * (QP >> 3);  // even by construction
+  const int XV = a.XV;
+  const int nchunk = G * (XV >> 3);  // even by construction
   const int grp = lane >> 5, rl = lane & 31;
 
   __syncthreads();
@@ -226,44 +222,41 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   for (int ks = 0; ks < nsteps; ++ks) {
     const int st = ks & 1;
     if (ks + 1 < nsteps) gload(step_b + ks + 1);
-    const uint16_t* dl = DYS(st) + (wo + rl) * OS;
+    const uint16_t* dl = DYS(st) + (wo + rl) * OS + 8;
     const uint16_t* xl = XS(st) + (wc + rl) * CS;
-    // this lane group's chunk t = kk + grp as (row g, column k0); rows hold QP/8 chunks
-    int g = 0, k0 = grp * 8;
-    if (k0 >= QP) {
-      k0 -= QP;
-      g = 1;
+    // this lane group's chunk t = kk + grp as (row g, column v0)
+    int g = 0, v0 = grp * 8;
+    while (v0 >= XV) {
+      v0 -= XV;
+      ++g;
     }
     for (int kk = 0; kk < nchunk; kk += 2) {
-      const bf16x8 af = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4w*>(dl + g * QP + k0));
+      // dY windows for s = 0..2: start v0 + PW - s relative to the aligned chunk at v0
+      const uint16_t* dr = dl + g * DP + v0;
+      const u32x4w cm = *reinterpret_cast<const u32x4w*>(dr - 8);
+      const u32x4w cz = *reinterpret_cast<const u32x4w*>(dr);
+      const u32x4w cp = *reinterpret_cast<const u32x4w*>(dr + 8);
+      bf16x8 af[S];
+      af[0] = __builtin_bit_cast(bf16x8, window8<8 + PW>(cm, cz, cp));
+      af[1] = __builtin_bit_cast(bf16x8, window8<7 + PW>(cm, cz, cp));
+      af[2] = __builtin_bit_cast(bf16x8, window8<6 + PW>(cm, cz, cp));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const uint16_t* xr = xl + (g + r) * XP + k0;
-        const u32x4w c0v = *reinterpret_cast<const u32x4w*>(xr);
-        const u32x4w c1v = *reinterpret_cast<const u32x4w*>(xr + 8);
+        const bf16x8 bx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4w*>(xl + (g + r) * XP + v0));
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          u32x4w wv;
-          if (s == 0) wv = window8<0>(c0v, c1v);
-          else if (s == 1) wv = window8<1>(c0v, c1v);
-          else if (s == 2) wv = window8<2>(c0v, c1v);
-          else if (s == 3) wv = window8<3>(c0v, c1v);
-          else wv = window8<4>(c0v, c1v);
-          acc[r * S + s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, __builtin_bit_cast(bf16x8, wv),
-                                                                    acc[r * S + s], 0, 0, 0);
-        }
+        for (int s = 0; s < S; ++s)
+          acc[r * S + s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bx, acc[r * S + s], 0, 0, 0);
       }
-      k0 += 16;
-      while (k0 >= QP) {  // QP = 8 advances two rows per 16 positions
-        k0 -= QP;
+      v0 += 16;
+      while (v0 >= XV) {  // XV = 8 advances two rows per 16 positions
+        v0 -= XV;
         ++g;
       }
     }
     if (do_bias) {
-      // thread t sums quarter (t % 4) of dY row o = t / 4 of this stage
-      const int o = tid >> 2, part = tid & 3;
-      const uint16_t* drow = DYS(st) + o * OS;
-      const int len = G * QP, q4 = len >> 2, beg = part * q4, end = part == 3 ? len : beg + q4;
+      // thread t sums quarter (t % 4) of the dY rows of o = t / 4 (gaps are zero)
+      const uint16_t* drow = DYS(st) + own * OS;
+      const int q4 = OS >> 2, beg = sub * q4, end = sub == 3 ? OS : beg + q4;
       for (int k = beg; k < end; ++k) dbias += bf16_to_f32(drow[k]);
     }
     if (ks + 1 < nsteps) sstore(st ^ 1);
@@ -285,8 +278,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int orow = o0 + wo + (v >> 2) * 8 + (v & 3);
-        if (orow + ohalf < a.O)
-        {
+        if (orow + ohalf < a.O) {
           const float val = acc[t][v];  // (a bit_cast of the vector element itself reads element 0)
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), pr, voff,
                                                 (((split * RS + t) * a.O) + orow) * a.C * 4, 0);
@@ -297,31 +289,23 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     // combine the 4 quarter sums of each o (adjacent lanes)
     dbias += __shfl_xor(dbias, 1, 64);
     dbias += __shfl_xor(dbias, 2, 64);
-    const int o = o0 + (tid >> 2);
-    if ((tid & 3) == 0 && o < a.O) a.dbias_part[(long)split * a.O + o] = dbias;
+    const int o = o0 + own;
+    if (sub == 0 && o < a.O) a.dbias_part[(long)split * a.O + o] = dbias;
   }
 }
 
-// dW[o][c][tap] = sum_z part[z][tap][o][c], bf16 out.  16 lanes share one output
-// element: lane g adds the splits z = g, g+16, ... and the 16 partial sums are
-// combined in a fixed butterfly order, so the result does not depend on timing.
+// dW[o][c][tap] = sum_z part[z][tap][o][c], bf16 out, in a fixed summation
+// order (reduce_splits_block), so the result does not depend on timing.
 __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __restrict__ part, int splits,
                                                                 int RS, int O, int C, uint16_t* __restrict__ dw) {
-  const long total = (long)RS * O * C;
-  const int g = threadIdx.x & 15;
-  const long i = (long)blockIdx.x * 16 + (threadIdx.x >> 4);
-  float s = 0.f;
-  if (i < total)
-    for (int z = g; z < splits; z += 16) s += part[(long)z * total + i];
-#pragma unroll
-  for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-  if (g == 0 && i < total) {
-    int c = (int)(i % C);
-    long t = i / C;
-    int o = (int)(t % O);
-    int tap = (int)(t / O);
+  // partials are [split][tap][O][C]; dW is OIHW
+  reduce_splits_block(part, splits, (long)RS * O * C, [&](long i, float s) {
+    const int c = (int)(i % C);
+    const long t = i / C;
+    const int o = (int)(t % O);
+    const int tap = (int)(t / O);
     dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
-  }
+  });
 }
 
 __global__ __launch_bounds__(256) void bias_reduce_bf16_kernel(const float* __restrict__ part, int splits, int O,
@@ -345,7 +329,7 @@ struct WgradPlan {
 bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, int ph, int pw) {
   WgradArgs& a = pl.a;
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
-  if (P <= 0 || Q <= 0 || R != 3 || S != 3) return false;
+  if (P <= 0 || Q <= 0 || R != 3 || S != 3 || ph > 2 || pw > 2) return false;
   a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph; a.pw = pw;
   // vector width: divides Q and W (rows start at multiples of Q / W elements)
   a.V = 8;
@@ -353,34 +337,40 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
   if (a.V < 2) return false;
   a.cpr_dy = Q / a.V;
   a.cpr_x = W / a.V;
-  a.QP = (Q + 7) / 8 * 8;
-  a.G = std::max(1, std::min(P, 128 / a.QP));
-  // prefer a row count that divides P (no zero rows in an image's last step)
-  for (int g = a.G; g * 2 > a.G && g > 1; --g)
-    if (P % g == 0 && ((g * a.QP / 8) & 1) == 0) {
+  a.dadv = 4 * a.V / Q;
+  a.cadv = 4 * a.V % Q;
+  a.xadv = 4 * a.V / W;
+  a.xcadv = 4 * a.V % W;
+  // Largest row count G dividing P whose two LDS stages fit in 160 KB.
+  a.G = 0;
+  for (int g = P; g >= 1; --g) {
+    if (P % g) continue;
+    int xv = (W + 7) / 8 * 8;
+    if ((g * (xv / 8)) & 1) xv += 8;  // chunks per step pair up into 16-deep MFMA steps
+    const int dp = std::max(xv, (Q + 7) / 8 * 8) + 8;
+    int os = 8 + g * dp;
+    if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
+    int cs = (g + R - 1) * xv;
+    if (((cs / 8) & 1) == 0) cs += 8;
+    const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2;
+    const int nd = (g * a.cpr_dy + 3) / 4, nx = ((g + R - 1) * a.cpr_x + 3) / 4;
+    // load items per thread held in VGPRs: 8 x 16-byte or 16 x 8/4-byte per tile
+    const int max_items = a.V == 8 ? 8 : 16;
+    if (lds <= 160 * 1024 && nd <= max_items && nx <= max_items) {
       a.G = g;
+      a.XV = xv;
+      a.XP = xv;
+      a.DP = dp;
+      a.OS = os;
+      a.CS = cs;
+      pl.lds = lds;
+      pl.nd = nd;
+      pl.nx = nx;
       break;
     }
-  if (((a.G * a.QP / 8) & 1) != 0) {  // chunks per step must pair up into 16-deep MFMA steps
-    if (a.G < P) a.G += 1; else a.QP += 8;
-    if (((a.G * a.QP / 8) & 1) != 0) a.QP += 8;
   }
-  a.XP = std::max(a.QP + 16, (W + 2 * pw + 7) / 8 * 8);
-  // LDS row strides: an ODD number of 16-byte units, so the 16 lanes that one
-  // LDS cycle serves (16 rows, 16 bytes each) land on 16 distinct bank groups
-  a.OS = a.G * a.QP;
-  if (((a.OS / 8) & 1) == 0) a.OS += 8;
-  a.CS = (a.G + R - 1) * a.XP;
-  if (((a.CS / 8) & 1) == 0) a.CS += 8;
-  const size_t stage = (size_t)(64 * a.OS + 64 * a.CS) * 2;
-  pl.lds = 2 * stage;
-  if (pl.lds > 160 * 1024) return false;
-  const int dy_items = 64 * a.G * a.cpr_dy, x_items = 64 * (a.G + R - 1) * a.cpr_x;
-  pl.nd = (dy_items + 255) / 256;
-  pl.nx = (x_items + 255) / 256;
-  const int max_nd = a.V == 2 ? 16 : 8, max_nx = a.V == 2 ? 24 : 16;
-  if (pl.nd > max_nd || pl.nx > max_nx) return false;
-  a.steps_per_img = (P + a.G - 1) / a.G;
+  if (a.G == 0) return false;
+  a.steps_per_img = P / a.G;
   a.total_steps = N * a.steps_per_img;
   pl.tiles_o = (O + 63) / 64;
   pl.tiles_c = (C + 63) / 64;
@@ -392,9 +382,9 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
   return true;
 }
 
-template <int R, int S, int V, int ND, int NX>
+template <int R, int S, int PW, int V, int ND, int NX>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
-  auto kern = wgrad_rows_bf16_kernel<R, S, V, ND, NX>;
+  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX>;
   static bool attr = false;
   if (!attr) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -407,12 +397,19 @@ int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
   return VH_OK;
 }
 
-template <int V>
+template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
-  if (pl.nd <= 4 && pl.nx <= 8) return launch_wgrad<3, 3, V, 4, 8>(pl, st);
-  if (pl.nd <= 8 && pl.nx <= 16) return launch_wgrad<3, 3, V, 8, 16>(pl, st);
-  if constexpr (V == 2) return launch_wgrad<3, 3, V, 16, 24>(pl, st);
+  const int n = std::max(pl.nd, pl.nx);
+  if (n <= 8) return launch_wgrad<3, 3, PW, V, 8, 8>(pl, st);
+  if constexpr (V != 8) {
+    if (n <= 16) return launch_wgrad<3, 3, PW, V, 16, 16>(pl, st);
+  }
   return VH_ERR_UNSUPPORTED;
+}
+
+template <int PW>
+int launch_pw(const WgradPlan& pl, hipStream_t st) {
+  return pl.a.V == 8 ? launch_v<PW, 8>(pl, st) : pl.a.V == 4 ? launch_v<PW, 4>(pl, st) : launch_v<PW, 2>(pl, st);
 }
 
 }  // namespace
@@ -444,10 +441,10 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   pl.a.part = ws;
   const size_t pbytes = (size_t)pl.splits * R * S * O * C * sizeof(float);
   pl.a.dbias_part = db ? (float*)((char*)ws + ((pbytes + 255) & ~size_t(255))) : nullptr;
-  int rc = pl.a.V == 8 ? launch_v<8>(pl, st) : pl.a.V == 4 ? launch_v<4>(pl, st) : launch_v<2>(pl, st);
+  int rc = pl.a.pw == 0 ? launch_pw<0>(pl, st) : pl.a.pw == 1 ? launch_pw<1>(pl, st) : launch_pw<2>(pl, st);
   if (rc) return rc;
   const long total = (long)R * S * O * C;
-  wgrad_reduce_bf16_kernel<<<(int)((total + 15) / 16), 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw);
+  wgrad_reduce_bf16_kernel<<<reduce_splits_grid(total), 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw);
   VH_LAUNCH_CHECK();
   if (db) {
     bias_reduce_bf16_kernel<<<(O + 255) / 256, 256, 0, st>>>(pl.a.dbias_part, pl.splits, O, (uint16_t*)db);
