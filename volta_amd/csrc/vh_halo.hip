@@ -19,6 +19,7 @@
 // of one fragment read walk consecutive 16-byte cells: lanes 0-31 read plane 0,
 // lanes 32-63 plane 1, each at consecutive positions / output channels.
 #include <algorithm>
+#include <type_traits>
 
 #include "vh_kernels.hpp"
 
@@ -37,6 +38,7 @@ struct HaloArgs {
   int rows_max;          // max ext rows any block needs
   int x_bytes;           // size of x in bytes (< 2^31: buffer-load range)
   int y_bytes;           // size of y in bytes (< 2^31)
+  int w_bytes;           // size of wt in bytes
   FastDiv fPQ, fQ;
   FastDiv fW2, fRowsMax, fHp;  // item decomposition (W/2, rows_max, Hp)
 };
@@ -63,7 +65,7 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 }
 
 template <int R, int S, int WM, int XI>
-__global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   extern __shared__ __attribute__((aligned(16))) u32x4 lds[];
@@ -78,7 +80,8 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   const int Wp = a.Wp;
   const int cells = a.rows_max * Wp;       // cells per half-plane
   const int w_units = BM * Cfg::WPU;       // 16-byte units per weight stage
-  const int stage = w_units + 2 * cells;   // uint4 per stage
+  const int stage = w_units + 2 * cells + 2;  // uint4 per stage; the last 2 units are a
+                                              // sink for stores of unused load items
   // stage st: weights at lds + st*stage, x halo right after them
 #define WSM(st) (lds + (st) * stage)
 #define XSM(st) (lds + (st) * stage + w_units)
@@ -94,17 +97,15 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
   a.fQ.divmod(pq_b, p_b, q_b);
   const int rows = (int)n_b * a.Hp + (int)p_b + R - e_start;  // ext rows used by this block
 
-  // zero the padding columns once (never written by the loader)
+  // zero the padding columns once (never written by the loader): per (stage,
+  // half-plane, ext row) the columns [0, pw) and [W + pw, Wp)
   const u32x4 z = {0u, 0u, 0u, 0u};
-  const int padc = Wp - a.W;  // = 2*pw for stride 1 'same'-style padding, general otherwise
-  for (int i = tid; i < 2 * 2 * a.rows_max * padc; i += 256) {
-    int st = i / (2 * a.rows_max * padc);
-    int rem = i % (2 * a.rows_max * padc);
-    int half = rem / (a.rows_max * padc);
-    int r2 = rem % (a.rows_max * padc);
-    int e = r2 / padc, pc = r2 % padc;
-    int u = pc < a.pw ? pc : a.W + pc;  // columns [0,pw) and [W+pw, Wp)
-    XSM(st)[half * cells + e * Wp + u] = z;
+  const int padc = Wp - a.W;
+  for (int i = tid; i < 4 * a.rows_max; i += 256) {
+    uint32_t sh, e;
+    a.fRowsMax.divmod((uint32_t)i, sh, e);
+    u32x4* rowp = lds + (sh >> 1) * stage + w_units + (sh & 1) * cells + e * Wp;
+    for (int pc = 0; pc < padc; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
   }
 
   // per-lane cell index of each B fragment column (fixed for the whole block)
@@ -149,51 +150,60 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
       loff = (int)half * cells + (int)e * Wp + a.pw + 2 * (int)wi;
     }
     x_voff[it] = voff;
-    x_loff[it] = loff;
+    x_loff[it] = loff >= 0 ? loff : 2 * cells;  // unused items store to the sink
   }
 
   const bool full_o = o0 + BM <= a.O;  // uniform: no per-row checks needed
-  u32x4 wreg[Cfg::WITER];
-  uint32_t xreg[Cfg::XITER][8];
-
-  auto gload = [&](int c0) {
+  // W load items, fixed for the block: byte offset of the 16-byte unit at
+  // channel 0 (out of range for rows past O) and its LDS unit index
+  const __amdgpu_buffer_rsrc_t wrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.wt, (short)0, a.w_bytes, 0x00020000);
+  int w_goff[Cfg::WITER], w_loff[Cfg::WITER];
 #pragma unroll
-    for (int it = 0; it < Cfg::WITER; ++it) {
-      int u = tid + it * 256;
-      if (u < Cfg::WUNITS) {
-        int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
-        int og = o0 + o;
-        if (full_o || og < a.O)
-          wreg[it] = *reinterpret_cast<const u32x4*>(a.wt + og * RSC + (long)tap * a.C + c0 + half * 8);
-        else
-          wreg[it] = z;
-      }
-    }
+  for (int it = 0; it < Cfg::WITER; ++it) {
+    const int u = tid + it * 256;
+    const int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
+    const int og = o0 + o;
+    const bool ok = u < Cfg::WUNITS && (full_o || og < a.O);
+    w_goff[it] = ok ? (int)((og * RSC + (long)tap * a.C + half * 8) * 2) : (int)0x80000000u;
+    w_loff[it] = u < Cfg::WUNITS ? o * Cfg::WPU + rem : w_units + 2 * cells;  // sink
+  }
+
+  // With two register sets (DEPTH 2) the global loads of channel group kt+2
+  // are issued while group kt is multiplied and group kt+1 is written to LDS,
+  // so every load has two compute phases to arrive; wide tiles (more than 4 x or 5 weight load
+  // items per thread) keep one set to stay within two waves' registers.
+  constexpr int DEPTH = (Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
+  u32x4 wreg[DEPTH][Cfg::WITER];
+  uint32_t xreg[DEPTH][Cfg::XITER][8];
+  auto gload = [&](auto SET, int c0) {
+    constexpr int sI = decltype(SET)::value;
+#pragma unroll
+    for (int it = 0; it < Cfg::WITER; ++it)
+      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_goff[it], c0 * 2, 0));
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       // invalid items carry an out-of-range offset: the buffer load returns 0
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        xreg[it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
+        xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
     }
   };
-  auto sstore = [&](int st) {
+  auto sstore = [&](auto SET, int st) {
+    constexpr int sI = decltype(SET)::value;
+    // unconditional stores (masked items go to the sink), so the wait for the
+    // older register set does not also wait for the loads issued after it
 #pragma unroll
-    for (int it = 0; it < Cfg::WITER; ++it) {
-      int u = tid + it * 256;
-      if (u < Cfg::WUNITS) {
-        int o = u / (RS * 2), rem = u % (RS * 2);
-        WSM(st)[o * Cfg::WPU + rem] = wreg[it];
-      }
-    }
+    for (int it = 0; it < Cfg::WITER; ++it) WSM(st)[w_loff[it]] = wreg[sI][it];
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
-      if (x_loff[it] >= 0) {
+      {
+        const uint32_t* xr = xreg[sI][it];
         u32x4 c0v, c1v;
-        c0v.x = pack_lo(xreg[it][0], xreg[it][1]); c0v.y = pack_lo(xreg[it][2], xreg[it][3]);
-        c0v.z = pack_lo(xreg[it][4], xreg[it][5]); c0v.w = pack_lo(xreg[it][6], xreg[it][7]);
-        c1v.x = pack_hi(xreg[it][0], xreg[it][1]); c1v.y = pack_hi(xreg[it][2], xreg[it][3]);
-        c1v.z = pack_hi(xreg[it][4], xreg[it][5]); c1v.w = pack_hi(xreg[it][6], xreg[it][7]);
+        c0v.x = pack_lo(xr[0], xr[1]); c0v.y = pack_lo(xr[2], xr[3]);
+        c0v.z = pack_lo(xr[4], xr[5]); c0v.w = pack_lo(xr[6], xr[7]);
+        c1v.x = pack_hi(xr[0], xr[1]); c1v.y = pack_hi(xr[2], xr[3]);
+        c1v.z = pack_hi(xr[4], xr[5]); c1v.w = pack_hi(xr[6], xr[7]);
         u32x4* base = XSM(st) + x_loff[it];
         base[0] = c0v;
         base[1] = c1v;
@@ -209,14 +219,8 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
-  const int nk = a.C / 16;
-  gload(0);
-  sstore(0);
-  __syncthreads();
   const int half_l = lane >> 5, row_l = lane & 31;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < nk) gload((kt + 1) * 16);
+  auto compute = [&](int st) {
     const u32x4* Wp_ = WSM(st) + (wm + row_l) * Cfg::WPU + half_l;
     const u32x4* Xp_ = XSM(st) + half_l * cells;
 #pragma unroll
@@ -227,13 +231,9 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
         const int toff = r * Wp + s;
         bf16x8 af[FM], bfr[FN];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          af[i] = __builtin_bit_cast(bf16x8, Wp_[i * 32 * Cfg::WPU + tap * 2]);
-        }
+        for (int i = 0; i < FM; ++i) af[i] = __builtin_bit_cast(bf16x8, Wp_[i * 32 * Cfg::WPU + tap * 2]);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          bfr[j] = __builtin_bit_cast(bf16x8, Xp_[bcell[j] + toff]);
-        }
+        for (int j = 0; j < FN; ++j) bfr[j] = __builtin_bit_cast(bf16x8, Xp_[bcell[j] + toff]);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -241,8 +241,64 @@ __global__ __launch_bounds__(256) void conv_halo_bf16_kernel(HaloArgs a) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
       }
     }
-    if (kt + 1 < nk) sstore(st ^ 1);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  // Channel groups kt = 0 .. nk-1, LDS buffer kt & 1.  DEPTH 2 invariant at an
+  // even kt: buffer 0 holds group kt, register set 1 holds group kt+1 (in
+  // flight), set 0 is free.  The steady-state loop issues its loads without
+  // conditions so that each wait covers only the older register set.
+  const int nk = a.C / 16;
+  if constexpr (DEPTH == 2) {
+    gload(I0{}, 0);
+    if (nk > 1) gload(I1{}, 16);
+    __builtin_amdgcn_sched_barrier(0);
+    sstore(I0{}, 0);
     __syncthreads();
+    int kt = 0;
+    // sched_barrier(0) keeps the compiler from sinking the loads to their
+    // use (which would leave them no time to arrive)
+    for (; kt + 3 < nk; kt += 2) {
+      gload(I0{}, (kt + 2) * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(0);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I1{}, 1);
+      __syncthreads();
+      gload(I1{}, (kt + 3) * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(1);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+      __syncthreads();
+    }
+    const int rem = nk - kt;  // 1, 2 or 3 groups left
+    if (rem == 3) gload(I0{}, (kt + 2) * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(0);
+    if (rem >= 2) {
+      sstore(I1{}, 1);
+      __syncthreads();
+      compute(1);
+      if (rem == 3) {
+        sstore(I0{}, 0);
+        __syncthreads();
+        compute(0);
+      }
+    }
+  } else {
+    gload(I0{}, 0);
+    sstore(I0{}, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) gload(I0{}, (kt + 1) * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(kt & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < nk) sstore(I0{}, (kt + 1) & 1);
+      __syncthreads();
+    }
   }
 
 #undef WSM
@@ -354,6 +410,9 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
   const long yb_ = (long)N * O * P * Q * 2;
   if (yb_ >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.y_bytes = (int)yb_;
+  const long wb = (long)O * R * S * C * 2;
+  if (wb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
+  a.w_bytes = (int)wb;
   a.fW2 = FastDiv((uint32_t)(W / 2));
   a.fHp = FastDiv((uint32_t)a.Hp);
   // 64 output channels x 256 positions per block (two blocks per CU fit in
@@ -372,7 +431,7 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
       int nb = ml / (P * Q), pb = (ml % (P * Q)) / Q;
       rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
     }
-    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp) * 16;
+    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2) * 16;
     lds = 2 * stage;
     const bool fits = lds <= 160 * 1024 && (2 * rows_max * (W / 2) + 255) / 256 <= 8;
     if (fits) break;

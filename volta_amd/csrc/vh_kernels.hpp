@@ -70,8 +70,8 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
 // ---- strided 1x1 bf16 convolutions, pad 0 (vh_pointwise.hip) ----
 // w is the OIHW weight itself ([O][C]); wt its transpose [C][O].  Each returns
 // VH_ERR_UNSUPPORTED without launching when the shape is outside its envelope
-// (stride >= 2; forward C % 16 == 0, dgrad O % 16 == 0, wgrad stride 2 and
-// W % 8 == 0).
+// (stride >= 2; forward C % 16 == 0 and C <= 248, dgrad O % 16 == 0 and
+// O <= 248, wgrad stride 2, W % 8 == 0, output rows a multiple of 4).
 int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, int B, int C, int H, int W, int O,
                      int S, hipStream_t st);
 int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, int H, int W, int O, int S,

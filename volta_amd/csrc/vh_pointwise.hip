@@ -66,154 +66,174 @@ __device__ __forceinline__ u32x2p evens(u32x4p v) {
 }
 
 // ------------------------------------------------------------------ forward
-// Block: 4 waves x 32 output positions; each wave computes MT*32 output
-// channels for its 32 positions.  B fragment: 8 channels of one position
-// (8 two-byte loads, channel planes apart); A fragment: 16 bytes of a weight row.
+// Block: the weight tile W[o0 .. o0+MT*32)[0 .. C) is copied to LDS once (odd
+// 16-byte pitch), then each of the 4 waves computes MT*32 output channels for
+// PT tiles of 32 output positions.  B fragment: 8 channels of one position (8
+// two-byte loads, channel planes apart); A fragment: one ds_read_b128.
+constexpr int PT = 2;  // position tiles per wave
+
 template <int MT>
 __global__ __launch_bounds__(256) void pw_fwd_bf16_kernel(PwArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  extern __shared__ __attribute__((aligned(16))) u32x4p wlds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
-  const uint32_t pos = ((uint32_t)blockIdx.x * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
   const int o0 = blockIdx.y * MT * 32;
-  const bool valid = pos < (uint32_t)a.npos;
-  uint32_t n, pq, p, q;
-  a.fPQ.divmod(valid ? pos : 0u, n, pq);
-  a.fQ.divmod(pq, p, q);
+  const int CU = a.C / 8, WPU = CU | 1;  // 16-byte units per weight row, LDS pitch
+  {
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
+    for (int u = tid; u < MT * 32 * CU; u += 256) {
+      const int r = u / CU, cu = u - r * CU;
+      const int o = o0 + r;
+      wlds[r * WPU + cu] = __builtin_bit_cast(
+          u32x4p, __builtin_amdgcn_raw_buffer_load_b128(wr, o < a.O ? (o * a.C + cu * 8) * 2 : kOutOfRange, 0, 0));
+    }
+  }
+  __syncthreads();
   const int HW2 = a.H * a.W * 2;
-  const int xbase = (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + p * (uint32_t)(a.S * a.W) +
-                           q * (uint32_t)a.S) * 2u) + half * 8 * HW2;
-  int xo[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) xo[j] = valid ? xbase + j * HW2 : kOutOfRange;
-  int wo[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int o = o0 + mt * 32 + col;
-    wo[mt] = o < a.O ? (o * a.C + 8 * half) * 2 : kOutOfRange;
-  }
-  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, a.x_bytes);
-  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
-
-  f32x16 acc[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
-  for (int c0 = 0; c0 < a.C; c0 += 16) {
-    const int so = c0 * HW2;
-    uint16_t xv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) xv[j] = __builtin_amdgcn_raw_buffer_load_b16(xr, xo[j], so, 0);
-    bf16x8 af[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      af[mt] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[mt], c0 * 2, 0));
-    const bf16x8 bf = pack8(xv);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
-  }
-
-  // epilogue: fp32 bias add, one rounding, NCHW store (lanes walk consecutive positions)
   const int PQ = a.P * a.Q;
   const int PQ2 = PQ * 2;
+  const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t yr = rsrc(a.out, a.out_bytes);
-  const int yo = valid ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + pq) * 2u) + half * 4 * PQ2 : kOutOfRange;
+  for (int t = 0; t < PT; ++t) {
+    const uint32_t pos = (((uint32_t)blockIdx.x * PT + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+    const bool valid = pos < (uint32_t)a.npos;
+    uint32_t n, pq, p, q;
+    a.fPQ.divmod(valid ? pos : 0u, n, pq);
+    a.fQ.divmod(pq, p, q);
+    const int xbase = (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + p * (uint32_t)(a.S * a.W) +
+                             q * (uint32_t)a.S) * 2u) + half * 8 * HW2;
+    int xo[8];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int j = 0; j < 8; ++j) xo[j] = valid ? xbase + j * HW2 : kOutOfRange;
+
+    f32x16 acc[MT];
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int orow = o0 + mt * 32 + (v >> 2) * 8 + (v & 3);
-      const int o = orow + half * 4;
-      if (o < a.O) {
-        const float b = a.bias ? bf16_to_f32(a.bias[o]) : 0.f;
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)(acc[mt][v] + b)), yr, yo,
-                                              orow * PQ2, 0);
-      }
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+    for (int c0 = 0; c0 < a.C; c0 += 16) {
+      const int so = c0 * HW2;
+      uint16_t xv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[j] = __builtin_amdgcn_raw_buffer_load_b16(xr, xo[j], so, 0);
+      bf16x8 af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        af[mt] = __builtin_bit_cast(bf16x8, wlds[(mt * 32 + col) * WPU + (c0 >> 3) + half]);
+      const bf16x8 bf = pack8(xv);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
     }
+
+    // epilogue: fp32 bias add, one rounding, NCHW store (lanes walk consecutive positions)
+    const int yo = valid ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + pq) * 2u) + half * 4 * PQ2 : kOutOfRange;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int orow = o0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+        const int o = orow + half * 4;
+        if (o < a.O) {
+          const float b = a.bias ? bf16_to_f32(a.bias[o]) : 0.f;
+          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)(acc[mt][v] + b)), yr, yo,
+                                                orow * PQ2, 0);
+        }
+      }
+  }
 }
 
 // ------------------------------------------------------------------ input gradient
-// Same GEMM shape with rows = input channels (A = W^T [C][O]) and contraction
-// over output channels (B = 8 channels of dY at one position).  Each result
-// is written with the zeros of its s x s cell of dX, so dX is covered exactly
-// once (the cells tile [0,H) x [0,W) because (P-1)*s <= H-1 < P*s).
+// Same GEMM shape with rows = input channels (A = W^T [C][O], staged in LDS
+// like the forward weights) and contraction over output channels (B = 8
+// channels of dY at one position).  Each result is written with the zeros of
+// its s x s cell of dX, so dX is covered exactly once (the cells tile
+// [0,H) x [0,W) because (P-1)*s <= H-1 < P*s).
 template <int MT, bool S2>
 __global__ __launch_bounds__(256) void pw_dgrad_bf16_kernel(PwArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  extern __shared__ __attribute__((aligned(16))) u32x4p wlds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
-  const uint32_t pos = ((uint32_t)blockIdx.x * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
   const int c0 = blockIdx.y * MT * 32;
-  const bool valid = pos < (uint32_t)a.npos;
-  uint32_t n, pq, p, q;
-  a.fPQ.divmod(valid ? pos : 0u, n, pq);
-  a.fQ.divmod(pq, p, q);
+  const int OU = a.O / 8, WPU = OU | 1;
+  {
+    const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
+    for (int u = tid; u < MT * 32 * OU; u += 256) {
+      const int r = u / OU, ou = u - r * OU;
+      const int c = c0 + r;
+      wlds[r * WPU + ou] = __builtin_bit_cast(
+          u32x4p, __builtin_amdgcn_raw_buffer_load_b128(wr, c < a.C ? (c * a.O + ou * 8) * 2 : kOutOfRange, 0, 0));
+    }
+  }
+  __syncthreads();
   const int PQ2 = a.P * a.Q * 2;
-  const int dbase = (int)((n * (uint32_t)a.O * (uint32_t)(a.P * a.Q) + pq) * 2u) + half * 8 * PQ2;
-  int dyo[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) dyo[j] = valid ? dbase + j * PQ2 : kOutOfRange;
-  int wo[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int c = c0 + mt * 32 + col;
-    wo[mt] = c < a.C ? (c * a.O + 8 * half) * 2 : kOutOfRange;
-  }
-  const __amdgpu_buffer_rsrc_t dr = rsrc(a.dy, a.dy_bytes);
-  const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
-
-  f32x16 acc[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
-  for (int k0 = 0; k0 < a.O; k0 += 16) {
-    const int so = k0 * PQ2;
-    uint16_t dv[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) dv[j] = __builtin_amdgcn_raw_buffer_load_b16(dr, dyo[j], so, 0);
-    bf16x8 af[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      af[mt] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(wr, wo[mt], k0 * 2, 0));
-    const bf16x8 bf = pack8(dv);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
-  }
-
   const int HW2 = a.H * a.W * 2;
-  const int h0 = (int)p * a.S, w0 = (int)q * a.S;
-  const int xo = valid ? (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + (uint32_t)(h0 * a.W + w0)) * 2u) +
-                             half * 4 * HW2
-                       : kOutOfRange;
+  const __amdgpu_buffer_rsrc_t dr = rsrc(a.dy, a.dy_bytes);
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.out, a.out_bytes);
-  if (S2) {
-    // s = 2, W even: (value, 0) as one 4-byte store on row h0, (0, 0) on row h0 + 1
-    const int xo1 = (valid && h0 + 1 < a.H) ? xo + a.W * 2 : kOutOfRange;
+  for (int t = 0; t < PT; ++t) {
+    const uint32_t pos = (((uint32_t)blockIdx.x * PT + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+    const bool valid = pos < (uint32_t)a.npos;
+    uint32_t n, pq, p, q;
+    a.fPQ.divmod(valid ? pos : 0u, n, pq);
+    a.fQ.divmod(pq, p, q);
+    const int dbase = (int)((n * (uint32_t)a.O * (uint32_t)(a.P * a.Q) + pq) * 2u) + half * 8 * PQ2;
+    int dyo[8];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int j = 0; j < 8; ++j) dyo[j] = valid ? dbase + j * PQ2 : kOutOfRange;
+
+    f32x16 acc[MT];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
-        if (crow + half * 4 < a.C) {
-          const uint32_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
-          __builtin_amdgcn_raw_buffer_store_b32(val, xr, xo, crow * HW2, 0);
-          __builtin_amdgcn_raw_buffer_store_b32(0u, xr, xo1, crow * HW2, 0);
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x16{};
+    for (int k0 = 0; k0 < a.O; k0 += 16) {
+      const int so = k0 * PQ2;
+      uint16_t dv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dv[j] = __builtin_amdgcn_raw_buffer_load_b16(dr, dyo[j], so, 0);
+      bf16x8 af[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        af[mt] = __builtin_bit_cast(bf16x8, wlds[(mt * 32 + col) * WPU + (k0 >> 3) + half]);
+      const bf16x8 bf = pack8(dv);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mt], bf, acc[mt], 0, 0, 0);
+    }
+
+    const int h0 = (int)p * a.S, w0 = (int)q * a.S;
+    const int xo = valid ? (int)((n * (uint32_t)a.C * (uint32_t)(a.H * a.W) + (uint32_t)(h0 * a.W + w0)) * 2u) +
+                               half * 4 * HW2
+                         : kOutOfRange;
+    if (S2) {
+      // s = 2, W even: (value, 0) as one 4-byte store on row h0, (0, 0) on row h0 + 1
+      const int xo1 = (valid && h0 + 1 < a.H) ? xo + a.W * 2 : kOutOfRange;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+          if (crow + half * 4 < a.C) {
+            const uint32_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
+            __builtin_amdgcn_raw_buffer_store_b32(val, xr, xo, crow * HW2, 0);
+            __builtin_amdgcn_raw_buffer_store_b32(0u, xr, xo1, crow * HW2, 0);
+          }
         }
-      }
-  } else {
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
-        if (crow + half * 4 < a.C) {
-          const uint16_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
-          for (int dh = 0; dh < a.S; ++dh)
-            for (int dw = 0; dw < a.S; ++dw) {
-              const bool in = valid && h0 + dh < a.H && w0 + dw < a.W;
-              __builtin_amdgcn_raw_buffer_store_b16((dh | dw) ? (uint16_t)0 : val, xr,
-                                                    in ? xo + (dh * a.W + dw) * 2 : kOutOfRange, crow * HW2, 0);
-            }
+        for (int v = 0; v < 16; ++v) {
+          const int crow = c0 + mt * 32 + (v >> 2) * 8 + (v & 3);
+          if (crow + half * 4 < a.C) {
+            const uint16_t val = __builtin_bit_cast(uint16_t, (__bf16)acc[mt][v]);
+            for (int dh = 0; dh < a.S; ++dh)
+              for (int dw = 0; dw < a.S; ++dw) {
+                const bool in = valid && h0 + dh < a.H && w0 + dw < a.W;
+                __builtin_amdgcn_raw_buffer_store_b16((dh | dw) ? (uint16_t)0 : val, xr,
+                                                      in ? xo + (dh * a.W + dw) * 2 : kOutOfRange, crow * HW2, 0);
+              }
+          }
         }
-      }
+    }
   }
 }
 
@@ -358,19 +378,20 @@ bool envelope(int B, int C, int H, int W, int O, int S) {
 // ------------------------------------------------------------------ host entry points
 int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, int B, int C, int H, int W, int O,
                      int S, hipStream_t st) {
-  if (!envelope(B, C, H, W, O, S) || C % 16 != 0) return VH_ERR_UNSUPPORTED;
+  if (!envelope(B, C, H, W, O, S) || C % 16 != 0 || C > 248) return VH_ERR_UNSUPPORTED;  // LDS weight tile
   PwArgs a = base_args(B, C, H, W, O, S);
   a.x = x;
   a.w = w;
   a.bias = (const uint16_t*)bias;
   a.out = y;
   a.out_bytes = a.dy_bytes;
-  dim3 grid((a.npos + 127) / 128, (O + 127) / 128);
+  dim3 grid((a.npos + PT * 128 - 1) / (PT * 128), (O + 127) / 128);
+  const size_t lds = (size_t)(O <= 64 ? 64 : 128) * ((C / 8) | 1) * 16;
   if (O <= 64) {
     grid.y = (O + 63) / 64;
-    pw_fwd_bf16_kernel<2><<<grid, 256, 0, st>>>(a);
+    pw_fwd_bf16_kernel<2><<<grid, 256, lds, st>>>(a);
   } else {
-    pw_fwd_bf16_kernel<4><<<grid, 256, 0, st>>>(a);
+    pw_fwd_bf16_kernel<4><<<grid, 256, lds, st>>>(a);
   }
   VH_LAUNCH_CHECK();
   return VH_OK;
@@ -378,21 +399,22 @@ int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, in
 
 int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, int H, int W, int O, int S,
                        hipStream_t st) {
-  if (!envelope(B, C, H, W, O, S) || O % 16 != 0) return VH_ERR_UNSUPPORTED;
+  if (!envelope(B, C, H, W, O, S) || O % 16 != 0 || O > 248) return VH_ERR_UNSUPPORTED;  // LDS weight tile
   PwArgs a = base_args(B, C, H, W, O, S);
   a.dy = dy;
   a.w = wt;
   a.out = dx;
   a.out_bytes = a.x_bytes;
   const bool s2 = S == 2 && W % 2 == 0;
-  dim3 grid((a.npos + 127) / 128, (C + 127) / 128);
+  dim3 grid((a.npos + PT * 128 - 1) / (PT * 128), (C + 127) / 128);
+  const size_t lds = (size_t)(C <= 64 ? 64 : 128) * ((O / 8) | 1) * 16;
   if (C <= 64) {
     grid.y = (C + 63) / 64;
-    if (s2) pw_dgrad_bf16_kernel<2, true><<<grid, 256, 0, st>>>(a);
-    else pw_dgrad_bf16_kernel<2, false><<<grid, 256, 0, st>>>(a);
+    if (s2) pw_dgrad_bf16_kernel<2, true><<<grid, 256, lds, st>>>(a);
+    else pw_dgrad_bf16_kernel<2, false><<<grid, 256, lds, st>>>(a);
   } else {
-    if (s2) pw_dgrad_bf16_kernel<4, true><<<grid, 256, 0, st>>>(a);
-    else pw_dgrad_bf16_kernel<4, false><<<grid, 256, 0, st>>>(a);
+    if (s2) pw_dgrad_bf16_kernel<4, true><<<grid, 256, lds, st>>>(a);
+    else pw_dgrad_bf16_kernel<4, false><<<grid, 256, lds, st>>>(a);
   }
   VH_LAUNCH_CHECK();
   return VH_OK;
