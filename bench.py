@@ -10,9 +10,8 @@ Inputs are synthetic and resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract).  `value` is whole-job TFLOP/s of the
 step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass), timed over K replays of the
-step captured in a HIP graph: forward of every layer, then backward in reverse
-layer order with each weight gradient on a second stream next to the input
-gradient chain (the dependency structure of a training step).  The same passes
+step captured in a HIP graph: forward of every layer, then input and weight
+gradients in reverse layer order (the order of a training step).  The same passes
 run one at a time give `per_op_ms` and `eager_sequential_ms_per_step`.  `roofline` is for the
 dominant pass, timed with HIP events on the stream it runs on (graph of 10
 calls of that pass alone).
@@ -89,12 +88,12 @@ def run_step(layers):
                       outs=(None, L["dw"], None))
 
 
-def make_train_step(torch, layers, side):
-    """One training step of the block in dependency order, as a framework runs it:
-    forward L0..L3 on the current stream; backward L3..L0 with each layer's input
-    gradient on the current stream and its weight gradient on `side`, started
-    once that layer's output gradient exists (here: after the input gradient of
-    the layer above) -- the usual overlap of dW with the dX chain."""
+def make_train_step(torch, layers, side=None):
+    """One training step of the block in dependency order: forward L0..L3, then
+    backward L3..L0 (input gradient, then weight gradient, of each layer).  With
+    `side` the weight gradients run on that second stream next to the input
+    gradient chain; on MI355X the kernels each fill the chip, so the overlap
+    buys nothing and the default is one stream."""
 
     def step():
         main = torch.cuda.current_stream()
@@ -103,15 +102,21 @@ def make_train_step(torch, layers, side):
         ready = torch.cuda.Event()
         ready.record(main)
         for L in reversed(layers):
-            side.wait_event(ready)
-            with torch.cuda.stream(side):
-                L["conv"].backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=L["conv"].algo,
-                                   outs=(None, L["dw"], None))
-            L["conv"].backward(L["dy"], L["x"], input_grad=True, weight_grad=False, algo=L["conv"].algo,
-                               outs=(L["dx"], None, None))
+            conv = L["conv"]
+            if side is not None:
+                side.wait_event(ready)
+                with torch.cuda.stream(side):
+                    conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=conv.algo,
+                                  outs=(None, L["dw"], None))
+            conv.backward(L["dy"], L["x"], input_grad=True, weight_grad=False, algo=conv.algo,
+                          outs=(L["dx"], None, None))
+            if side is None:
+                conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=conv.algo,
+                              outs=(None, L["dw"], None))
             ready = torch.cuda.Event()
             ready.record(main)
-        main.wait_stream(side)
+        if side is not None:
+            main.wait_stream(side)
 
     return step
 
@@ -283,10 +288,8 @@ def main():
     layers = build_layers(torch, vnn, dev)
     step_flops = 3.0 * sum(L["flops"] for L in layers)
 
-    # headline: the training step (forward, then dX / dW with dW on a second
-    # stream) captured in one HIP graph, K replays timed
-    side = torch.cuda.Stream()
-    train_step = make_train_step(torch, layers, side)
+    # headline: the training step captured in one HIP graph, K replays timed
+    train_step = make_train_step(torch, layers)
     ms_per_step = time_graph_step(torch, train_step, args.steps, args.warmup)
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
 
@@ -345,7 +348,7 @@ def main():
         "pct_bf16_peak": round(100.0 * tflops / PEAK_TFLOPS["bf16"], 2),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "schedule": "HIP graph of the training step; dW of each layer on a second stream, overlapping the dX chain",
+        "schedule": "training step (fwd L0..L3, then dX and dW of L3..L0) captured in one HIP graph, one stream",
         "eager_sequential_ms_per_step": round(eager_ms, 4),
         "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
         "secondary": secondary,

@@ -152,6 +152,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
   VT rdy[ND], rx[NX];
+  // Branch-free load / store sequences (selects, and a sink slot in LDS for
+  // unused items), so the compiler can count outstanding loads exactly.
   auto gload = [&](int step) {
     const int n = step / a.steps_per_img;
     const int p0 = (step - n * a.steps_per_img) * G;
@@ -164,9 +166,10 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     for (int it = 0; it < ND; ++it) {
       const bool ok = dy_own_ok && sub + 4 * it < dy_chunks;
       rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + col) * 2 : (int)0x80000000u, 0);
-      g += a.dadv;
       col += a.cadv;
-      if (col >= a.Q) { col -= a.Q; ++g; }
+      const int wrap = col >= a.Q;
+      col -= wrap ? a.Q : 0;
+      g += a.dadv + wrap;
     }
     int j = xj0;
     col = xc0;
@@ -174,30 +177,36 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     for (int it = 0; it < NX; ++it) {
       const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax;
       rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + col) * 2 : (int)0x80000000u, 0);
-      j += a.xadv;
       col += a.xcadv;
-      if (col >= a.W) { col -= a.W; ++j; }
+      const int wrap = col >= a.W;
+      col -= wrap ? a.W : 0;
+      j += a.xadv + wrap;
     }
   };
   auto sstore = [&](int st) {
     uint16_t* d = DYS(st) + own * OS + 8;
     uint16_t* xs = XS(st) + own * CS;
+    uint16_t* sink = smem + 2 * stage;  // 16 bytes past both stages
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      if (sub + 4 * it < dy_chunks) *reinterpret_cast<VT*>(d + g * DP + col) = rdy[it];
-      g += a.dadv;
+      uint16_t* dst = sub + 4 * it < dy_chunks ? d + g * DP + col : sink;
+      *reinterpret_cast<VT*>(dst) = rdy[it];
       col += a.cadv;
-      if (col >= a.Q) { col -= a.Q; ++g; }
+      const int wrap = col >= a.Q;
+      col -= wrap ? a.Q : 0;
+      g += a.dadv + wrap;
     }
     int j = xj0;
     col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      if (sub + 4 * it < x_chunks) *reinterpret_cast<VT*>(xs + j * XP + col) = rx[it];
-      j += a.xadv;
+      uint16_t* dst = sub + 4 * it < x_chunks ? xs + j * XP + col : sink;
+      *reinterpret_cast<VT*>(dst) = rx[it];
       col += a.xcadv;
-      if (col >= a.W) { col -= a.W; ++j; }
+      const int wrap = col >= a.W;
+      col -= wrap ? a.W : 0;
+      j += a.xadv + wrap;
     }
   };
 
@@ -213,15 +222,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int nchunk = G * (XV >> 3);  // even by construction
   const int grp = lane >> 5, rl = lane & 31;
 
-  __syncthreads();
-  if (nsteps > 0) {
-    gload(step_b);
-    sstore(0);
-  }
-  __syncthreads();
-  for (int ks = 0; ks < nsteps; ++ks) {
-    const int st = ks & 1;
-    if (ks + 1 < nsteps) gload(step_b + ks + 1);
+  auto compute = [&](int st) {
     const uint16_t* dl = DYS(st) + (wo + rl) * OS + 8;
     const uint16_t* xl = XS(st) + (wc + rl) * CS;
     // this lane group's chunk t = kk + grp as (row g, column v0)
@@ -259,9 +260,26 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
       const int q4 = OS >> 2, beg = sub * q4, end = sub == 3 ? OS : beg + q4;
       for (int k = beg; k < end; ++k) dbias += bf16_to_f32(drow[k]);
     }
-    if (ks + 1 < nsteps) sstore(st ^ 1);
+  };
+
+  __syncthreads();
+  if (nsteps > 0) {
+    gload(step_b);
+    __builtin_amdgcn_sched_barrier(0);
+    sstore(0);
+  }
+  __syncthreads();
+  // steady state: the next step's loads are issued before this step's MFMAs
+  // (sched_barrier keeps the compiler from sinking them to their use)
+  for (int ks = 0; ks + 1 < nsteps; ++ks) {
+    gload(step_b + ks + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(ks & 1);
+    __builtin_amdgcn_sched_barrier(0);
+    sstore((ks + 1) & 1);
     __syncthreads();
   }
+  if (nsteps > 0) compute((nsteps - 1) & 1);
 #undef DYS
 #undef XS
 
@@ -352,10 +370,10 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
     if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
     int cs = (g + R - 1) * xv;
     if (((cs / 8) & 1) == 0) cs += 8;
-    const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2;
+    const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2 + 16;  // + sink for unused items
     const int nd = (g * a.cpr_dy + 3) / 4, nx = ((g + R - 1) * a.cpr_x + 3) / 4;
-    // load items per thread held in VGPRs: 8 x 16-byte or 16 x 8/4-byte per tile
-    const int max_items = a.V == 8 ? 8 : 16;
+    // load items per thread held in VGPRs (16 at most)
+    const int max_items = 16;
     if (lds <= 160 * 1024 && nd <= max_items && nx <= max_items) {
       a.G = g;
       a.XV = xv;
@@ -401,9 +419,7 @@ template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
   const int n = std::max(pl.nd, pl.nx);
   if (n <= 8) return launch_wgrad<3, 3, PW, V, 8, 8>(pl, st);
-  if constexpr (V != 8) {
-    if (n <= 16) return launch_wgrad<3, 3, PW, V, 16, 16>(pl, st);
-  }
+  if (n <= 16) return launch_wgrad<3, 3, PW, V, 16, 16>(pl, st);
   return VH_ERR_UNSUPPORTED;
 }
 
