@@ -207,12 +207,12 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wt = at(ws, o_w);
-  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wt, (int)d.O, (int)d.C, (int)RS, 0, st));
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
-    int r = halo_conv_bf16(x, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
+    int r = halo_conv_bf16(x, w, 0, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
                            (int)d.KW, (int)d.PH, (int)d.PW, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
+  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wt, (int)d.O, (int)d.C, (int)RS, 0, st));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wt, (int)(RS * d.C), (int)d.O, ((RS * d.C) % vec) == 0};
   p.args.b = Operand{x, 0, p.args.N, 0};
@@ -246,9 +246,8 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   void* wd = at(ws, o_w);
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && d.PH <= d.KH - 1 && d.PW <= d.KW - 1 && g_fast_paths) {
     // stride 1: dX = conv(dY, W rotated 180 degrees with O and C swapped), pad K-1-p
-    VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 1));
-    int r = halo_conv_bf16(dy, wd, nullptr, dx, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C, (int)d.KH,
-                           (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
+    int r = halo_conv_bf16(dy, w, 1, wd, nullptr, dx, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C,
+                           (int)d.KH, (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));

@@ -25,11 +25,17 @@
 
 namespace vh {
 
+#define VH_TRY_HALO(expr)       \
+  do {                          \
+    int _s = (expr);            \
+    if (_s != VH_OK) return _s; \
+  } while (0)
+
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct HaloArgs {
   const uint16_t* x;     // [N][C][H][W]
-  const uint16_t* wt;    // [O][R*S][C]
+  const uint16_t* wt;    // grouped [C/16][O][R*S][16]
   const uint16_t* bias;  // [O] or nullptr
   uint16_t* y;           // [N][O][P][Q]
   int N, C, H, W, O, P, Q, ph, pw;
@@ -124,7 +130,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   const int HW = a.H * a.W;
-  const long RSC = (long)RS * a.C;
 
   // x load items (fixed for the whole block; only the channel group moves):
   // item -> (half, ext row e, column pair wi).  x_voff is the byte offset of the
@@ -154,18 +159,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   const bool full_o = o0 + BM <= a.O;  // uniform: no per-row checks needed
-  // W load items, fixed for the block: byte offset of the 16-byte unit at
-  // channel 0 (out of range for rows past O) and its LDS unit index
+  // W load items, fixed for the block: byte offset of the 16-byte unit in
+  // channel group 0 (out of range for rows past O) and its LDS unit index
+  const int OG2 = a.O * RS * 2;  // bytes per channel of the grouped weights: group offset = c0 * OG2
   const __amdgpu_buffer_rsrc_t wrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.wt, (short)0, a.w_bytes, 0x00020000);
   int w_goff[Cfg::WITER], w_loff[Cfg::WITER];
 #pragma unroll
   for (int it = 0; it < Cfg::WITER; ++it) {
     const int u = tid + it * 256;
-    const int o = u / (RS * 2), rem = u % (RS * 2), tap = rem >> 1, half = rem & 1;
+    const int o = u / (RS * 2), rem = u % (RS * 2);
     const int og = o0 + o;
     const bool ok = u < Cfg::WUNITS && (full_o || og < a.O);
-    w_goff[it] = ok ? (int)((og * RSC + (long)tap * a.C + half * 8) * 2) : (int)0x80000000u;
+    // the tile of one channel group is contiguous: unit u of the block's rows
+    w_goff[it] = ok ? ((o0 * RS * 2 + u) * 16) : (int)0x80000000u;
     w_loff[it] = u < Cfg::WUNITS ? o * Cfg::WPU + rem : w_units + 2 * cells;  // sink
   }
 
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     constexpr int sI = decltype(SET)::value;
 #pragma unroll
     for (int it = 0; it < Cfg::WITER; ++it)
-      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_goff[it], c0 * 2, 0));
+      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_goff[it], c0 * OG2, 0));
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       // invalid items carry an out-of-range offset: the buffer load returns 0
@@ -387,12 +394,15 @@ int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
 
 // Returns VH_ERR_UNSUPPORTED (without launching) when the shape is outside what
 // the halo kernel handles; the caller then uses the generic implicit GEMM.
-int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int N, int C, int H, int W, int O,
-                   int R, int S, int ph, int pw, hipStream_t st) {
+size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)C * O * R * S * 2; }
+
+int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
+                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st) {
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0) return VH_ERR_UNSUPPORTED;
   if ((C % 16) != 0 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
   if (!((R == 3 && S == 3) || (R == 5 && S == 5) || (R == 1 && S == 1))) return VH_ERR_UNSUPPORTED;
+  const void* wt = ws;
   HaloArgs a;
   a.x = (const uint16_t*)x;
   a.wt = (const uint16_t*)wt;
@@ -439,6 +449,7 @@ int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int
   }
   a.rows_max = rows_max;
   a.fRowsMax = FastDiv((uint32_t)rows_max);
+  VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
     return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \

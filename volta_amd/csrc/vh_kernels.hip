@@ -312,6 +312,37 @@ __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::s
   }
 }
 
+// Grouped weight layout of the bf16 stride-1 kernel (vh_halo.hip): for a
+// GEMM with M rows (output channels of the convolution the kernel computes) and
+// contraction channels K (multiple of 16), dst[kg][m][tap][16] holds channel
+// 16*kg + i in slot i, so the tile of one 16-channel group and a range of rows
+// is one contiguous run.  mode 0: M = O, K = C, from W[m][k][tap] (forward);
+// mode 1: M = C, K = O, from W[k][m][tap] with the taps rotated 180 degrees
+// (input gradient as a forward convolution).  Walks dst in order.
+__global__ __launch_bounds__(256) void relayout_grouped_kernel(const uint16_t* __restrict__ src,
+                                                               uint16_t* __restrict__ dst, int M, int K, int RS,
+                                                               int mode, FastDiv fRS, FastDiv fM) {
+  const uint32_t total = (uint32_t)M * K * RS;
+  for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < total; d += gridDim.x * 256u) {
+    const uint32_t i = d & 15u, t = d >> 4;
+    uint32_t t2, tap, kg, m;
+    fRS.divmod(t, t2, tap);
+    fM.divmod(t2, kg, m);
+    const uint32_t k = kg * 16u + i;
+    const uint32_t s = mode == 0 ? (m * (uint32_t)K + k) * RS + tap
+                                 : (k * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap);
+    dst[d] = src[s];
+  }
+}
+
+int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st) {
+  if (K % 16 != 0) return set_error(VH_ERR_UNSUPPORTED, "grouped weight layout needs 16 | K");
+  relayout_grouped_kernel<<<grid_for((long)M * K * RS), 256, 0, st>>>(
+      (const uint16_t*)w, (uint16_t*)dst, M, K, RS, mode, FastDiv((uint32_t)RS), FastDiv((uint32_t)M));
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 // Element-wise form of the same map for windows of more than 64 taps.
 template <typename T>
 __global__ __launch_bounds__(256) void relayout_simple_kernel(const typename Elem<T>::storage* __restrict__ src,

@@ -53,11 +53,19 @@ int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice
 template <typename T>
 int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
 
+// Grouped bf16 weight layout [K/16][M][RS][16] of the halo kernel (vh_kernels.hip).
+int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st);
+
 // ---- stride-1 bf16 halo convolution (vh_halo.hip) ----
-// wt is [O][R*S][C]; returns VH_ERR_UNSUPPORTED without launching when the shape
-// is outside the kernel's envelope.
-int halo_conv_bf16(const void* x, const void* wt, const void* bias, void* y, int N, int C, int H, int W, int O,
-                   int R, int S, int ph, int pw, hipStream_t st);
+// Computes y = conv(x, W') with C input and O output channels, where W' is
+// taken from the OIHW weight w: w_mode 0 uses w as is (w is [O][C][R][S]);
+// w_mode 1 uses w transposed and rotated 180 degrees (w is [C][O][R][S]: the
+// input gradient of a stride-1 convolution).  ws (O*C*R*S*2 bytes) receives the
+// re-laid-out copy.  Returns VH_ERR_UNSUPPORTED without launching anything when
+// the shape is outside the kernel's envelope.
+size_t halo_conv_bf16_ws(int C, int O, int R, int S);
+int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
+                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st);
 
 // ---- stride-1 bf16 weight gradient (vh_wgrad.hip) ----
 // Workspace bytes needed (0 if the shape is outside the kernel's envelope).
