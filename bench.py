@@ -9,10 +9,10 @@ input gradient and weight gradient of every layer (dY ~ N(0,1) injected).
 Inputs are synthetic and resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract).  `value` is whole-job TFLOP/s of the
-step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass), timed over K replays of the
-step captured in a HIP graph: forward of every layer, then input and weight
-gradients in reverse layer order (the order of a training step).  The same passes
-run one at a time give `per_op_ms` and `eager_sequential_ms_per_step`.  `roofline` is for the
+step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass) over K steps issued on one
+stream: forward of every layer, then input and weight gradients in reverse
+layer order (the order of a training step).  The same step captured in a HIP
+graph gives `graph_ms_per_step`; each pass alone gives `per_op_ms`.  `roofline` is for the
 dominant pass, timed with HIP events on the stream it runs on (graph of 10
 calls of that pass alone).
 `cpu_baseline` times the CPU oracle (a C restatement of Volta's
@@ -76,16 +76,6 @@ def build_layers(torch, vnn, dev):
         byts = 2.0 * (x.numel() + conv.weight.numel() + y.numel())
         layers.append(dict(name=name, conv=conv, x=x, dy=dy, y=y, dx=dx, dw=dw, flops=flops, bytes=byts))
     return layers
-
-
-def run_step(layers):
-    for L in layers:
-        conv = L["conv"]
-        conv.forward(L["x"], out=L["y"])
-        conv.backward(L["dy"], L["x"], input_grad=True, weight_grad=False, algo=conv.algo,
-                      outs=(L["dx"], None, None))
-        conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=conv.algo,
-                      outs=(None, L["dw"], None))
 
 
 def make_train_step(torch, layers, side=None):
@@ -154,15 +144,15 @@ def time_op_graph(torch, fn, reps, replays):
     return time_graph_step(torch, many, replays, 1) / reps
 
 
-def time_eager_step(torch, layers, steps, warmup):
-    """The same passes issued eagerly, one at a time on one stream."""
+def time_eager_fn(torch, fn, steps, warmup):
+    """`fn` issued eagerly `steps` times between two HIP events (after warm-up)."""
     for _ in range(warmup):
-        run_step(layers)
+        fn()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
-        run_step(layers)
+        fn()
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
@@ -288,14 +278,16 @@ def main():
     layers = build_layers(torch, vnn, dev)
     step_flops = 3.0 * sum(L["flops"] for L in layers)
 
-    # headline: the training step captured in one HIP graph, K replays timed
+    # headline: the training step (forward, then dX and dW in reverse layer
+    # order) issued eagerly on one stream, K steps between HIP events; the same
+    # step captured in one HIP graph is timed too (graph_ms_per_step)
     train_step = make_train_step(torch, layers)
-    ms_per_step = time_graph_step(torch, train_step, args.steps, args.warmup)
+    graph_ms = time_graph_step(torch, train_step, args.steps, args.warmup)
+    ms_per_step = time_eager_fn(torch, train_step, args.steps, args.warmup)
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
 
     # per-op pass: each pass alone, `reps` calls captured in a HIP graph and
     # replayed (GPU time per call without host launch gaps)
-    eager_ms = time_eager_step(torch, layers, args.steps, args.warmup)
     ops = []
     for L in layers:
         conv = L["conv"]
@@ -348,8 +340,8 @@ def main():
         "pct_bf16_peak": round(100.0 * tflops / PEAK_TFLOPS["bf16"], 2),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "schedule": "training step (fwd L0..L3, then dX and dW of L3..L0) captured in one HIP graph, one stream",
-        "eager_sequential_ms_per_step": round(eager_ms, 4),
+        "schedule": "training step: fwd L0..L3, then dX and dW of L3..L0, eager on one stream",
+        "graph_ms_per_step": round(graph_ms, 4),
         "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
         "secondary": secondary,
     }
