@@ -56,6 +56,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--profile-op", default=None,
+                    help="run only this pass (e.g. '3x3 256->256 @14 wgrad') --steps times, then a "
+                         "256 MiB device copy, for rocprofv3 counter runs; prints nothing else")
     return ap.parse_args()
 
 
@@ -156,6 +159,32 @@ def time_eager_fn(torch, fn, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def pass_fns(L):
+    conv = L["conv"]
+    return {
+        "fwd": lambda: conv.forward(L["x"], out=L["y"]),
+        "dgrad": lambda: conv.backward(L["dy"], L["x"], input_grad=True, weight_grad=False, algo=conv.algo,
+                                       outs=(L["dx"], None, None)),
+        "wgrad": lambda: conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True, algo=conv.algo,
+                                       outs=(None, L["dw"], None)),
+    }
+
+
+def profile_op(torch, layers, name, reps):
+    """Counter runs: the named pass `reps` times, then a plain copy of 256 MiB
+    (the calibration kernel: it reads and writes exactly 256 MiB)."""
+    layer, op = name.rsplit(" ", 1)
+    L = next(L for L in layers if L["name"] == layer)
+    fn = pass_fns(L)[op]
+    for _ in range(reps):
+        fn()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def gemm_secondary(torch, vnn, dev, reps=5):
@@ -278,6 +307,10 @@ def main():
     layers = build_layers(torch, vnn, dev)
     step_flops = 3.0 * sum(L["flops"] for L in layers)
 
+    if args.profile_op:
+        profile_op(torch, layers, args.profile_op, args.steps)
+        return
+
     # headline: the training step (forward, then dX and dW in reverse layer
     # order) issued eagerly on one stream, K steps between HIP events; the same
     # step captured in one HIP graph is timed too (graph_ms_per_step)
@@ -290,15 +323,7 @@ def main():
     # replayed (GPU time per call without host launch gaps)
     ops = []
     for L in layers:
-        conv = L["conv"]
-        fns = {
-            "fwd": lambda L=L, conv=conv: conv.forward(L["x"], out=L["y"]),
-            "dgrad": lambda L=L, conv=conv: conv.backward(L["dy"], L["x"], input_grad=True, weight_grad=False,
-                                                          algo=conv.algo, outs=(L["dx"], None, None)),
-            "wgrad": lambda L=L, conv=conv: conv.backward(L["dy"], L["x"], input_grad=False, weight_grad=True,
-                                                          algo=conv.algo, outs=(None, L["dw"], None)),
-        }
-        for k, fn in fns.items():
+        for k, fn in pass_fns(L).items():
             ms = time_op_graph(torch, fn, reps=10, replays=max(2, args.steps // 4))
             ops.append(dict(layer=L["name"], op=k, ms=ms, flops=L["flops"], bytes=L["bytes"]))
     dom = max(ops, key=lambda o: o["ms"])

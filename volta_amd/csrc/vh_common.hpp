@@ -73,6 +73,17 @@ struct FastDiv {
   }
 };
 
+// XCD-aware block order.  The dispatcher deals the workgroups of a 1-D grid
+// to the 8 XCDs (each with its own L2) round robin by block id.  Logical
+// block L = xcd * (nb / 8) + slot puts consecutive logical blocks -- which
+// the callers arrange to share input data -- on the same XCD.  Identity when
+// nb is not a multiple of 8.
+__device__ __forceinline__ int xcd_block(int nb) {
+  const int h = blockIdx.x;
+  if (nb & 7) return h;
+  return (h & 7) * (nb >> 3) + (h >> 3);
+}
+
 // Deterministic reduction of split-K partial sums part[z][i] (z < splits,
 // i < total) by a 256-thread block: 64 consecutive outputs per pass, wave w
 // adds z = w, w+4, w+8, ... in order and the four wave sums are added in wave

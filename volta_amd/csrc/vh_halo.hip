@@ -45,6 +45,7 @@ struct HaloArgs {
   int x_bytes;           // size of x in bytes (< 2^31: buffer-load range)
   int y_bytes;           // size of y in bytes (< 2^31)
   int w_bytes;           // size of wt in bytes
+  int tiles_m, tiles_o;  // grid = tiles_m * tiles_o blocks
   FastDiv fPQ, fQ;
   FastDiv fW2, fRowsMax, fHp;  // item decomposition (W/2, rows_max, Hp)
 };
@@ -81,8 +82,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int wm = (wave / Cfg::WN) * FM * 32;  // wave's first output channel in the tile
   const int wn = (wave % Cfg::WN) * FN * 32;  // wave's first position in the tile
 
-  const int m0 = blockIdx.x * BN;
-  const int o0 = blockIdx.y * BM;
+  // logical block -> (position tile, o tile): the o tiles of one position tile
+  // (same x rows) and neighbouring position tiles (shared halo rows) are
+  // consecutive, hence on one XCD's L2
+  const int lb = xcd_block(a.tiles_m * a.tiles_o);
+  const int m0 = (lb / a.tiles_o) * BN;
+  const int o0 = (lb % a.tiles_o) * BM;
   const int Wp = a.Wp;
   const int cells = a.rows_max * Wp;       // cells per half-plane
   const int w_units = BM * Cfg::WPU;       // 16-byte units per weight stage
@@ -374,8 +379,10 @@ int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
                               160 * 1024);
     attr_set = true;
   }
-  dim3 grid((unsigned)((a.M + Cfg::BN - 1) / Cfg::BN), (unsigned)((a.O + Cfg::BM - 1) / Cfg::BM));
-  kern<<<grid, 256, lds_bytes, st>>>(a);
+  HaloArgs g = a;
+  g.tiles_m = (a.M + Cfg::BN - 1) / Cfg::BN;
+  g.tiles_o = (a.O + Cfg::BM - 1) / Cfg::BM;
+  kern<<<dim3((unsigned)(g.tiles_m * g.tiles_o)), 256, lds_bytes, st>>>(g);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }

@@ -51,6 +51,7 @@ struct WgradArgs {
   int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < Q
   int xadv, xcadv;     // the same for x rows (columns < W)
   int dy_bytes, x_bytes, part_bytes;  // buffer ranges (< 2^31)
+  int tiles_o, tiles_c, splits;       // grid = tiles_o * tiles_c * splits blocks
 };
 
 template <int V> struct BufLoad;
@@ -118,8 +119,12 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wo = (wave >> 1) * 32, wc = (wave & 1) * 32;
-  const int o0 = blockIdx.x * TO, c0 = blockIdx.y * TC;
-  const int split = blockIdx.z;
+  // logical block -> (o tile, c tile, split): the tiles of one split (which
+  // read the same dY / x rows) are consecutive, hence on one XCD's L2
+  const int lb = xcd_block(a.tiles_o * a.tiles_c * a.splits);
+  const int tile = lb % (a.tiles_o * a.tiles_c), split = lb / (a.tiles_o * a.tiles_c);
+  const int tile_c = tile / a.tiles_o;
+  const int o0 = (tile % a.tiles_o) * TO, c0 = tile_c * TC;
   const int G = a.G, DP = a.DP, XP = a.XP, OS = a.OS, CS = a.CS;
   const int XR = G + R - 1;
   const int dy_elems = TO * OS, x_elems = TC * CS;
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
   float dbias = 0.f;
-  const bool do_bias = a.dbias_part != nullptr && blockIdx.y == 0;
+  const bool do_bias = a.dbias_part != nullptr && tile_c == 0;
 
   const int XV = a.XV;
   const int nchunk = G * (XV >> 3);  // even by construction
@@ -397,6 +402,9 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
   int splits = std::max(1, std::min(a.total_steps, (256 + tiles - 1) / tiles));
   a.steps_per_split = (a.total_steps + splits - 1) / splits;
   pl.splits = (a.total_steps + a.steps_per_split - 1) / a.steps_per_split;
+  a.tiles_o = pl.tiles_o;
+  a.tiles_c = pl.tiles_c;
+  a.splits = pl.splits;
   return true;
 }
 
@@ -409,7 +417,7 @@ int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
                               160 * 1024);
     attr = true;
   }
-  dim3 grid((unsigned)pl.tiles_o, (unsigned)pl.tiles_c, (unsigned)pl.splits);
+  dim3 grid((unsigned)(pl.tiles_o * pl.tiles_c * pl.splits));
   kern<<<grid, 256, pl.lds, st>>>(pl.a);
   VH_LAUNCH_CHECK();
   return VH_OK;
