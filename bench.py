@@ -35,6 +35,18 @@ PEAK_HBM_GBS = 8000.0
 
 METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
 
+# HBM bytes per call of a pass, from two rocprofv3 counter runs of
+# `bench.py --profile-op <pass>` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch,
+# summed over the pass's kernels).  Calibration on the 256 MiB copy of the same
+# runs: WRITE_SIZE reads 262144 KiB (factor 1), FETCH_SIZE 131088 KiB (factor 2).
+# Summary: profiles/c3_wgrad_256_traffic.md.  Keyed by pass name; used for
+# roofline.traffic when that pass is the dominant one.
+MEASURED_TRAFFIC_BYTES = {
+    # wgrad_rows_bf16_kernel: fetch 12746 KiB x2, write 36864 KiB;
+    # wgrad_reduce_bf16_kernel: fetch 18458 KiB x2, write 1152 KiB
+    "3x3 256->256 @14 wgrad": (12746 * 2 + 36864 + 18458 * 2 + 1152) * 1024,
+}
+
 # (name, C, O, H, K, stride, pad) at N=128
 C3_LAYERS = [
     ("3x3 64->64 @56", 64, 64, 56, 3, 1, 1),
@@ -338,6 +350,8 @@ def main():
         roof = dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
                     frac=round(ach / PEAK_HBM_GBS, 4), traffic=None)
     roof["kernel"] = f"{dom['layer']} {dom['op']}"
+    roof["traffic"] = MEASURED_TRAFFIC_BYTES.get(roof["kernel"])
+    roof["algorithmic_bytes"] = dom["bytes"]
     roof["launch_ms"] = round(dom["ms"], 4)
 
     secondary = gemm_secondary(torch, vnn, dev)
