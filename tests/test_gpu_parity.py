@@ -97,7 +97,8 @@ def test_conv_ramp_window_sums(algo):
 
 
 # ------------------------------------------------------------------ matmul family
-MM_CASES = [(37, 19, 23), (128, 256, 64), (130, 70, 200), (64, 1024, 96), (256, 512, 384), (3, 5, 300)]
+MM_CASES = [(37, 19, 23), (128, 256, 64), (130, 70, 200), (64, 1024, 96), (256, 512, 384), (3, 5, 300),
+            (200, 72, 136), (8, 40, 24), (520, 264, 392)]  # K % 8 == 0, M / N off the tile sizes
 
 
 @pytest.mark.parametrize("mkn", MM_CASES)
