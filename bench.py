@@ -68,6 +68,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--configs", action="store_true",
+                    help="instead of the headline line, time a fwd+bwd step of every BASELINE config "
+                         "(one JSON line each)")
     ap.add_argument("--profile-op", default=None,
                     help="run only this pass (e.g. '3x3 256->256 @14 wgrad') --steps times, then a "
                          "256 MiB device copy, for rocprofv3 counter runs; prints nothing else")
@@ -199,6 +202,69 @@ def profile_op(torch, layers, name, reps):
     torch.cuda.synchronize()
 
 
+def config_steps(torch, vnn, dev, steps, warmup):
+    """Fwd+bwd step of each BASELINE config (synthetic inputs of the config's
+    shapes, the library's MI355X algorithm choice), one JSON line per config."""
+    g = torch.Generator().manual_seed(3)
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
+
+    def conv_layer(dt, N, C, O, H, K, S, P, first):
+        conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dts[dt], generator=g)
+        x = torch.randn((N, C, H, H), generator=g).to(dev, dts[dt])
+        HO = conv_out(H, K, S, P)
+        dy = torch.randn((N, O, HO, HO), generator=g).to(dev, dts[dt])
+        y = torch.empty((N, O, HO, HO), device=dev, dtype=dts[dt])
+        outs = (None if first else torch.empty_like(x), torch.empty_like(conv.weight), torch.empty_like(conv.bias))
+        passes = 2 if first else 3
+        fl = passes * 2.0 * N * O * C * K * K * HO * HO
+
+        def run():
+            conv.forward(x, out=y)
+            conv.backward(dy, x, input_grad=not first, weight_grad=True, outs=outs)
+        return run, fl
+
+    def convt_layer(dt, N, CI, CO, H, K, S, P):
+        ct = vnn.ConvTranspose2d(CI, CO, K, S, P, device=dev, dtype=dts[dt], generator=g)
+        x = torch.randn((N, CI, H, H), generator=g).to(dev, dts[dt])
+        HO = (H - 1) * S + K - 2 * P
+        dy = torch.randn((N, CO, HO, HO), generator=g).to(dev, dts[dt])
+        y = torch.empty((N, CO, HO, HO), device=dev, dtype=dts[dt])
+        outs = (torch.empty_like(x), torch.empty_like(ct.weight), torch.empty_like(ct.bias))
+        fl = 3 * 2.0 * N * H * H * CI * CO * K * K
+
+        def run():
+            ct.forward(x, out=y)
+            ct.backward(dy, x, outs=outs)
+        return run, fl
+
+    cfgs = {
+        "configs[0] MNIST-CNN f32 N=64": ("f32", [conv_layer("f32", 64, 1, 32, 28, 3, 1, 1, True),
+                                                 conv_layer("f32", 64, 32, 64, 28, 3, 1, 1, False)]),
+        "configs[3] DCGAN ConvTranspose2d f32 N=128": ("f32", [convt_layer("f32", 128, 100, 512, 1, 4, 1, 0),
+                                                               convt_layer("f32", 128, 512, 256, 4, 4, 2, 1),
+                                                               convt_layer("f32", 128, 256, 128, 8, 4, 2, 1),
+                                                               convt_layer("f32", 128, 128, 64, 16, 4, 2, 1),
+                                                               convt_layer("f32", 128, 64, 3, 32, 4, 2, 1)]),
+        "configs[4] super-resolution bf16 N=16 256x256": ("bf16", [
+            conv_layer("bf16", 16, 3, 64, 256, 5, 1, 2, True), conv_layer("bf16", 16, 64, 64, 256, 3, 1, 1, False),
+            conv_layer("bf16", 16, 64, 32, 256, 3, 1, 1, False), conv_layer("bf16", 16, 32, 27, 256, 3, 1, 1, False)]),
+    }
+    ps = vnn.PixelShuffle(3)
+    xs = torch.randn((16, 27, 256, 256), generator=g).to(dev, torch.bfloat16)
+    dys = torch.randn((16, 3, 768, 768), generator=g).to(dev, torch.bfloat16)
+    cfgs["configs[4] super-resolution bf16 N=16 256x256"][1].append((lambda: (ps.forward(xs), ps.backward(dys)), 0.0))
+    for name, (dt, layers) in cfgs.items():
+        def step(layers=layers):
+            for run, _ in layers:
+                run()
+        ms = time_eager_fn(torch, step, steps, warmup)
+        fl = sum(f for _, f in layers)
+        tf = fl / (ms * 1e-3) / 1e12
+        print(json.dumps({"config": name, "dtype": dt, "ms_per_step": round(ms, 4), "gflop_per_step": round(fl / 1e9, 3),
+                          "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_TFLOPS[dt], 2)}), flush=True)
+    print(json.dumps({"config": "configs[1] Linear / square products", **gemm_secondary(torch, vnn, dev)}), flush=True)
+
+
 def gemm_secondary(torch, vnn, dev, reps=5):
     """Linear 4096x1024 -> 4096 fwd + dX + dW (+ bias) in f32 and bf16, and the
     8192^3 bf16 product; reported beside the headline (same HIP-event timing)."""
@@ -321,6 +387,9 @@ def main():
 
     if args.profile_op:
         profile_op(torch, layers, args.profile_op, args.steps)
+        return
+    if args.configs:
+        config_steps(torch, vnn, dev, args.steps, args.warmup)
         return
 
     # headline: the training step (forward, then dX and dW in reverse layer
