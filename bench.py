@@ -9,9 +9,10 @@ input gradient and weight gradient of every layer (dY ~ N(0,1) injected).
 Inputs are synthetic and resident in HBM before timing starts.
 
 Prints ONE JSON line (driver contract).  `value` is whole-job TFLOP/s of the
-step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass) over K steps issued on one
-stream: forward of every layer, then input and weight gradients in reverse
-layer order (the order of a training step).  The same step captured in a HIP
+step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass) over K steps: forward of
+every layer, then input and weight gradients in reverse layer order (the order
+of a training step), each weight gradient on a second stream next to the
+input-gradient chain (--one-stream: all on one stream).  The same step captured in a HIP
 graph gives `graph_ms_per_step`; each pass alone gives `per_op_ms`.  `roofline` is for the
 dominant pass, timed with HIP events on the stream it runs on (graph of 10
 calls of that pass alone).
@@ -68,6 +69,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--one-stream", action="store_true",
+                    help="issue the whole step on one stream (default: each layer's weight gradient on a "
+                         "second stream next to the input-gradient chain)")
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, time a fwd+bwd step of every BASELINE config "
                          "(one JSON line each)")
@@ -99,9 +103,11 @@ def build_layers(torch, vnn, dev):
 def make_train_step(torch, layers, side=None):
     """One training step of the block in dependency order: forward L0..L3, then
     backward L3..L0 (input gradient, then weight gradient, of each layer).  With
-    `side` the weight gradients run on that second stream next to the input
-    gradient chain; on MI355X the kernels each fill the chip, so the overlap
-    buys nothing and the default is one stream."""
+    `side` each layer's weight gradient runs on that second stream, started once
+    its output gradient exists (after the input gradient of the layer above), next
+    to the input-gradient chain -- the usual dW / dX overlap of a training step;
+    the split-K reductions and block tails of one pass then share the chip with
+    the next pass."""
 
     def step():
         main = torch.cuda.current_stream()
@@ -395,7 +401,7 @@ def main():
     # headline: the training step (forward, then dX and dW in reverse layer
     # order) issued eagerly on one stream, K steps between HIP events; the same
     # step captured in one HIP graph is timed too (graph_ms_per_step)
-    train_step = make_train_step(torch, layers)
+    train_step = make_train_step(torch, layers, None if args.one_stream else torch.cuda.Stream())
     graph_ms = time_graph_step(torch, train_step, args.steps, args.warmup)
     ms_per_step = time_eager_fn(torch, train_step, args.steps, args.warmup)
     tflops = step_flops / (ms_per_step * 1e-3) / 1e12
@@ -448,7 +454,8 @@ def main():
         "pct_bf16_peak": round(100.0 * tflops / PEAK_TFLOPS["bf16"], 2),
         "roofline": roof,
         "cpu_baseline": cpu,
-        "schedule": "training step: fwd L0..L3, then dX and dW of L3..L0, eager on one stream",
+        "schedule": "training step: fwd L0..L3, then dX and dW of L3..L0, eager, "
+                    + ("one stream" if args.one_stream else "dW of each layer on a second stream"),
         "graph_ms_per_step": round(graph_ms, 4),
         "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
         "secondary": secondary,
