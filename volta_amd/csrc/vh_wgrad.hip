@@ -227,38 +227,68 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int nchunk = G * (XV >> 3);  // even by construction
   const int grp = lane >> 5, rl = lane & 31;
 
+  // Fragments of one 16-position step: the three aligned dY chunks around v0
+  // (the dY windows of the three s taps) and the x chunk of each tap row r.
+  struct Frag {
+    u32x4w cm, cz, cp, x[R];
+  };
   auto compute = [&](int st) {
     const uint16_t* dl = DYS(st) + (wo + rl) * OS + 8;
     const uint16_t* xl = XS(st) + (wc + rl) * CS;
-    // this lane group's chunk t = kk + grp as (row g, column v0)
+    // this lane group's chunk t = kk + grp as (row g, column v0); branch-free
+    // advance by 16 positions (XV is a multiple of 8, so at most two wraps)
     int g = 0, v0 = grp * 8;
-    while (v0 >= XV) {
-      v0 -= XV;
-      ++g;
-    }
-    for (int kk = 0; kk < nchunk; kk += 2) {
-      // dY windows for s = 0..2: start v0 + PW - s relative to the aligned chunk at v0
+    auto wrap = [&]() {
+      const int w1 = v0 >= XV;
+      v0 -= w1 ? XV : 0;
+      g += w1;
+      const int w2 = v0 >= XV;
+      v0 -= w2 ? XV : 0;
+      g += w2;
+    };
+    wrap();
+    auto load = [&](Frag& f) {
       const uint16_t* dr = dl + g * DP + v0;
-      const u32x4w cm = *reinterpret_cast<const u32x4w*>(dr - 8);
-      const u32x4w cz = *reinterpret_cast<const u32x4w*>(dr);
-      const u32x4w cp = *reinterpret_cast<const u32x4w*>(dr + 8);
+      const uint16_t* xr = xl + g * XP + v0;
+      f.cm = *reinterpret_cast<const u32x4w*>(dr - 8);
+      f.cz = *reinterpret_cast<const u32x4w*>(dr);
+      f.cp = *reinterpret_cast<const u32x4w*>(dr + 8);
+#pragma unroll
+      for (int r = 0; r < R; ++r) f.x[r] = *reinterpret_cast<const u32x4w*>(xr + r * XP);
+    };
+    auto mma = [&](const Frag& f) {
+      // dY windows for s = 0..2: start v0 + PW - s relative to the aligned chunk at v0
       bf16x8 af[S];
-      af[0] = __builtin_bit_cast(bf16x8, window8<8 + PW>(cm, cz, cp));
-      af[1] = __builtin_bit_cast(bf16x8, window8<7 + PW>(cm, cz, cp));
-      af[2] = __builtin_bit_cast(bf16x8, window8<6 + PW>(cm, cz, cp));
+      af[0] = __builtin_bit_cast(bf16x8, window8<8 + PW>(f.cm, f.cz, f.cp));
+      af[1] = __builtin_bit_cast(bf16x8, window8<7 + PW>(f.cm, f.cz, f.cp));
+      af[2] = __builtin_bit_cast(bf16x8, window8<6 + PW>(f.cm, f.cz, f.cp));
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const bf16x8 bx = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4w*>(xl + (g + r) * XP + v0));
+        const bf16x8 bx = __builtin_bit_cast(bf16x8, f.x[r]);
 #pragma unroll
         for (int s = 0; s < S; ++s)
           acc[r * S + s] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[s], bx, acc[r * S + s], 0, 0, 0);
       }
+    };
+    // software pipeline: the LDS reads of step kk+1 are issued before the MFMAs
+    // of step kk (the last prefetch re-reads the final step: harmless)
+    const int nkk = nchunk >> 1;  // even number of chunks: nkk >= 1
+    Frag fa, fb;
+    load(fa);
+    int kk = 0;
+    for (; kk + 2 <= nkk; kk += 2) {
       v0 += 16;
-      while (v0 >= XV) {  // XV = 8 advances two rows per 16 positions
-        v0 -= XV;
-        ++g;
+      wrap();
+      load(fb);
+      mma(fa);
+      if (kk + 2 < nkk) {
+        v0 += 16;
+        wrap();
       }
+      load(fa);
+      mma(fb);
     }
+    if (kk < nkk) mma(fa);
     if (do_bias) {
       // thread t sums quarter (t % 4) of the dY rows of o = t / 4 (gaps are zero)
       const uint16_t* drow = DYS(st) + own * OS;
