@@ -244,6 +244,10 @@ HALO_CASES = [
     (2, 16, 32, 12, 12, 1, 3, 0),    # stride 3
     (3, 48, 80, 16, 16, 1, 2, 0),    # strided 1x1: O, C not tile multiples
     (2, 32, 64, 15, 16, 1, 2, 0),    # strided 1x1: odd H (last cell row clipped)
+    (2, 64, 64, 8, 256, 3, 1, 1),    # wide rows: weight gradient over column segments
+    (1, 32, 40, 5, 200, 3, 1, 1),    # wide rows, W not a multiple of the segment width
+    (1, 16, 24, 4, 300, 3, 1, 2),    # wide rows, Q = W + 2 (bias columns past W)
+    (1, 20, 30, 6, 166, 3, 1, 0),    # wide rows, no padding, 2-element chunks
 ]
 
 

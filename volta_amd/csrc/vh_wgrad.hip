@@ -39,8 +39,12 @@ struct WgradArgs {
   float* dbias_part;   // [splits][O] or nullptr
   int N, C, H, W, O, P, Q, ph, pw;
   int G;               // output rows per K step (divides P)
-  int XV;              // x columns walked per row: W rounded up so G*XV/8 is even
-  int DP;              // LDS pitch of a dY row (elements): >= max(XV, Q) + 8
+  int XV;              // x columns walked per row and step (segment width): multiple of 8
+  int nseg;            // column segments per row (1: whole rows)
+  int HL;              // dY columns loaded left of the segment: 0 (whole rows) or 8
+  int BW;              // dY columns per row slot summed for the bias gradient (multiple of 8)
+  int RL, XL;          // dY / x elements loaded per row and step
+  int DP;              // LDS pitch of a dY row (elements)
   int XP;              // LDS pitch of an x row (elements): XV
   int OS, CS;          // LDS strides per o / per c (elements)
   int steps_per_img;   // P / G
@@ -48,8 +52,8 @@ struct WgradArgs {
   int steps_per_split;
   int V;               // elements per global load (8, 4 or 2): divides Q and W
   int cpr_dy, cpr_x;   // chunks of V elements per dY row / per x row
-  int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < Q
-  int xadv, xcadv;     // the same for x rows (columns < W)
+  int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < RL
+  int xadv, xcadv;     // the same for x rows (columns < XL)
   int dy_bytes, x_bytes, part_bytes;  // buffer ranges (< 2^31)
   int tiles_o, tiles_c, splits;       // grid = tiles_o * tiles_c * splits blocks
 };
@@ -150,9 +154,9 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   // at (g0, col0) and advance by 4V elements per item (a.dadv rows + a.cadv
   // columns, with one carry); recomputed per step instead of kept in registers
   int dg0 = 0, dc0 = sub * V;
-  while (dc0 >= a.Q) { dc0 -= a.Q; ++dg0; }
+  while (dc0 >= a.RL) { dc0 -= a.RL; ++dg0; }
   int xj0 = 0, xc0 = sub * V;
-  while (xc0 >= a.W) { xc0 -= a.W; ++xj0; }
+  while (xc0 >= a.XL) { xc0 -= a.XL; ++xj0; }
   const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
@@ -161,35 +165,42 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   // unused items), so the compiler can count outstanding loads exactly.
   auto gload = [&](int step) {
     const int n = step / a.steps_per_img;
-    const int p0 = (step - n * a.steps_per_img) * G;
+    const int rem = step - n * a.steps_per_img;
+    const int pb = rem / a.nseg;
+    const int p0 = pb * G, v0s = (rem - pb * a.nseg) * a.XV;  // first row, first x column
     // byte offsets of this step's image / first row (G divides P: all G dY rows exist)
     const int dys = dy_base_g + (n * a.O * PQ + p0 * a.Q) * 2;
     const int xso = x_base_g + (n * a.C * HW + (p0 - a.ph) * a.W) * 2;
     const int jmin = a.ph - p0, jmax = a.H + a.ph - p0;  // x rows j in [jmin, jmax) exist
+    const int dc_org = v0s - a.HL;                       // dY column of run element 0
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks;
-      rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + col) * 2 : (int)0x80000000u, 0);
+      const int cg = dc_org + col;  // a V-chunk is all inside [0, Q) or all outside
+      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks && cg >= 0 && cg < a.Q;
+      rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + cg) * 2 : (int)0x80000000u, 0);
       col += a.cadv;
-      const int wrap = col >= a.Q;
-      col -= wrap ? a.Q : 0;
+      const int wrap = col >= a.RL;
+      col -= wrap ? a.RL : 0;
       g += a.dadv + wrap;
     }
     int j = xj0;
     col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax;
-      rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + col) * 2 : (int)0x80000000u, 0);
+      const int cg = v0s + col;
+      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax && cg < a.W;
+      rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + cg) * 2 : (int)0x80000000u, 0);
       col += a.xcadv;
-      const int wrap = col >= a.W;
-      col -= wrap ? a.W : 0;
+      const int wrap = col >= a.XL;
+      col -= wrap ? a.XL : 0;
       j += a.xadv + wrap;
     }
   };
   auto sstore = [&](int st) {
-    uint16_t* d = DYS(st) + own * OS + 8;
+    // dY run element 0 (column v0s - HL) lands 8 - HL elements into the row's
+    // slot, so column v0s is always at slot + 8
+    uint16_t* d = DYS(st) + own * OS + (8 - a.HL);
     uint16_t* xs = XS(st) + own * CS;
     uint16_t* sink = smem + 2 * stage;  // 16 bytes past both stages
     int g = dg0, col = dc0;
@@ -198,8 +209,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
       uint16_t* dst = sub + 4 * it < dy_chunks ? d + g * DP + col : sink;
       *reinterpret_cast<VT*>(dst) = rdy[it];
       col += a.cadv;
-      const int wrap = col >= a.Q;
-      col -= wrap ? a.Q : 0;
+      const int wrap = col >= a.RL;
+      col -= wrap ? a.RL : 0;
       g += a.dadv + wrap;
     }
     int j = xj0;
@@ -209,8 +220,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
       uint16_t* dst = sub + 4 * it < x_chunks ? xs + j * XP + col : sink;
       *reinterpret_cast<VT*>(dst) = rx[it];
       col += a.xcadv;
-      const int wrap = col >= a.W;
-      col -= wrap ? a.W : 0;
+      const int wrap = col >= a.XL;
+      col -= wrap ? a.XL : 0;
       j += a.xadv + wrap;
     }
   };
@@ -290,10 +301,13 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     }
     if (kk < nkk) mma(fa);
     if (do_bias) {
-      // thread t sums quarter (t % 4) of the dY rows of o = t / 4 (gaps are zero)
-      const uint16_t* drow = DYS(st) + own * OS;
-      const int q4 = OS >> 2, beg = sub * q4, end = sub == 3 ? OS : beg + q4;
-      for (int k = beg; k < end; ++k) dbias += bf16_to_f32(drow[k]);
+      // thread t sums quarter (t % 4) of the columns [8, 8 + BW) of every dY row
+      // slot of o = t / 4: the step's own dY columns (past Q they hold zeros;
+      // the halo columns of a segment belong to its neighbours)
+      const uint16_t* drow = DYS(st) + own * OS + 8;
+      const int q4 = a.BW >> 2, beg = sub * q4;
+      for (int gg = 0; gg < G; ++gg)
+        for (int k = beg; k < beg + q4; ++k) dbias += bf16_to_f32(drow[gg * DP + k]);
     }
   };
 
@@ -388,42 +402,66 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
   a.V = 8;
   while (a.V > 1 && ((Q % a.V) || (W % a.V))) a.V >>= 1;
   if (a.V < 2) return false;
-  a.cpr_dy = Q / a.V;
-  a.cpr_x = W / a.V;
-  a.dadv = 4 * a.V / Q;
-  a.cadv = 4 * a.V % Q;
-  a.xadv = 4 * a.V / W;
-  a.xcadv = 4 * a.V % W;
-  // Largest row count G dividing P whose two LDS stages fit in 160 KB.
+
+  // Whole rows if they fit (the largest row count G dividing P whose two LDS
+  // stages fit in 160 KB), else column segments of 128, 64, 32 or 16 x columns
+  // (dY loaded with 8 columns on either side), choosing the segment width and
+  // G with the fewest loaded elements per output position.
   a.G = 0;
-  for (int g = P; g >= 1; --g) {
-    if (P % g) continue;
-    int xv = (W + 7) / 8 * 8;
-    if ((g * (xv / 8)) & 1) xv += 8;  // chunks per step pair up into 16-deep MFMA steps
-    const int dp = std::max(xv, (Q + 7) / 8 * 8) + 8;
-    int os = 8 + g * dp;
-    if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
-    int cs = (g + R - 1) * xv;
-    if (((cs / 8) & 1) == 0) cs += 8;
-    const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2 + 16;  // + sink for unused items
-    const int nd = (g * a.cpr_dy + 3) / 4, nx = ((g + R - 1) * a.cpr_x + 3) / 4;
-    // load items per thread held in VGPRs (16 at most)
-    const int max_items = 16;
-    if (lds <= 160 * 1024 && nd <= max_items && nx <= max_items) {
+  const int wfull = (W + 7) / 8 * 8, span = std::max(W, Q);
+  const int seg_w[] = {wfull, 128, 64, 32, 16};
+  double best = 1e30;
+  for (int si = 0; si < 5; ++si) {
+    const int sw = seg_w[si];
+    const bool whole = si == 0;
+    if (!whole && (a.G != 0 && a.HL == 0)) break;  // whole rows fit
+    if (!whole && sw >= wfull) continue;
+    for (int g = P; g >= 1; --g) {
+      if (P % g) continue;
+      int xv = sw;
+      if ((g * (xv / 8)) & 1) {
+        if (!whole) continue;         // segment widths are fixed: need an even chunk count
+        xv += 8;                      // whole rows: one zero chunk more
+      }
+      const int hl = whole ? 0 : 8;
+      const int rl = whole ? Q : xv + 16, xl = whole ? W : xv;
+      if (rl % a.V || xl % a.V) continue;
+      const int dp = whole ? std::max(xv, (Q + 7) / 8 * 8) + 8 : xv + 16;
+      int os = whole ? 8 + g * dp : g * dp;
+      if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
+      int cs = (g + R - 1) * xv;
+      if (((cs / 8) & 1) == 0) cs += 8;
+      const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2 + 16;  // + sink for unused items
+      const int nd = (g * (rl / a.V) + 3) / 4, nx = ((g + R - 1) * (xl / a.V) + 3) / 4;
+      if (lds > 160 * 1024 || nd > 16 || nx > 16) continue;
+      const double cost = double(g * rl + (g + R - 1) * xl) / double(g * xv);
+      if (!whole && cost >= best) continue;
+      best = cost;
       a.G = g;
       a.XV = xv;
       a.XP = xv;
       a.DP = dp;
       a.OS = os;
       a.CS = cs;
+      a.HL = hl;
+      a.RL = rl;
+      a.XL = xl;
+      a.BW = whole ? dp - 8 : xv;
+      a.nseg = whole ? 1 : (span + xv - 1) / xv;
       pl.lds = lds;
       pl.nd = nd;
       pl.nx = nx;
-      break;
+      if (whole) break;  // largest G
     }
   }
   if (a.G == 0) return false;
-  a.steps_per_img = P / a.G;
+  a.cpr_dy = a.RL / a.V;
+  a.cpr_x = a.XL / a.V;
+  a.dadv = 4 * a.V / a.RL;
+  a.cadv = 4 * a.V % a.RL;
+  a.xadv = 4 * a.V / a.XL;
+  a.xcadv = 4 * a.V % a.XL;
+  a.steps_per_img = P / a.G * a.nseg;
   a.total_steps = N * a.steps_per_img;
   pl.tiles_o = (O + 63) / 64;
   pl.tiles_c = (C + 63) / 64;
