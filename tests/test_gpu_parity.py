@@ -248,6 +248,10 @@ HALO_CASES = [
     (1, 32, 40, 5, 200, 3, 1, 1),    # wide rows, W not a multiple of the segment width
     (1, 16, 24, 4, 300, 3, 1, 2),    # wide rows, Q = W + 2 (bias columns past W)
     (1, 20, 30, 6, 166, 3, 1, 0),    # wide rows, no padding, 2-element chunks
+    (2, 27, 32, 16, 16, 3, 1, 1),    # C not a multiple of 16: partial last channel group (forward)
+    (2, 32, 27, 12, 12, 3, 1, 1),    # O = 27: partial channel group in the input gradient
+    (2, 3, 64, 20, 24, 5, 1, 2),     # 3 input channels, 5x5: one partial group, one LDS stage
+    (1, 5, 20, 8, 10, 3, 1, 1),      # C = 5 forward; input gradient over 20 = 16 + 4 channels
 ]
 
 
@@ -310,7 +314,8 @@ def test_conv_transpose2d_fwd_bwd(case, dt):
 
 # ------------------------------------------------------------------ PixelShuffle
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
-@pytest.mark.parametrize("shape", [(2, 27, 8, 9, 3), (1, 12, 4, 4, 2), (2, 3, 5, 7, 1)])
+@pytest.mark.parametrize("shape", [(2, 27, 8, 9, 3), (1, 12, 4, 4, 2), (2, 3, 5, 7, 1), (3, 18, 5, 24, 3),
+                                   (2, 48, 6, 16, 4), (1, 8, 3, 8, 2)])
 def test_pixel_shuffle_exact(shape, dt):
     B, CR, H, W, r = shape
     g = rng(CR)

@@ -185,7 +185,9 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
-  const size_t wbytes = (size_t)d.O * d.C * RS * elem_size(dt);
+  // weight staging: the generic layout, or the halo kernel's channel-grouped one (padded to 16 channels)
+  const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
+                                 halo_conv_bf16_ws((int)d.C, (int)d.O, (int)d.KH, (int)d.KW));
   IgemmPlan p{};
   p.dtype = dt;
   p.akind = KD_DENSE_K;
@@ -224,7 +226,8 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
 static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st) {
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
-  const size_t wbytes = (size_t)d.O * d.C * RS * elem_size(dt);
+  const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
+                                 halo_conv_bf16_ws((int)d.O, (int)d.C, (int)d.KH, (int)d.KW));
   IgemmPlan p{};
   p.dtype = dt;
   p.akind = KD_DENSE_K;

@@ -91,10 +91,10 @@ __device__ __forceinline__ int xcd_block(int nb) {
 // store(i, sum) writes the result.
 template <typename Store>
 __device__ __forceinline__ void reduce_splits_block(const float* __restrict__ part, int splits, long total,
-                                                    Store store) {
+                                                    Store store, int blk, int nblk) {
   __shared__ float red[4][64];
   const int j = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (long base = (long)blockIdx.x * 64; base < total; base += (long)gridDim.x * 64) {
+  for (long base = (long)blk * 64; base < total; base += (long)nblk * 64) {
     const long i = base + j;
     float s = 0.f;
     if (i < total) {
@@ -106,6 +106,12 @@ __device__ __forceinline__ void reduce_splits_block(const float* __restrict__ pa
     if (w == 0 && i < total) store(i, ((red[0][j] + red[1][j]) + red[2][j]) + red[3][j]);
     __syncthreads();
   }
+}
+
+template <typename Store>
+__device__ __forceinline__ void reduce_splits_block(const float* __restrict__ part, int splits, long total,
+                                                    Store store) {
+  reduce_splits_block(part, splits, total, store, (int)blockIdx.x, (int)gridDim.x);
 }
 
 inline int reduce_splits_grid(long total) { return (int)std::min<long>((total + 63) / 64, 1L << 20); }

@@ -46,6 +46,7 @@ struct HaloArgs {
   int y_bytes;           // size of y in bytes (< 2^31)
   int w_bytes;           // size of wt in bytes
   int tiles_m, tiles_o;  // grid = tiles_m * tiles_o blocks
+  int stages;            // LDS stages (1 when there is a single channel group)
   FastDiv fPQ, fQ;
   FastDiv fW2, fRowsMax, fHp;  // item decomposition (W/2, rows_max, Hp)
 };
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // half-plane, ext row) the columns [0, pw) and [W + pw, Wp)
   const u32x4 z = {0u, 0u, 0u, 0u};
   const int padc = Wp - a.W;
-  for (int i = tid; i < 4 * a.rows_max; i += 256) {
+  for (int i = tid; i < 2 * a.stages * a.rows_max; i += 256) {
     uint32_t sh, e;
     a.fRowsMax.divmod((uint32_t)i, sh, e);
     u32x4* rowp = lds + (sh >> 1) * stage + w_units + (sh & 1) * cells + e * Wp;
@@ -193,12 +194,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int it = 0; it < Cfg::WITER; ++it)
       wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_goff[it], c0 * OG2, 0));
+    if (c0 + 16 <= a.C) {
 #pragma unroll
-    for (int it = 0; it < Cfg::XITER; ++it) {
-      // invalid items carry an out-of-range offset: the buffer load returns 0
+      for (int it = 0; it < Cfg::XITER; ++it) {
+        // invalid items carry an out-of-range offset: the buffer load returns 0
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
+        for (int j = 0; j < 8; ++j)
+          xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
+      }
+    } else {
+      // last, partial channel group (C not a multiple of 16): channels past C
+      // load as zero (their padded weights are zero too); the upper half-plane
+      // items (LDS offset >= cells) hold channels c0 + 8 + j
+#pragma unroll
+      for (int it = 0; it < Cfg::XITER; ++it) {
+        const int lim = a.C - c0 - (x_loff[it] >= cells ? 8 : 0);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          xreg[sI][it][j] =
+              __builtin_amdgcn_raw_buffer_load_b32(xrsrc, j < lim ? x_voff[it] : (int)0x80000000u, (c0 + j) * HW2, 0);
+      }
     }
   };
   auto sstore = [&](auto SET, int st) {
@@ -261,7 +276,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // even kt: buffer 0 holds group kt, register set 1 holds group kt+1 (in
   // flight), set 0 is free.  The steady-state loop issues its loads without
   // conditions so that each wait covers only the older register set.
-  const int nk = a.C / 16;
+  const int nk = (a.C + 15) / 16;
   if constexpr (DEPTH == 2) {
     gload(I0{}, 0);
     if (nk > 1) gload(I1{}, 16);
@@ -401,13 +416,14 @@ int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
 
 // Returns VH_ERR_UNSUPPORTED (without launching) when the shape is outside what
 // the halo kernel handles; the caller then uses the generic implicit GEMM.
-size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)C * O * R * S * 2; }
+size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)((C + 15) / 16 * 16) * O * R * S * 2; }
 
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
                    int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st) {
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0) return VH_ERR_UNSUPPORTED;
-  if ((C % 16) != 0 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
+  if (C < 1 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
+  const int nk = (C + 15) / 16, Cp = nk * 16;  // channel groups; weights padded with zeros to Cp
   if (!((R == 3 && S == 3) || (R == 5 && S == 5) || (R == 1 && S == 1))) return VH_ERR_UNSUPPORTED;
   const void* wt = ws;
   HaloArgs a;
@@ -427,7 +443,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   const long yb_ = (long)N * O * P * Q * 2;
   if (yb_ >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.y_bytes = (int)yb_;
-  const long wb = (long)O * R * S * C * 2;
+  const long wb = (long)O * R * S * Cp * 2;
   if (wb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.w_bytes = (int)wb;
   a.fW2 = FastDiv((uint32_t)(W / 2));
@@ -449,7 +465,8 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
       rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
     }
     const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2) * 16;
-    lds = 2 * stage;
+    a.stages = nk == 1 ? 1 : 2;  // a single channel group needs no second buffer
+    lds = a.stages * stage;
     const bool fits = lds <= 160 * 1024 && (2 * rows_max * (W / 2) + 255) / 256 <= 8;
     if (fits) break;
     if (WM == 2 || O <= 64) return VH_ERR_UNSUPPORTED;

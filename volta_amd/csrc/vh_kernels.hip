@@ -133,15 +133,12 @@ __global__ __launch_bounds__(256) void direct_wgrad_kernel(const typename Elem<T
   if (threadIdx.x == 0) part[(long)blockIdx.y * gridDim.x + widx] = red[0] + red[1] + red[2] + red[3];
 }
 
-// Sum of partials [splits][n] -> out[n] (dtype T), fixed order.
+// Sum of partials [splits][n] -> out[n] (dtype T), fixed order (four waves
+// over interleaved splits, then the wave sums in order).
 template <typename T>
 __global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restrict__ part, int splits, long n,
                                                            typename Elem<T>::storage* __restrict__ out) {
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
-    float s = 0.f;
-    for (int z = 0; z < splits; ++z) s += part[(long)z * n + i];
-    out[i] = Elem<T>::from_f32(s);
-  }
+  reduce_splits_block(part, splits, n, [&](long i, float s) { out[i] = Elem<T>::from_f32(s); });
 }
 
 // ============================================================== pad / im2col / col2im
@@ -322,7 +319,8 @@ __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::s
 __global__ __launch_bounds__(256) void relayout_grouped_kernel(const uint16_t* __restrict__ src,
                                                                uint16_t* __restrict__ dst, int M, int K, int RS,
                                                                int mode, FastDiv fRS, FastDiv fM) {
-  const uint32_t total = (uint32_t)M * K * RS;
+  // K is padded to whole groups of 16; the padding channels are zero
+  const uint32_t total = (uint32_t)M * ((K + 15) & ~15) * RS;
   for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < total; d += gridDim.x * 256u) {
     const uint32_t i = d & 15u, t = d >> 4;
     uint32_t t2, tap, kg, m;
@@ -331,13 +329,12 @@ __global__ __launch_bounds__(256) void relayout_grouped_kernel(const uint16_t* _
     const uint32_t k = kg * 16u + i;
     const uint32_t s = mode == 0 ? (m * (uint32_t)K + k) * RS + tap
                                  : (k * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap);
-    dst[d] = src[s];
+    dst[d] = k < (uint32_t)K ? src[s] : (uint16_t)0;
   }
 }
 
 int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st) {
-  if (K % 16 != 0) return set_error(VH_ERR_UNSUPPORTED, "grouped weight layout needs 16 | K");
-  relayout_grouped_kernel<<<grid_for((long)M * K * RS), 256, 0, st>>>(
+  relayout_grouped_kernel<<<grid_for((long)M * ((K + 15) / 16 * 16) * RS), 256, 0, st>>>(
       (const uint16_t*)w, (uint16_t*)dst, M, K, RS, mode, FastDiv((uint32_t)RS), FastDiv((uint32_t)M));
   VH_LAUNCH_CHECK();
   return VH_OK;
@@ -381,6 +378,53 @@ __global__ __launch_bounds__(256) void channel_sum_kernel(const typename Elem<T>
   if (threadIdx.x == 0) part[(long)blockIdx.y * C + c] = red[0] + red[1] + red[2] + red[3];
 }
 
+typedef unsigned int u32x4w __attribute__((ext_vector_type(4)));
+
+// Sum of the elements of a 16-byte chunk (8 bf16 or 4 f32), in element order.
+template <typename T>
+__device__ __forceinline__ float vec_sum(const u32x4w v);
+template <>
+__device__ __forceinline__ float vec_sum<bf16>(const u32x4w v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += __uint_as_float(v[i] << 16);
+    s += __uint_as_float(v[i] & 0xffff0000u);
+  }
+  return s;
+}
+template <>
+__device__ __forceinline__ float vec_sum<float>(const u32x4w v) {
+  return ((__uint_as_float(v[0]) + __uint_as_float(v[1])) + __uint_as_float(v[2])) + __uint_as_float(v[3]);
+}
+
+// Per-channel sum, planes of whole 16-byte chunks (HW a multiple of 16 bytes):
+// block (c, n, hs) adds slice hs of plane (n, c) -> partial[n * hsl + hs][C].
+template <typename T>
+__global__ __launch_bounds__(256) void channel_sum_planes_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                                 int C, int HWv, int hsl,
+                                                                 float* __restrict__ part) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  const int c = blockIdx.x, n = blockIdx.y, hs = blockIdx.z;
+  const int per = (HWv + hsl - 1) / hsl;
+  const int b = hs * per, e = min(HWv, b + per);
+  const u32x4w* src = reinterpret_cast<const u32x4w*>(x + ((long)n * C + c) * HWv * VE);
+  float s0 = 0.f, s1 = 0.f;
+  int k = b + threadIdx.x;
+  for (; k + 256 < e; k += 512) {
+    const u32x4w v0 = src[k], v1 = src[k + 256];
+    s0 += vec_sum<T>(v0);
+    s1 += vec_sum<T>(v1);
+  }
+  if (k < e) s0 += vec_sum<T>(src[k]);
+  float s = wave_sum(s0 + s1);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[((long)n * hsl + hs) * C + c] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 // Column sums of a row-major [M][N] matrix -> partial[split][N]; lanes walk columns.
 template <typename T>
 __global__ __launch_bounds__(256) void column_sum_kernel(const typename Elem<T>::storage* __restrict__ x, int M,
@@ -419,6 +463,52 @@ __global__ __launch_bounds__(256) void pixel_shuffle_kernel(const typename Elem<
       int ii = rr / r, jj = rr - ii * r;
       out[i] = in[(bc * HO + (long)h * r + ii) * WO + (long)w * r + jj];
     }
+  }
+}
+
+// Vectorised pixel shuffle for r in 2..4 and W a multiple of VE = 16 / sizeof(S):
+// work item (b, c, ho, w0) covers VE input columns w0.. of the r input rows that
+// output row ho interleaves (channels (c*r + ho%r)*r + j, row ho/r), i.e. VE*r
+// contiguous output elements.  Forward reads the r input chunks and writes the
+// interleaved run; backward reads the run and writes the r chunks.
+template <typename T, int R>
+__global__ __launch_bounds__(256) void pixel_shuffle_vec_kernel(const typename Elem<T>::storage* __restrict__ in,
+                                                                typename Elem<T>::storage* __restrict__ out,
+                                                                int H, int W, int items, int backward) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  const int item = blockIdx.x * 256 + threadIdx.x;
+  if (item >= items) return;
+  const int wv = W / VE, HO = H * R, WO = W * R;
+  const int w0 = (item % wv) * VE;
+  const int row = item / wv;  // (b*C + c) * HO + ho
+  const int ho = row % HO, bc = row / HO;
+  const int h = ho / R, ii = ho - h * R;
+  // input-side plane of channel (c*R + ii)*R + j at row h: bc*R*R + ii*R + j
+  const long in0 = ((long)(bc * R + ii) * R) * H * W + (long)h * W + w0;
+  const long o0 = (long)row * WO + (long)w0 * R;
+  S chunk[R][VE];
+  S run[R * VE];
+  if (!backward) {
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      *reinterpret_cast<u32x4w*>(chunk[j]) = *reinterpret_cast<const u32x4w*>(in + in0 + (long)j * H * W);
+#pragma unroll
+    for (int k = 0; k < R * VE; ++k) run[k] = chunk[k % R][k / R];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      *reinterpret_cast<u32x4w*>(out + o0 + j * VE) = *reinterpret_cast<const u32x4w*>(run + j * VE);
+  } else {
+    // in = output-shaped gradient, out = input-shaped gradient
+    const long r0 = o0, c0 = in0;
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      *reinterpret_cast<u32x4w*>(run + j * VE) = *reinterpret_cast<const u32x4w*>(in + r0 + j * VE);
+#pragma unroll
+    for (int k = 0; k < R * VE; ++k) chunk[k % R][k / R] = run[k];
+#pragma unroll
+    for (int j = 0; j < R; ++j)
+      *reinterpret_cast<u32x4w*>(out + c0 + (long)j * H * W) = *reinterpret_cast<const u32x4w*>(chunk[j]);
   }
 }
 
@@ -461,7 +551,7 @@ int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g,
   dim3 grid((unsigned)nw, (unsigned)slices);
   direct_wgrad_kernel<T><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
   VH_LAUNCH_CHECK();
-  sum_partials_kernel<T><<<grid_for(nw), 256, 0, st>>>(ws, slices, nw, (S*)dw);
+  sum_partials_kernel<T><<<reduce_splits_grid(nw), 256, 0, st>>>(ws, slices, nw, (S*)dw);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -539,19 +629,42 @@ int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hip
   return VH_OK;
 }
 
+// Slices per plane for the plane-vectorised channel sum (0: not applicable):
+// about 4096 blocks in all, each slice at least 1024 chunks of 16 bytes.
+static int channel_sum_plane_slices(int N, int C, int HW, size_t esize) {
+  const int ve = (int)(16 / esize);
+  if (HW % ve || N < 1 || N > 65535 || (long)N * C * HW >= (1L << 31)) return 0;
+  const int hwv = HW / ve;
+  const long blocks = (long)N * C;
+  int hsl = (int)std::max<long>(1, std::min<long>(4096 / std::max<long>(blocks, 1), hwv / 1024));
+  return std::min(hsl, 65535);
+}
+
 size_t channel_sum_ws(int N, int C, int HW, int* nslice) {
   long len = (long)N * HW;
   int s = (int)std::max<long>(1, std::min<long>(std::max<long>(1, 1024 / std::max(C, 1)), len / 4096));
+  // the plane-vectorised form keeps N * slices partials (bounded by the larger of the two)
+  const int hsl = std::max(channel_sum_plane_slices(N, C, HW, 2), channel_sum_plane_slices(N, C, HW, 4));
+  const int sp = hsl ? N * hsl : 0;
   *nslice = s;
-  return (size_t)s * C * sizeof(float);
+  return (size_t)std::max(s, sp) * C * sizeof(float);
 }
 
 template <typename T>
 int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st) {
   using S = typename Elem<T>::storage;
+  const int hsl = ((uintptr_t)x & 15) ? 0 : channel_sum_plane_slices(N, C, HW, sizeof(S));
+  if (hsl) {
+    channel_sum_planes_kernel<T><<<dim3(C, N, hsl), 256, 0, st>>>((const S*)x, C, HW / (int)(16 / sizeof(S)), hsl,
+                                                                   ws);
+    VH_LAUNCH_CHECK();
+    sum_partials_kernel<T><<<reduce_splits_grid(C), 256, 0, st>>>(ws, N * hsl, C, (S*)out);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   channel_sum_kernel<T><<<dim3(C, nslice), 256, 0, st>>>((const S*)x, N, C, HW, ws, nslice);
   VH_LAUNCH_CHECK();
-  sum_partials_kernel<T><<<grid_for(C), 256, 0, st>>>(ws, nslice, C, (S*)out);
+  sum_partials_kernel<T><<<reduce_splits_grid(C), 256, 0, st>>>(ws, nslice, C, (S*)out);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -569,7 +682,7 @@ int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice
   using S = typename Elem<T>::storage;
   column_sum_kernel<T><<<dim3((N + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
   VH_LAUNCH_CHECK();
-  sum_partials_kernel<T><<<grid_for(N), 256, 0, st>>>(ws, nslice, N, (S*)out);
+  sum_partials_kernel<T><<<reduce_splits_grid(N), 256, 0, st>>>(ws, nslice, N, (S*)out);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -579,6 +692,20 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
                       hipStream_t st) {
   using S = typename Elem<T>::storage;
   long total = (long)B * C * H * W * r * r;
+  constexpr int VE = 16 / sizeof(S);
+  const bool aligned = (((uintptr_t)in | (uintptr_t)out) & 15) == 0;
+  if (aligned && r >= 2 && r <= 4 && W % VE == 0 && total < (1L << 31) && total > 0) {
+    const int items = (int)((long)B * C * H * r * (W / VE));
+    const int grid = (items + 255) / 256;
+    if (r == 2)
+      pixel_shuffle_vec_kernel<T, 2><<<grid, 256, 0, st>>>((const S*)in, (S*)out, H, W, items, backward);
+    else if (r == 3)
+      pixel_shuffle_vec_kernel<T, 3><<<grid, 256, 0, st>>>((const S*)in, (S*)out, H, W, items, backward);
+    else
+      pixel_shuffle_vec_kernel<T, 4><<<grid, 256, 0, st>>>((const S*)in, (S*)out, H, W, items, backward);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   pixel_shuffle_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)in, (S*)out, C, H, W, r, total, backward);
   VH_LAUNCH_CHECK();
   return VH_OK;

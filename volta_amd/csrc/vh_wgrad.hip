@@ -363,25 +363,24 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 
 // dW[o][c][tap] = sum_z part[z][tap][o][c], bf16 out, in a fixed summation
 // order (reduce_splits_block), so the result does not depend on timing.
+// Blocks [0, nbw) reduce the dW partials, the rest the bias partials [split][O].
 __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __restrict__ part, int splits,
-                                                                int RS, int O, int C, uint16_t* __restrict__ dw) {
-  // partials are [split][tap][O][C]; dW is OIHW
-  reduce_splits_block(part, splits, (long)RS * O * C, [&](long i, float s) {
-    const int c = (int)(i % C);
-    const long t = i / C;
-    const int o = (int)(t % O);
-    const int tap = (int)(t / O);
-    dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
-  });
-}
-
-__global__ __launch_bounds__(256) void bias_reduce_bf16_kernel(const float* __restrict__ part, int splits, int O,
-                                                               uint16_t* __restrict__ db) {
-  int o = blockIdx.x * 256 + threadIdx.x;
-  if (o >= O) return;
-  float s = 0.f;
-  for (int z = 0; z < splits; ++z) s += part[(long)z * O + o];
-  db[o] = f32_to_bf16(s);
+                                                                int RS, int O, int C, uint16_t* __restrict__ dw,
+                                                                const float* __restrict__ bpart,
+                                                                uint16_t* __restrict__ db, int nbw) {
+  if ((int)blockIdx.x < nbw) {
+    // partials are [split][tap][O][C]; dW is OIHW
+    reduce_splits_block(part, splits, (long)RS * O * C, [&](long i, float s) {
+      const int c = (int)(i % C);
+      const long t = i / C;
+      const int o = (int)(t % O);
+      const int tap = (int)(t / O);
+      dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
+    }, (int)blockIdx.x, nbw);
+  } else {
+    reduce_splits_block(bpart, splits, (long)O, [&](long i, float s) { db[i] = f32_to_bf16(s); },
+                        (int)blockIdx.x - nbw, (int)gridDim.x - nbw);
+  }
 }
 
 namespace {
@@ -536,12 +535,10 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   int rc = pl.a.pw == 0 ? launch_pw<0>(pl, st) : pl.a.pw == 1 ? launch_pw<1>(pl, st) : launch_pw<2>(pl, st);
   if (rc) return rc;
   const long total = (long)R * S * O * C;
-  wgrad_reduce_bf16_kernel<<<reduce_splits_grid(total), 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw);
+  const int nbw = reduce_splits_grid(total), nbb = db ? reduce_splits_grid(O) : 0;
+  wgrad_reduce_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw, pl.a.dbias_part,
+                                                      (uint16_t*)db, nbw);
   VH_LAUNCH_CHECK();
-  if (db) {
-    bias_reduce_bf16_kernel<<<(O + 255) / 256, 256, 0, st>>>(pl.a.dbias_part, pl.splits, O, (uint16_t*)db);
-    VH_LAUNCH_CHECK();
-  }
   return VH_OK;
 }
 
