@@ -29,6 +29,12 @@
 
 namespace vh {
 
+#define VH_TRY_W(expr)          \
+  do {                          \
+    int _s = (expr);            \
+    if (_s != VH_OK) return _s; \
+  } while (0)
+
 typedef unsigned int u32x4w __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2w __attribute__((ext_vector_type(2)));
 
@@ -383,6 +389,159 @@ __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __r
   }
 }
 
+// ---------------------------------------------------------------- few input channels
+// Weight gradient for C <= 16 input channels (e.g. a first layer on RGB input),
+// where a 64-wide channel tile would be mostly empty.  v_mfma_f32_16x16x32_bf16:
+// D[o][c] (16 x 16) per tap, K = 32 x columns v of one output row p:
+//   A[o][k] = dY[o][p][v + pw - s]   (lane: o = lane % 16, k = 8 * (lane / 16) ..)
+//   B[k][c] = x[c][p + r - ph][v]    (lane: c = lane % 16, same k)
+// Operands come straight from global memory (no LDS): each lane loads the
+// aligned 8-column chunks v-8, v, v+8 of its dY row (the windows of the S taps
+// are funnel shifts of these) and the chunk v of its x channel in the R rows.
+// Wave w of a block owns o0 + 16w .. +16 and walks the block's range of K steps
+// (n, p, 32-column chunk) with the next step's loads in flight.  Partials:
+// [split][tap][O][C] and [split][O] for the bias, reduced like the row kernel's.
+// af[i] = the 8 bf16 starting START - i elements into (c0, c1, c2), i < NW
+template <int START, int NW>
+struct DyWindows {
+  __device__ static void run(bf16x8* af, const u32x4w& c0, const u32x4w& c1, const u32x4w& c2) {
+    af[0] = __builtin_bit_cast(bf16x8, window8<START>(c0, c1, c2));
+    DyWindows<START - 1, NW - 1>::run(af + 1, c0, c1, c2);
+  }
+};
+template <int START>
+struct DyWindows<START, 0> {
+  __device__ static void run(bf16x8*, const u32x4w&, const u32x4w&, const u32x4w&) {}
+};
+
+struct SmallcArgs {
+  const uint16_t* dy;  // [N][O][P][Q]
+  const uint16_t* x;   // [N][C][H][W]
+  float* part;         // [splits][RS][O][C]
+  float* dbias_part;   // [splits][O] or nullptr
+  int N, C, H, W, O, P, Q, ph;
+  int nq;              // 32-column chunks per row: ceil(max(W, Q) / 32)
+  int total_steps;     // N * P * nq
+  int steps_per_split;
+  int tiles_o;
+  int dy_bytes, x_bytes;
+};
+
+template <int R, int S, int PW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void wgrad_smallc_bf16_kernel(SmallcArgs a) {
+  static_assert(PW <= 2 && S - 1 - PW <= 2, "dY windows reach at most 2 columns either side");
+  constexpr int RS = R * S;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile_o = blockIdx.x % a.tiles_o, split = blockIdx.x / a.tiles_o;
+  const int ob = tile_o * 64 + wave * 16;  // the wave's first o
+  const int kg = lane >> 4, li = lane & 15;
+  const int o = ob + li, c = li;           // A row / B column of this lane
+  const bool o_ok = o < a.O, c_ok = c < a.C;
+  const int PQ = a.P * a.Q, HW = a.H * a.W;
+  const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  const int OOR = (int)0x80000000u;
+
+  const int step_b = split * a.steps_per_split;
+  const int step_e = min(a.total_steps, step_b + a.steps_per_split);
+  const int nsteps = step_e - step_b;  // >= 1 (splits are sized so)
+
+  struct Ops {
+    u32x4w cm, cz, cp, x[R];
+  };
+  // position of a step: (n, p, column chunk); advanced incrementally
+  int n, p, qc;
+  {
+    const int PN = a.P * a.nq;
+    n = step_b / PN;
+    const int rem = step_b - n * PN;
+    p = rem / a.nq;
+    qc = rem - p * a.nq;
+  }
+  auto load = [&](Ops& f) {
+    const int v = qc * 32 + kg * 8;  // this lane's 8 x columns v .. v+7
+    const int drow = o_ok ? ((n * a.O + o) * PQ + p * a.Q) * 2 : 0;
+    const int vm = v - 8, vp = v + 8;
+    f.cm = BufLoad<8>::ld(dyr, o_ok && vm >= 0 && vm < a.Q ? drow + vm * 2 : OOR, 0);
+    f.cz = BufLoad<8>::ld(dyr, o_ok && v < a.Q ? drow + v * 2 : OOR, 0);
+    f.cp = BufLoad<8>::ld(dyr, o_ok && vp < a.Q ? drow + vp * 2 : OOR, 0);
+    const int xrow = ((n * a.C + c) * HW + v) * 2;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int h = p - a.ph + r;
+      f.x[r] = BufLoad<8>::ld(xrr, c_ok && v < a.W && h >= 0 && h < a.H ? xrow + h * a.W * 2 : OOR, 0);
+    }
+  };
+  auto advance = [&]() {
+    ++qc;
+    const int w1 = qc == a.nq;
+    qc = w1 ? 0 : qc;
+    p += w1;
+    const int w2 = p == a.P;
+    p = w2 ? 0 : p;
+    n += w2;
+  };
+
+  f32x4 acc[RS];
+#pragma unroll
+  for (int t = 0; t < RS; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float bsum = 0.f;
+  const bool do_bias = a.dbias_part != nullptr;
+
+  auto compute = [&](const Ops& f) {
+    // dY columns v + PW - s: window start 8 + PW - s in (cm, cz, cp)
+    bf16x8 af[S];
+    DyWindows<8 + PW, S>::run(af, f.cm, f.cz, f.cp);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bf16x8 bx = __builtin_bit_cast(bf16x8, f.x[r]);
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+        acc[r * S + s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[s], bx, acc[r * S + s], 0, 0, 0);
+    }
+    if (do_bias) {
+      // every dY chunk (row p, columns v .. v+7) is some step's cz exactly once
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        bsum += __uint_as_float(f.cz[i] << 16) + __uint_as_float(f.cz[i] & 0xffff0000u);
+    }
+  };
+
+  // two operand sets: the loads of step k+1 are issued before the MFMAs of
+  // step k; the last prefetch re-reads the final step (always in range)
+  Ops fa, fb;
+  load(fa);
+  int k = 0;
+  for (; k + 2 <= nsteps; k += 2) {
+    advance();
+    load(fb);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fa);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 2 < nsteps) advance();
+    load(fa);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fb);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (k < nsteps) compute(fa);
+
+  // partials: lane holds D[o = ob + 4*kg + j][c = li]
+#pragma unroll
+  for (int t = 0; t < RS; ++t)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int oo = ob + kg * 4 + j;
+      if (oo < a.O && c_ok) a.part[(((long)split * RS + t) * a.O + oo) * a.C + c] = acc[t][j];
+    }
+  if (do_bias) {
+    bsum += __shfl_xor(bsum, 16, 64);
+    bsum += __shfl_xor(bsum, 32, 64);
+    if (kg == 0 && o_ok) a.dbias_part[(long)split * a.O + o] = bsum;
+  }
+}
+
 namespace {
 
 struct WgradPlan {
@@ -475,6 +634,43 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
   return true;
 }
 
+// Plan of the few-channel kernel: false if the shape is outside its envelope.
+bool plan_smallc(SmallcArgs& a, int N, int C, int H, int W, int O, int R, int S, int ph, int pw) {
+  const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
+  if (P <= 0 || Q <= 0 || C < 1 || C > 16 || (W % 8) || (Q % 8)) return false;
+  if (!((R == 3 && S == 3) || (R == 5 && S == 5 && pw == 2))) return false;
+  if (pw > 2 || S - 1 - pw > 2) return false;
+  const long dyb = (long)N * O * P * Q * 2, xb = (long)N * C * H * W * 2;
+  if (dyb >= (1L << 31) - 64 || xb >= (1L << 31) - 64) return false;
+  a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph;
+  a.nq = (std::max(W, Q) + 31) / 32;
+  a.total_steps = N * P * a.nq;
+  a.tiles_o = (O + 63) / 64;
+  // about two blocks per CU (about 190 VGPRs per lane: two waves per SIMD)
+  const int splits = std::max(1, std::min(a.total_steps, (512 + a.tiles_o - 1) / a.tiles_o));
+  a.steps_per_split = (a.total_steps + splits - 1) / splits;
+  a.dy_bytes = (int)dyb;
+  a.x_bytes = (int)xb;
+  return true;
+}
+
+int smallc_splits(const SmallcArgs& a) { return (a.total_steps + a.steps_per_split - 1) / a.steps_per_split; }
+
+int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
+  const dim3 grid((unsigned)(a.tiles_o * smallc_splits(a)));
+  if (R == 5) {
+    wgrad_smallc_bf16_kernel<5, 5, 2><<<grid, 256, 0, st>>>(a);
+  } else if (pw == 0) {
+    wgrad_smallc_bf16_kernel<3, 3, 0><<<grid, 256, 0, st>>>(a);
+  } else if (pw == 1) {
+    wgrad_smallc_bf16_kernel<3, 3, 1><<<grid, 256, 0, st>>>(a);
+  } else {
+    wgrad_smallc_bf16_kernel<3, 3, 2><<<grid, 256, 0, st>>>(a);
+  }
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 template <int R, int S, int PW, int V, int ND, int NX>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
   auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX>;
@@ -506,6 +702,13 @@ int launch_pw(const WgradPlan& pl, hipStream_t st) {
 }  // namespace
 
 size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, int pw, bool bias) {
+  SmallcArgs sa;
+  if (plan_smallc(sa, N, C, H, W, O, R, S, ph, pw)) {
+    const int splits = smallc_splits(sa);
+    size_t b = (size_t)splits * R * S * O * C * sizeof(float);
+    if (bias) b = ((b + 255) & ~size_t(255)) + (size_t)splits * O * sizeof(float);
+    return b;
+  }
   WgradPlan pl;
   if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return 0;
   size_t b = (size_t)pl.splits * R * S * O * C * sizeof(float);
@@ -515,10 +718,27 @@ size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, in
 
 int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, int C, int H, int W, int O, int R,
                     int S, int ph, int pw, float* ws, size_t ws_bytes, hipStream_t st) {
+  const size_t need = wgrad_rows_ws(N, C, H, W, O, R, S, ph, pw, db != nullptr);
+  if (need == 0) return VH_ERR_UNSUPPORTED;
+  if (need > ws_bytes) return set_error(VH_ERR_BAD_ARG, "wgrad workspace too small");
+  SmallcArgs sa;
+  if (plan_smallc(sa, N, C, H, W, O, R, S, ph, pw)) {
+    const int splits = smallc_splits(sa);
+    const size_t pbytes = (size_t)splits * R * S * O * C * sizeof(float);
+    sa.dy = (const uint16_t*)dy;
+    sa.x = (const uint16_t*)x;
+    sa.part = ws;
+    sa.dbias_part = db ? (float*)((char*)ws + ((pbytes + 255) & ~size_t(255))) : nullptr;
+    VH_TRY_W(launch_smallc(sa, R, S, pw, st));
+    const long total = (long)R * S * O * C;
+    const int nbw = reduce_splits_grid(total), nbb = db ? reduce_splits_grid(O) : 0;
+    wgrad_reduce_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, splits, R * S, O, C, (uint16_t*)dw, sa.dbias_part,
+                                                        (uint16_t*)db, nbw);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   WgradPlan pl;
   if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return VH_ERR_UNSUPPORTED;
-  const size_t need = wgrad_rows_ws(N, C, H, W, O, R, S, ph, pw, db != nullptr);
-  if (need > ws_bytes) return set_error(VH_ERR_BAD_ARG, "wgrad workspace too small");
   {
     const long dyb = (long)N * O * pl.a.P * pl.a.Q * 2, xb = (long)N * C * H * W * 2;
     const long pb = (long)pl.splits * R * S * O * C * 4;
