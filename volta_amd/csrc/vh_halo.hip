@@ -39,16 +39,28 @@ struct HaloArgs {
   const uint16_t* bias;  // [O] or nullptr
   uint16_t* y;           // [N][O][P][Q]
   int N, C, H, W, O, P, Q, ph, pw;
-  int Hp, Wp;            // padded input extents
-  int M;                 // N*P*Q
+  // Column strips: the output is cut into nstrips strips of TW columns; strip j
+  // of image n is "virtual image" n*nstrips + j of P x TW positions (positions
+  // past Q are computed and dropped).  One strip (TW = Q) means whole rows.
+  int TW, nstrips;
+  int Hp;                // padded input rows: H + 2*ph
+  int Wp;                // LDS cells per ext row (even): >= TW + S - 1 + cs
+  int cs;                // cell of input column strip*TW - pw (0, or 1 for strips
+                         // with pw odd: cell 0 then sits on an even input column)
+  int lcol0, lcell0;     // first loaded column pair: input column strip*TW + lcol0
+                         // goes to cell lcell0 (whole rows: 0 -> pw, padding
+                         // cells zeroed once; strips: -pw-cs -> 0, all loaded)
+  int npairs;            // column pairs loaded per ext row
+  int M;                 // N*nstrips*P*TW virtual positions
   int rows_max;          // max ext rows any block needs
   int x_bytes;           // size of x in bytes (< 2^31: buffer-load range)
   int y_bytes;           // size of y in bytes (< 2^31)
   int w_bytes;           // size of wt in bytes
   int tiles_m, tiles_o;  // grid = tiles_m * tiles_o blocks
   int stages;            // LDS stages (1 when there is a single channel group)
-  FastDiv fPQ, fQ;
-  FastDiv fW2, fRowsMax, fHp;  // item decomposition (W/2, rows_max, Hp)
+  FastDiv fPQ, fQ;              // P*TW, TW
+  FastDiv fW2, fRowsMax, fHp;   // item decomposition (Wp/2, rows_max, Hp)
+  FastDiv fStrips;              // nstrips
 };
 
 template <int R, int S, int WM, int XI>
@@ -109,17 +121,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   a.fQ.divmod(pq_b, p_b, q_b);
   const int rows = (int)n_b * a.Hp + (int)p_b + R - e_start;  // ext rows used by this block
 
-  // zero the padding columns once (never written by the loader): per (stage,
-  // half-plane, ext row) the columns [0, pw) and [W + pw, Wp)
-  const u32x4 z = {0u, 0u, 0u, 0u};
-  const int padc = Wp - a.W;
-  for (int i = tid; i < 2 * a.stages * a.rows_max; i += 256) {
-    uint32_t sh, e;
-    a.fRowsMax.divmod((uint32_t)i, sh, e);
-    u32x4* rowp = lds + (sh >> 1) * stage + w_units + (sh & 1) * cells + e * Wp;
-    for (int pc = 0; pc < padc; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
+  // whole rows: zero the padding cells once (never written by the loader):
+  // per (stage, half-plane, ext row) the cells [0, pw) and [W + pw, Wp).
+  // Strips load every cell (columns outside the image load as zeros).
+  if (a.nstrips == 1) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    const int padc = Wp - a.W;
+    for (int i = tid; i < 2 * a.stages * a.rows_max; i += 256) {
+      uint32_t sh, e;
+      a.fRowsMax.divmod((uint32_t)i, sh, e);
+      u32x4* rowp = lds + (sh >> 1) * stage + w_units + (sh & 1) * cells + e * Wp;
+      for (int pc = 0; pc < padc; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
+    }
   }
-
   // per-lane cell index of each B fragment column (fixed for the whole block)
   int bcell[FN];
 #pragma unroll
@@ -130,7 +144,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       uint32_t n, pq, p, q;
       a.fPQ.divmod((uint32_t)m, n, pq);
       a.fQ.divmod(pq, p, q);
-      cidx = ((int)n * a.Hp + (int)p - e_start) * Wp + (int)q;
+      cidx = ((int)n * a.Hp + (int)p - e_start) * Wp + (int)q + a.cs;
     }
     bcell[j] = cidx;
   }
@@ -154,11 +168,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     a.fRowsMax.divmod(t, half, e);
     int voff = (int)0x80000000u, loff = -1;
     if (half < 2u && (int)e < rows) {
-      uint32_t eg = (uint32_t)(e_start + (int)e), n, hr;
-      a.fHp.divmod(eg, n, hr);
-      int h = (int)hr - a.ph;
-      if (h >= 0 && h < a.H) voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + 2 * wi) * 2);
-      loff = (int)half * cells + (int)e * Wp + a.pw + 2 * (int)wi;
+      uint32_t eg = (uint32_t)(e_start + (int)e), vimg, hr, n, strip;
+      a.fHp.divmod(eg, vimg, hr);
+      a.fStrips.divmod(vimg, n, strip);
+      const int h = (int)hr - a.ph;
+      // input columns of the pair (even, W even: both inside or both outside)
+      const int col = (int)strip * a.TW + a.lcol0 + 2 * (int)wi;
+      if (h >= 0 && h < a.H && col >= 0 && col < a.W)
+        voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + col) * 2);
+      loff = (int)half * cells + (int)e * Wp + a.lcell0 + 2 * (int)wi;
     }
     x_voff[it] = voff;
     x_loff[it] = loff >= 0 ? loff : 2 * cells;  // unused items store to the sink
@@ -341,10 +359,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int yoff[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    uint32_t m = (uint32_t)(m0 + wn + j * 32 + (lane & 31)), n, pq;
-    a.fPQ.divmod(m, n, pq);
-    yoff[j] = (int)m < a.M ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + pq) * 2u) + (lane >> 5) * 4 * PQ2
-                           : (int)0x80000000u;
+    uint32_t m = (uint32_t)(m0 + wn + j * 32 + (lane & 31)), vimg, pq, p, ql, n, strip;
+    a.fPQ.divmod(m, vimg, pq);
+    a.fQ.divmod(pq, p, ql);
+    a.fStrips.divmod(vimg, n, strip);
+    const int q = (int)strip * a.TW + (int)ql;
+    yoff[j] = (int)m < a.M && q < a.Q
+                  ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + p * (uint32_t)a.Q + (uint32_t)q) * 2u) +
+                        (lane >> 5) * 4 * PQ2
+                  : (int)0x80000000u;
   }
   float bv[FM][16];
 #pragma unroll
@@ -404,7 +427,7 @@ int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
 
 template <int R, int S, int WM>
 int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
-  const int items = 2 * a.rows_max * (a.W / 2);
+  const int items = 2 * a.rows_max * a.npairs;
   const int xi = (items + 255) / 256;
   if (xi <= 2) return launch_halo<R, S, WM, 2>(a, lds_bytes, st);
   if (xi <= 4) return launch_halo<R, S, WM, 4>(a, lds_bytes, st);
@@ -433,10 +456,6 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.y = (uint16_t*)y;
   a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph; a.pw = pw;
   a.Hp = H + 2 * ph;  // = P + R - 1
-  a.Wp = W + 2 * pw;  // = Q + S - 1
-  a.M = N * P * Q;
-  a.fPQ = FastDiv((uint32_t)(P * Q));
-  a.fQ = FastDiv((uint32_t)Q);
   const long xb = (long)N * C * H * W * 2;
   if (xb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;  // 32-bit buffer offsets
   a.x_bytes = (int)xb;
@@ -446,31 +465,75 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   const long wb = (long)O * R * S * Cp * 2;
   if (wb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.w_bytes = (int)wb;
-  a.fW2 = FastDiv((uint32_t)(W / 2));
   a.fHp = FastDiv((uint32_t)a.Hp);
-  // 64 output channels x 256 positions per block (two blocks per CU fit in
-  // LDS for the config-3 layers); 128 x 128 only when the wider tile does not fit.
-  int WM = 1;
-  int rows_max = 0;
-  size_t lds = 0;
-  for (;; WM = 2) {
-    const int BN = (4 / WM) * 64;
-    const int BM = WM * 64;
+  a.stages = nk == 1 ? 1 : 2;  // a single channel group needs no second buffer
+
+  // Tile shape: 64 output channels x 256 positions (WM 1) or 128 x 128 (WM 2),
+  // over whole rows or over column strips of TW columns.  Preference: two
+  // blocks per CU (LDS <= 80 KB), then the fewest computed columns (strips
+  // past Q are waste), then the fewest staged input cells per block.
+  struct Cand {
+    int TW, WM, rows_max, Wp;
+    size_t lds;
+    long cols;  // virtual columns per row: nstrips * TW
+  };
+  auto eval = [&](int TW, int WM, Cand& c) {
+    const int BN = (4 / WM) * 64, BM = WM * 64;
+    const int nstrips = (Q + TW - 1) / TW;
+    const long Mv = (long)N * nstrips * P * TW;
+    if (Mv >= (1L << 31)) return false;
+    const bool whole = TW == Q;
+    const int cs = whole ? 0 : (pw & 1);
+    const int Wp = whole ? W + 2 * pw : (TW + S - 1 + cs + 1) & ~1;
+    const int npairs = whole ? W / 2 : Wp / 2;
+    const long PQv = (long)P * TW;
     // exact maximum number of ext rows over all blocks
-    rows_max = 0;
-    for (int m0 = 0; m0 < a.M; m0 += BN) {
-      int ml = std::min(m0 + BN, a.M) - 1;
-      int na = m0 / (P * Q), pa = (m0 % (P * Q)) / Q;
-      int nb = ml / (P * Q), pb = (ml % (P * Q)) / Q;
-      rows_max = std::max(rows_max, nb * a.Hp + pb + R - (na * a.Hp + pa));
+    int rows_max = 0;
+    for (long m0 = 0; m0 < Mv; m0 += BN) {
+      const long ml = std::min(m0 + BN, Mv) - 1;
+      const long ra = (m0 / PQv) * a.Hp + (m0 % PQv) / TW, rb = (ml / PQv) * a.Hp + (ml % PQv) / TW;
+      rows_max = std::max(rows_max, (int)(rb + R - ra));
     }
-    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2) * 16;
-    a.stages = nk == 1 ? 1 : 2;  // a single channel group needs no second buffer
-    lds = a.stages * stage;
-    const bool fits = lds <= 160 * 1024 && (2 * rows_max * (W / 2) + 255) / 256 <= 8;
-    if (fits) break;
-    if (WM == 2 || O <= 64) return VH_ERR_UNSUPPORTED;
+    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * Wp + 2) * 16;
+    const size_t lds = a.stages * stage;
+    if (lds > 160 * 1024 || (2 * rows_max * npairs + 255) / 256 > 8) return false;
+    c = Cand{TW, WM, rows_max, Wp, lds, (long)nstrips * TW};
+    return true;
+  };
+  Cand best{}, c{};
+  bool have = false;
+  auto better = [&](const Cand& x) {
+    // (fits two per CU, fewer virtual columns, whole rows / wider strips)
+    const bool x2 = x.lds <= 80 * 1024, b2 = best.lds <= 80 * 1024;
+    if (!have) return true;
+    if (x2 != b2) return x2;
+    if (x.cols != best.cols) return x.cols < best.cols;
+    // fewer staged input cells per block: less re-reading of halo rows
+    return x.rows_max * x.Wp < best.rows_max * best.Wp;
+  };
+  const int tws[] = {Q, 128, 64, 32};
+  for (int i = 0; i < 4; ++i) {
+    const int TW = tws[i];
+    if (i > 0 && TW >= Q) continue;
+    if (eval(TW, 1, c) && better(c)) { best = c; have = true; }
+    if (O > 64 && (!have || best.lds > 80 * 1024) && eval(TW, 2, c) && better(c)) { best = c; have = true; }
   }
+  if (!have) return VH_ERR_UNSUPPORTED;
+  const int WM = best.WM, rows_max = best.rows_max;
+  const size_t lds = best.lds;
+  a.TW = best.TW;
+  a.nstrips = (Q + a.TW - 1) / a.TW;
+  a.Wp = best.Wp;
+  a.M = N * a.nstrips * P * a.TW;
+  a.fPQ = FastDiv((uint32_t)(P * a.TW));
+  a.fQ = FastDiv((uint32_t)a.TW);
+  a.fStrips = FastDiv((uint32_t)a.nstrips);
+  const bool whole = a.nstrips == 1;
+  a.cs = whole ? 0 : (pw & 1);
+  a.lcol0 = whole ? 0 : -pw - a.cs;
+  a.lcell0 = whole ? pw : 0;
+  a.npairs = whole ? W / 2 : a.Wp / 2;
+  a.fW2 = FastDiv((uint32_t)a.npairs);
   a.rows_max = rows_max;
   a.fRowsMax = FastDiv((uint32_t)rows_max);
   VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));

@@ -119,7 +119,7 @@ __device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, co
 // Load items: thread t serves row owner t/4 (an o of the dY tile, a c of the x
 // tile) and takes that owner's chunks t%4, t%4 + 4, ...; chunk k of a dY owner
 // is row k / cpr, column (k % cpr) * V.  Offsets advance incrementally.
-template <int R, int S, int PW, int V, int ND, int NX>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG>
 __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   static_assert(R == 3 && S == 3, "3x3 windows");
   constexpr int RS = R * S;
@@ -172,8 +172,9 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   auto gload = [&](int step) {
     const int n = step / a.steps_per_img;
     const int rem = step - n * a.steps_per_img;
-    const int pb = rem / a.nseg;
-    const int p0 = pb * G, v0s = (rem - pb * a.nseg) * a.XV;  // first row, first x column
+    // first row, first x column of the step (whole rows: one segment at 0)
+    const int pb = SEG ? rem / a.nseg : rem;
+    const int p0 = pb * G, v0s = SEG ? (rem - pb * a.nseg) * a.XV : 0;
     // byte offsets of this step's image / first row (G divides P: all G dY rows exist)
     const int dys = dy_base_g + (n * a.O * PQ + p0 * a.Q) * 2;
     const int xso = x_base_g + (n * a.C * HW + (p0 - a.ph) * a.W) * 2;
@@ -182,8 +183,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      const int cg = dc_org + col;  // a V-chunk is all inside [0, Q) or all outside
-      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks && cg >= 0 && cg < a.Q;
+      const int cg = SEG ? dc_org + col : col;  // a V-chunk is all inside [0, Q) or all outside
+      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks && (!SEG || (cg >= 0 && cg < a.Q));
       rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + cg) * 2 : (int)0x80000000u, 0);
       col += a.cadv;
       const int wrap = col >= a.RL;
@@ -194,8 +195,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      const int cg = v0s + col;
-      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax && cg < a.W;
+      const int cg = SEG ? v0s + col : col;
+      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax && (!SEG || cg < a.W);
       rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + cg) * 2 : (int)0x80000000u, 0);
       col += a.xcadv;
       const int wrap = col >= a.XL;
@@ -671,9 +672,9 @@ int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
   return VH_OK;
 }
 
-template <int R, int S, int PW, int V, int ND, int NX>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
-  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX>;
+  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG>;
   static bool attr = false;
   if (!attr) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -689,8 +690,10 @@ int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
 template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
   const int n = std::max(pl.nd, pl.nx);
-  if (n <= 8) return launch_wgrad<3, 3, PW, V, 8, 8>(pl, st);
-  if (n <= 16) return launch_wgrad<3, 3, PW, V, 16, 16>(pl, st);
+  const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
+  if (n <= 8) return seg ? launch_wgrad<3, 3, PW, V, 8, 8, true>(pl, st) : launch_wgrad<3, 3, PW, V, 8, 8, false>(pl, st);
+  if (n <= 16)
+    return seg ? launch_wgrad<3, 3, PW, V, 16, 16, true>(pl, st) : launch_wgrad<3, 3, PW, V, 16, 16, false>(pl, st);
   return VH_ERR_UNSUPPORTED;
 }
 
