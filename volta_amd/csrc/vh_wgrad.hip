@@ -24,6 +24,7 @@
 // order and writes dW (OIHW).  The optional bias gradient (sum of dY over
 // positions) is accumulated by the c-tile-0 blocks from the same LDS copy of dY.
 #include <algorithm>
+#include <type_traits>
 
 #include "vh_kernels.hpp"
 
@@ -119,7 +120,7 @@ __device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, co
 // Load items: thread t serves row owner t/4 (an o of the dY tile, a c of the x
 // tile) and takes that owner's chunks t%4, t%4 + 4, ...; chunk k of a dY owner
 // is row k / cpr, column (k % cpr) * V.  Offsets advance incrementally.
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH>
 __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   static_assert(R == 3 && S == 3, "3x3 windows");
   constexpr int RS = R * S;
@@ -166,10 +167,15 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
-  VT rdy[ND], rx[NX];
+  // DEPTH register sets: with two, the loads of step k+2 are in flight while
+  // step k is multiplied and step k+1 is written to LDS
+  VT rdy[DEPTH][ND], rx[DEPTH][NX];
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, DEPTH - 1>;
   // Branch-free load / store sequences (selects, and a sink slot in LDS for
   // unused items), so the compiler can count outstanding loads exactly.
-  auto gload = [&](int step) {
+  auto gload = [&](auto SET, int step) {
+    constexpr int sI = decltype(SET)::value;
     const int n = step / a.steps_per_img;
     const int rem = step - n * a.steps_per_img;
     // first row, first x column of the step (whole rows: one segment at 0)
@@ -185,7 +191,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     for (int it = 0; it < ND; ++it) {
       const int cg = SEG ? dc_org + col : col;  // a V-chunk is all inside [0, Q) or all outside
       const bool ok = dy_own_ok && sub + 4 * it < dy_chunks && (!SEG || (cg >= 0 && cg < a.Q));
-      rdy[it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + cg) * 2 : (int)0x80000000u, 0);
+      rdy[sI][it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + cg) * 2 : (int)0x80000000u, 0);
       col += a.cadv;
       const int wrap = col >= a.RL;
       col -= wrap ? a.RL : 0;
@@ -197,14 +203,15 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
     for (int it = 0; it < NX; ++it) {
       const int cg = SEG ? v0s + col : col;
       const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax && (!SEG || cg < a.W);
-      rx[it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + cg) * 2 : (int)0x80000000u, 0);
+      rx[sI][it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + cg) * 2 : (int)0x80000000u, 0);
       col += a.xcadv;
       const int wrap = col >= a.XL;
       col -= wrap ? a.XL : 0;
       j += a.xadv + wrap;
     }
   };
-  auto sstore = [&](int st) {
+  auto sstore = [&](auto SET, int st) {
+    constexpr int sI = decltype(SET)::value;
     // dY run element 0 (column v0s - HL) lands 8 - HL elements into the row's
     // slot, so column v0s is always at slot + 8
     uint16_t* d = DYS(st) + own * OS + (8 - a.HL);
@@ -214,7 +221,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
       uint16_t* dst = sub + 4 * it < dy_chunks ? d + g * DP + col : sink;
-      *reinterpret_cast<VT*>(dst) = rdy[it];
+      *reinterpret_cast<VT*>(dst) = rdy[sI][it];
       col += a.cadv;
       const int wrap = col >= a.RL;
       col -= wrap ? a.RL : 0;
@@ -225,7 +232,7 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
       uint16_t* dst = sub + 4 * it < x_chunks ? xs + j * XP + col : sink;
-      *reinterpret_cast<VT*>(dst) = rx[it];
+      *reinterpret_cast<VT*>(dst) = rx[sI][it];
       col += a.xcadv;
       const int wrap = col >= a.XL;
       col -= wrap ? a.XL : 0;
@@ -319,23 +326,65 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   };
 
   __syncthreads();
-  if (nsteps > 0) {
-    gload(step_b);
-    __builtin_amdgcn_sched_barrier(0);
-    sstore(0);
-  }
-  __syncthreads();
-  // steady state: the next step's loads are issued before this step's MFMAs
-  // (sched_barrier keeps the compiler from sinking them to their use)
-  for (int ks = 0; ks + 1 < nsteps; ++ks) {
-    gload(step_b + ks + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(ks & 1);
-    __builtin_amdgcn_sched_barrier(0);
-    sstore((ks + 1) & 1);
+  if constexpr (DEPTH == 2) {
+    // invariant at an even ks: LDS buffer 0 holds step ks, register set 1
+    // step ks+1 (in flight), set 0 is free; the steady-state loads are
+    // unconditional so that each wait covers only the older set
+    if (nsteps > 0) {
+      gload(I0{}, step_b);
+      if (nsteps > 1) gload(I1{}, step_b + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+    }
     __syncthreads();
+    int ks = 0;
+    for (; ks + 3 < nsteps; ks += 2) {
+      gload(I0{}, step_b + ks + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(0);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I1{}, 1);
+      __syncthreads();
+      gload(I1{}, step_b + ks + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(1);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+      __syncthreads();
+    }
+    const int rem = nsteps - ks;  // 0 (no steps), 1, 2 or 3
+    if (rem == 3) gload(I0{}, step_b + ks + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (rem >= 1) compute(0);
+    if (rem >= 2) {
+      sstore(I1{}, 1);
+      __syncthreads();
+      compute(1);
+      if (rem == 3) {
+        sstore(I0{}, 0);
+        __syncthreads();
+        compute(0);
+      }
+    }
+  } else {
+    if (nsteps > 0) {
+      gload(I0{}, step_b);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+    }
+    __syncthreads();
+    // steady state: the next step's loads are issued before this step's MFMAs
+    // (sched_barrier keeps the compiler from sinking them to their use)
+    for (int ks = 0; ks + 1 < nsteps; ++ks) {
+      gload(I0{}, step_b + ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(ks & 1);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, (ks + 1) & 1);
+      __syncthreads();
+    }
+    if (nsteps > 0) compute((nsteps - 1) & 1);
   }
-  if (nsteps > 0) compute((nsteps - 1) & 1);
 #undef DYS
 #undef XS
 
@@ -672,9 +721,9 @@ int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
   return VH_OK;
 }
 
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
-  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG>;
+  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH>;
   static bool attr = false;
   if (!attr) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -691,6 +740,11 @@ template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
   const int n = std::max(pl.nd, pl.nx);
   const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
+  // two register sets when they fit (V = 8: 16-byte items, at most 6 + 6)
+  if constexpr (V == 8) {
+    if (pl.nd <= 6 && pl.nx <= 6)
+      return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2>(pl, st) : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
+  }
   if (n <= 8) return seg ? launch_wgrad<3, 3, PW, V, 8, 8, true>(pl, st) : launch_wgrad<3, 3, PW, V, 8, 8, false>(pl, st);
   if (n <= 16)
     return seg ? launch_wgrad<3, 3, PW, V, 16, 16, true>(pl, st) : launch_wgrad<3, 3, PW, V, 16, 16, false>(pl, st);
