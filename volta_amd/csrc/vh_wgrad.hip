@@ -139,7 +139,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int G = a.G, DP = a.DP, XP = a.XP, OS = a.OS, CS = a.CS;
   const int XR = G + R - 1;
   const int dy_elems = TO * OS, x_elems = TC * CS;
-  const int stage = dy_elems + x_elems;  // elements per stage
+  const int stage = dy_elems + x_elems + 8;  // elements per stage (the last 8: a sink
+                                             // for the stores of unused load items)
 #define DYS(st) (smem + (st) * stage)
 #define XS(st) (smem + (st) * stage + dy_elems)
 
@@ -167,6 +168,40 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
 
+  // Whole rows: an owner's dY run (G rows) and x run (G+2 rows) are contiguous
+  // in global memory, so item it sits at a fixed offset it*4V elements from the
+  // thread's first item; only the LDS slot of each item and, for x, its run row
+  // (whose validity moves with the step) are kept, computed once.  Unused items
+  // and owners past O / C go to the sink / load zeros.
+  constexpr int kSinkRow = 1 << 20;
+  int d_lds[SEG ? 1 : ND], x_lds[SEG ? 1 : NX], x_row[SEG ? 1 : NX];
+  const int sink_el = dy_elems + x_elems;  // the stage's sink, relative to the stage
+  if constexpr (!SEG) {
+    int g = dg0, col = dc0;
+#pragma unroll
+    for (int it = 0; it < ND; ++it) {
+      d_lds[it] = sub + 4 * it < dy_chunks ? own * OS + 8 + g * DP + col : sink_el;
+      col += a.cadv;
+      const int wrap = col >= a.RL;
+      col -= wrap ? a.RL : 0;
+      g += a.dadv + wrap;
+    }
+    int j = xj0;
+    col = xc0;
+#pragma unroll
+    for (int it = 0; it < NX; ++it) {
+      const bool ok = sub + 4 * it < x_chunks;
+      x_lds[it] = ok ? dy_elems + own * CS + j * XP + col : sink_el;
+      x_row[it] = ok && x_own_ok ? j : kSinkRow;
+      col += a.xcadv;
+      const int wrap = col >= a.XL;
+      col -= wrap ? a.XL : 0;
+      j += a.xadv + wrap;
+    }
+  }
+  const int d_voff = dy_own_ok ? dy_base_g + sub * V * 2 : (int)0x80000000u;
+  const int x_voff = x_base_g + sub * V * 2;
+
   // DEPTH register sets: with two, the loads of step k+2 are in flight while
   // step k is multiplied and step k+1 is written to LDS
   VT rdy[DEPTH][ND], rx[DEPTH][NX];
@@ -176,6 +211,23 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   // unused items), so the compiler can count outstanding loads exactly.
   auto gload = [&](auto SET, int step) {
     constexpr int sI = decltype(SET)::value;
+    if constexpr (!SEG) {
+      const int n = step / a.steps_per_img;
+      const int p0 = (step - n * a.steps_per_img) * G;
+      const int dstep = (n * a.O * PQ + p0 * a.Q) * 2;  // scalar byte offset of the dY run
+#pragma unroll
+      for (int it = 0; it < ND; ++it)
+        rdy[sI][it] = BufLoad<V>::ld(dyr, d_voff + it * 8 * V, dstep);
+      // x run row j is input row p0 - ph + j; t = byte offset of the thread's first item
+      const int rbase = p0 - a.ph;
+      const int t = x_voff + (n * a.C * HW + rbase * a.W) * 2;
+#pragma unroll
+      for (int it = 0; it < NX; ++it) {
+        const bool ok = (unsigned)(x_row[it] + rbase) < (unsigned)a.H;
+        rx[sI][it] = BufLoad<V>::ld(xrr, ok ? t + it * 8 * V : (int)0x80000000u, 0);
+      }
+      return;
+    }
     const int n = step / a.steps_per_img;
     const int rem = step - n * a.steps_per_img;
     // first row, first x column of the step (whole rows: one segment at 0)
@@ -212,11 +264,19 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   };
   auto sstore = [&](auto SET, int st) {
     constexpr int sI = decltype(SET)::value;
+    if constexpr (!SEG) {
+      uint16_t* base = smem + st * stage;
+#pragma unroll
+      for (int it = 0; it < ND; ++it) *reinterpret_cast<VT*>(base + d_lds[it]) = rdy[sI][it];
+#pragma unroll
+      for (int it = 0; it < NX; ++it) *reinterpret_cast<VT*>(base + x_lds[it]) = rx[sI][it];
+      return;
+    }
     // dY run element 0 (column v0s - HL) lands 8 - HL elements into the row's
     // slot, so column v0s is always at slot + 8
     uint16_t* d = DYS(st) + own * OS + (8 - a.HL);
     uint16_t* xs = XS(st) + own * CS;
-    uint16_t* sink = smem + 2 * stage;  // 16 bytes past both stages
+    uint16_t* sink = smem + st * stage + dy_elems + x_elems;  // the stage's sink
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
@@ -639,7 +699,7 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
       if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
       int cs = (g + R - 1) * xv;
       if (((cs / 8) & 1) == 0) cs += 8;
-      const size_t lds = 2 * (size_t)(64 * os + 64 * cs) * 2 + 16;  // + sink for unused items
+      const size_t lds = 2 * ((size_t)(64 * os + 64 * cs) + 8) * 2;  // + a 16-byte sink per stage
       const int nd = (g * (rl / a.V) + 3) / 4, nx = ((g + R - 1) * (xl / a.V) + 3) / 4;
       if (lds > 160 * 1024 || nd > 16 || nx > 16) continue;
       const double cost = double(g * rl + (g + R - 1) * xl) / double(g * xv);
