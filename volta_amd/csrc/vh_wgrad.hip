@@ -806,6 +806,9 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
       return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2>(pl, st) : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
   }
   if (n <= 8) return seg ? launch_wgrad<3, 3, PW, V, 8, 8, true>(pl, st) : launch_wgrad<3, 3, PW, V, 8, 8, false>(pl, st);
+  // whole rows: closer-fitting item counts (unused items still issue a load and a sink store)
+  if (!seg && pl.nd <= 8 && pl.nx <= 12) return launch_wgrad<3, 3, PW, V, 8, 12, false>(pl, st);
+  if (!seg && pl.nd <= 12 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 12, 16, false>(pl, st);
   if (n <= 16)
     return seg ? launch_wgrad<3, 3, PW, V, 16, 16, true>(pl, st) : launch_wgrad<3, 3, PW, V, 16, 16, false>(pl, st);
   return VH_ERR_UNSUPPORTED;
