@@ -800,10 +800,13 @@ template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
   const int n = std::max(pl.nd, pl.nx);
   const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
-  // two register sets when they fit (V = 8: 16-byte items, at most 6 + 6)
+  // two register sets when they fit (16-byte items: at most 6 + 6; 4- and
+  // 8-byte items of whole rows: 16 + 16)
   if constexpr (V == 8) {
     if (pl.nd <= 6 && pl.nx <= 6)
       return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2>(pl, st) : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
+  } else {
+    if (!seg && pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 2>(pl, st);
   }
   if (n <= 8) return seg ? launch_wgrad<3, 3, PW, V, 8, 8, true>(pl, st) : launch_wgrad<3, 3, PW, V, 8, 8, false>(pl, st);
   // whole rows: closer-fitting item counts (unused items still issue a load and a sink store)
