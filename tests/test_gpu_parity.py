@@ -145,6 +145,8 @@ CONV_CASES = [
     (2, 8, 4, 9, 9, 4, 2, 1),
     (3, 5, 7, 6, 5, 2, 3, 0),
     (1, 2, 3, 12, 12, 9, 1, 4),      # 81-tap window (element-wise weight relayout)
+    (2, 16, 24, 11, 9, 3, 2, 1),     # stride 2, 3x3: phases with 1 and 2 taps per axis, odd sizes
+    (2, 8, 16, 10, 10, 1, 2, 0),     # 1x1 stride 2: odd input phases get no taps (zeros)
 ]
 
 
@@ -290,6 +292,8 @@ CT_CASES = [
     (2, 64, 32, 8, 8, 4, 2, 1),      # config 4 inner layer shape
     (2, 16, 3, 16, 16, 4, 2, 1),     # config 4 last layer (to RGB)
     (1, 5, 6, 5, 3, 3, 2, 1),
+    (2, 8, 5, 5, 7, 3, 2, 0),        # stride 2, no padding, odd output sizes
+    (1, 4, 6, 3, 3, 5, 3, 2),        # stride 3, 5x5
 ]
 
 

@@ -221,6 +221,89 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
+// Input gradient of a strided convolution (and ConvTranspose2d's forward), one
+// stride phase at a time: input positions (a + sh*i, b + sw*j) receive only the
+// taps kh = (a + ph) mod sh + sh*t (and likewise kw), so each phase is a stride-1
+// implicit GEMM over its Rc x Sc taps with padding (a + ph - kh0) / sh, storing
+// into the phase's positions (OK_NCHW_SUB) -- 1/(sh*sw) of the MFMA work of the
+// dense tap loop, whose other taps multiply zeros. A phase without taps stores
+// zeros (plus the bias). The phases run in order on one stream, sharing one
+// workspace.
+struct DgradPhase {
+  int a, b, Hc, Wc, kh0, kw0, Rc, Sc, offa, offb;
+};
+
+static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias, void* dx, const ConvDims& d,
+                        hipStream_t st) {
+  const int SH = (int)d.SH, SW = (int)d.SW;
+  std::vector<DgradPhase> ph;
+  size_t wmax = 0, gmax = 0;
+  for (int a = 0; a < SH && a < d.H; ++a)
+    for (int b = 0; b < SW && b < d.W; ++b) {
+      DgradPhase f;
+      f.a = a;
+      f.b = b;
+      f.Hc = (int)((d.H - a + SH - 1) / SH);
+      f.Wc = (int)((d.W - b + SW - 1) / SW);
+      f.kh0 = (int)((a + d.PH) % SH);
+      f.kw0 = (int)((b + d.PW) % SW);
+      f.Rc = f.kh0 < d.KH ? (int)((d.KH - f.kh0 + SH - 1) / SH) : 0;
+      f.Sc = f.kw0 < d.KW ? (int)((d.KW - f.kw0 + SW - 1) / SW) : 0;
+      f.offa = (int)((a + d.PH - f.kh0) / SH);
+      f.offb = (int)((b + d.PW - f.kw0) / SW);
+      const long K = (long)f.Rc * f.Sc * d.O;
+      wmax = std::max(wmax, (size_t)K * d.C * elem_size(dt));
+      IgemmPlan p{};
+      p.dtype = dt;
+      p.args.M = (int)d.C;
+      p.args.N = (int)(d.B * f.Hc * f.Wc);
+      p.args.K = (int)K;
+      p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
+      gmax = std::max(gmax, igemm_prepare(p));
+      ph.push_back(f);
+    }
+  Carve cv;
+  const size_t o_w = cv.take(std::max<size_t>(wmax, 16)), o_g = cv.take(gmax);
+  void* ws;
+  VH_TRY(ws_get(st, cv.off, &ws));
+  void* wp = at(ws, o_w);
+  const int vec = dt == VH_BF16 ? 8 : 4;
+  for (const DgradPhase& f : ph) {
+    const int K = f.Rc * f.Sc * (int)d.O;
+    if (K > 0)
+      VH_TRY(VH_DISPATCH(dt, run_relayout_phase, w, wp, (int)d.O, (int)d.C, (int)d.KH, (int)d.KW, f.kh0, f.kw0,
+                         SH, SW, f.Rc, f.Sc, st));
+    IgemmPlan p{};
+    p.dtype = dt;
+    p.akind = KD_DENSE_K;
+    p.bkind = KD_CONV_DGRAD_DY;
+    p.okind = OK_NCHW_SUB;
+    p.args.M = (int)d.C;
+    p.args.N = (int)(d.B * f.Hc * f.Wc);
+    p.args.K = K;
+    p.args.g = make_geom((int)d.B, (int)d.C, f.Hc, f.Wc, (int)d.O, std::max(1, f.Rc), std::max(1, f.Sc), (int)d.HO,
+                         (int)d.WO, 1, 1, f.offa, f.offb);
+    p.args.hwo = f.Hc * f.Wc;
+    p.args.f_hwo = FastDiv((uint32_t)(f.Hc * f.Wc));
+    p.args.f_wsub = FastDiv((uint32_t)f.Wc);
+    p.args.sub_sh = SH;
+    p.args.sub_sw = SW;
+    p.args.sub_a = f.a;
+    p.args.sub_b = f.b;
+    p.args.sub_H = (int)d.H;
+    p.args.sub_W = (int)d.W;
+    p.args.d = dx;
+    p.args.bias = bias;
+    p.args.bias_mode = bias ? 1 : 0;
+    p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
+    igemm_prepare(p);
+    p.args.a = Operand{wp, std::max(K, 1), (int)d.C, (K % vec) == 0};
+    p.args.b = Operand{dy, 0, p.args.N, 0};
+    VH_TRY(run_igemm(p, (float*)at(ws, o_g), st));
+  }
+  return VH_OK;
+}
+
 // Input gradient as implicit GEMM: rows = input channels (A = weight in
 // [C][kh][kw][O] order), columns = input positions (B = gather of dY).
 static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st) {
@@ -253,11 +336,13 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
                            (int)d.KH, (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
-  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths && ((uintptr_t)dx & 3) == 0) {
+    VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
     int r = pw_conv_bf16_dgrad(dy, wd, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
+  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) return dgrad_phases(dt, dy, w, nullptr, dx, d, st);
+  VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wd, (int)(RS * d.O), (int)d.C, ((RS * d.O) % vec) == 0};
   p.args.b = Operand{dy, 0, p.args.N, 0};
@@ -847,6 +932,7 @@ int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight
   if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   // y = dgrad(dy := x; W viewed OIHW with O = in_channels, C = out_channels) + bias
+  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) return dgrad_phases(dtype, input, weight, bias, output, d, st);
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   IgemmPlan p{};

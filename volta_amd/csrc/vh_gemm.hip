@@ -80,6 +80,7 @@ int launch_typed(IgemmPlan& p, float* ws, hipStream_t st) {
   VH_COMBO(KD_DENSE_MN, KD_DENSE_MN, OK_DENSE)           // matmul backward B
   VH_COMBO(KD_DENSE_K, KD_CONV_FWD_X, OK_NCHW)           // conv fwd, convT dX
   VH_COMBO(KD_DENSE_K, KD_CONV_DGRAD_DY, OK_NCHW)        // conv dgrad, convT fwd
+  VH_COMBO(KD_DENSE_K, KD_CONV_DGRAD_DY, OK_NCHW_SUB)    // the same, one stride phase at a time
   VH_COMBO(KD_CONV_WGRAD_DY, KD_CONV_WGRAD_X, OK_WGRAD_OIHW)  // conv wgrad, convT dW
   VH_COMBO(KD_DENSE_K, KD_DENSE_K, OK_NCHW)              // im2col conv fwd
   VH_COMBO(KD_DENSE_MN, KD_CONV_FWD_X, OK_DENSE_T)       // im2col conv dcol

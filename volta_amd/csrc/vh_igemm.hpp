@@ -32,6 +32,8 @@ enum OutKind : int {
   OK_NCHW = 2,       // row = channel (M channels), col = (n, hw) over N*HWo
   OK_WGRAD_OIHW = 3, // row = o, col = (kh,kw,c) -> d[o][c][kh][kw]
   OK_PARTIAL = 4,    // fp32 ws[(z*M + row)*N + col]
+  OK_NCHW_SUB = 5,   // row = channel, col = (n, hh, ww) of one stride phase (a, b) of an
+                     // NCHW output: d[n][row][sub_sh*hh + sub_a][sub_sw*ww + sub_b]
 };
 
 // Convolution geometry (x: N,C,H,W; weight O,C,R,S; y: N,O,P,Q).
@@ -59,6 +61,8 @@ struct IgemmArgs {
   FastDiv f_hwo;     // OK_NCHW: divide by hwo
   FastDiv f_cw;      // OK_WGRAD_OIHW: divide by C (channels of the weight grad)
   int wg_c, wg_rs;   // OK_WGRAD_OIHW: C and R*S
+  int sub_sh, sub_sw, sub_a, sub_b, sub_H, sub_W;  // OK_NCHW_SUB: strides, phase, full extents
+  FastDiv f_wsub;    // OK_NCHW_SUB: divide by the phase's width
   ConvGeom g;
 };
 
@@ -284,6 +288,12 @@ __device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int co
     uint32_t n, hw;
     args.f_hwo.divmod((uint32_t)col, n, hw);
     idx = ((long)n * args.M + row) * args.hwo + hw;
+  } else if (OUT == OK_NCHW_SUB) {
+    uint32_t n, hw, hh, ww;
+    args.f_hwo.divmod((uint32_t)col, n, hw);
+    args.f_wsub.divmod(hw, hh, ww);
+    idx = (((long)n * args.M + row) * args.sub_H + args.sub_sh * (int)hh + args.sub_a) * args.sub_W +
+          args.sub_sw * (int)ww + args.sub_b;
   } else {  // OK_WGRAD_OIHW
     uint32_t rs, c;
     args.f_cw.divmod((uint32_t)col, rs, c);

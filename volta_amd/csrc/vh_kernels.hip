@@ -340,6 +340,26 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
   return VH_OK;
 }
 
+// Weights of one stride phase of an input gradient: dst[c][i][j][o] =
+// w[o][c][kh0 + sh*i][kw0 + sw*j] for i < Rc, j < Sc (the taps that reach the
+// phase's input positions), the A operand of a stride-1 implicit GEMM.
+template <typename T>
+__global__ __launch_bounds__(256) void relayout_phase_kernel(const typename Elem<T>::storage* __restrict__ w,
+                                                             typename Elem<T>::storage* __restrict__ dst, int O,
+                                                             int C, int R, int S, int kh0, int kw0, int sh, int sw,
+                                                             int Rc, int Sc) {
+  const long total = (long)C * Rc * Sc * O;
+  for (long d = (long)blockIdx.x * 256 + threadIdx.x; d < total; d += (long)gridDim.x * 256) {
+    const int o = (int)(d % O);
+    long t = d / O;
+    const int j = (int)(t % Sc);
+    t /= Sc;
+    const int i = (int)(t % Rc);
+    const int c = (int)(t / Rc);
+    dst[d] = w[(((long)o * C + c) * R + kh0 + sh * i) * S + kw0 + sw * j];
+  }
+}
+
 // Element-wise form of the same map for windows of more than 64 taps.
 template <typename T>
 __global__ __launch_bounds__(256) void relayout_simple_kernel(const typename Elem<T>::storage* __restrict__ src,
@@ -606,6 +626,18 @@ int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH
 }
 
 template <typename T>
+int run_relayout_phase(const void* w, void* dst, int O, int C, int R, int S, int kh0, int kw0, int sh, int sw,
+                       int Rc, int Sc, hipStream_t st) {
+  using E = typename Elem<T>::storage;
+  const long total = (long)C * Rc * Sc * O;
+  if (total <= 0) return VH_OK;
+  relayout_phase_kernel<T><<<grid_for(total), 256, 0, st>>>((const E*)w, (E*)dst, O, C, R, S, kh0, kw0, sh, sw,
+                                                             Rc, Sc);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
 int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip) {
   using S = typename Elem<T>::storage;
   if (RS > 64) {
@@ -726,6 +758,8 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
   template int run_col2im<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \
                              hipStream_t);                                                              \
   template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t, int);               \
+  template int run_relayout_phase<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,  \
+                                     hipStream_t);                                                      \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
   template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);
