@@ -237,7 +237,8 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
                         hipStream_t st) {
   const int SH = (int)d.SH, SW = (int)d.SW;
   std::vector<DgradPhase> ph;
-  size_t wmax = 0, gmax = 0;
+  PhaseTable tab{};
+  size_t wtot = 0, gmax = 0;
   for (int a = 0; a < SH && a < d.H; ++a)
     for (int b = 0; b < SW && b < d.W; ++b) {
       DgradPhase f;
@@ -252,7 +253,14 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
       f.offa = (int)((a + d.PH - f.kh0) / SH);
       f.offb = (int)((b + d.PW - f.kw0) / SW);
       const long K = (long)f.Rc * f.Sc * d.O;
-      wmax = std::max(wmax, (size_t)K * d.C * elem_size(dt));
+      if (tab.n == 16) return VH_ERR_UNSUPPORTED;
+      tab.kh0[tab.n] = f.kh0;
+      tab.kw0[tab.n] = f.kw0;
+      tab.rc[tab.n] = f.Rc;
+      tab.sc[tab.n] = f.Sc;
+      tab.off[tab.n] = (long)(wtot / elem_size(dt));
+      ++tab.n;
+      wtot += round_bytes((size_t)K * d.C * elem_size(dt));
       IgemmPlan p{};
       p.dtype = dt;
       p.args.M = (int)d.C;
@@ -263,16 +271,16 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
       ph.push_back(f);
     }
   Carve cv;
-  const size_t o_w = cv.take(std::max<size_t>(wmax, 16)), o_g = cv.take(gmax);
+  const size_t o_w = cv.take(std::max<size_t>(wtot, 16)), o_g = cv.take(gmax);
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
-  void* wp = at(ws, o_w);
+  VH_TRY(VH_DISPATCH(dt, run_relayout_phase, w, at(ws, o_w), (int)d.O, (int)d.C, (int)d.KH, (int)d.KW, SH, SW, tab,
+                     st));
   const int vec = dt == VH_BF16 ? 8 : 4;
-  for (const DgradPhase& f : ph) {
+  for (size_t pi = 0; pi < ph.size(); ++pi) {
+    const DgradPhase& f = ph[pi];
     const int K = f.Rc * f.Sc * (int)d.O;
-    if (K > 0)
-      VH_TRY(VH_DISPATCH(dt, run_relayout_phase, w, wp, (int)d.O, (int)d.C, (int)d.KH, (int)d.KW, f.kh0, f.kw0,
-                         SH, SW, f.Rc, f.Sc, st));
+    const void* wp = at(ws, o_w + (size_t)tab.off[pi] * elem_size(dt));
     IgemmPlan p{};
     p.dtype = dt;
     p.akind = KD_DENSE_K;
@@ -341,7 +349,10 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
     int r = pw_conv_bf16_dgrad(dy, wd, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
-  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) return dgrad_phases(dt, dy, w, nullptr, dx, d, st);
+  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) {
+    int r = dgrad_phases(dt, dy, w, nullptr, dx, d, st);  // unsupported only beyond 16 phases
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wd, (int)(RS * d.O), (int)d.C, ((RS * d.O) % vec) == 0};
@@ -932,7 +943,10 @@ int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight
   if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   // y = dgrad(dy := x; W viewed OIHW with O = in_channels, C = out_channels) + bias
-  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) return dgrad_phases(dtype, input, weight, bias, output, d, st);
+  if ((d.SH > 1 || d.SW > 1) && g_fast_paths) {
+    int r = dgrad_phases(dtype, input, weight, bias, output, d, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   IgemmPlan p{};

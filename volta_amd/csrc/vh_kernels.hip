@@ -340,23 +340,31 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
   return VH_OK;
 }
 
-// Weights of one stride phase of an input gradient: dst[c][i][j][o] =
-// w[o][c][kh0 + sh*i][kw0 + sw*j] for i < Rc, j < Sc (the taps that reach the
-// phase's input positions), the A operand of a stride-1 implicit GEMM.
+// Weights of the stride phases of an input gradient, all phases in one pass:
+// phase (a, b) (its first taps kh0 = (a + ph) mod sh, kw0 = (b + pw) mod sw)
+// gets dst[c][i][j][o] = w[o][c][kh0 + sh*i][kw0 + sw*j] for the Rc x Sc taps
+// that reach its input positions -- the A operand of a stride-1 implicit GEMM.
+// Phases are stored one after another (offsets in the table).  Tap (kh, kw)
+// belongs to the phase with kh0 = kh mod sh, kw0 = kw mod sw (at most one), so
+// the pass walks w once and scatters each element to its phase.
 template <typename T>
 __global__ __launch_bounds__(256) void relayout_phase_kernel(const typename Elem<T>::storage* __restrict__ w,
                                                              typename Elem<T>::storage* __restrict__ dst, int O,
-                                                             int C, int R, int S, int kh0, int kw0, int sh, int sw,
-                                                             int Rc, int Sc) {
-  const long total = (long)C * Rc * Sc * O;
-  for (long d = (long)blockIdx.x * 256 + threadIdx.x; d < total; d += (long)gridDim.x * 256) {
-    const int o = (int)(d % O);
-    long t = d / O;
-    const int j = (int)(t % Sc);
-    t /= Sc;
-    const int i = (int)(t % Rc);
-    const int c = (int)(t / Rc);
-    dst[d] = w[(((long)o * C + c) * R + kh0 + sh * i) * S + kw0 + sw * j];
+                                                             int C, int R, int S, int sh, int sw, PhaseTable tab) {
+  const long total = (long)O * C * R * S;
+  for (long s_ = (long)blockIdx.x * 256 + threadIdx.x; s_ < total; s_ += (long)gridDim.x * 256) {
+    const int kw = (int)(s_ % S);
+    long t = s_ / S;
+    const int kh = (int)(t % R);
+    t /= R;
+    const int c = (int)(t % C);
+    const int o = (int)(t / C);
+    for (int pi = 0; pi < tab.n; ++pi) {
+      const int kh0 = tab.kh0[pi], kw0 = tab.kw0[pi];
+      if (kh % sh != kh0 || kw % sw != kw0) continue;
+      const int i = kh / sh, j = kw / sw, Rc = tab.rc[pi], Sc = tab.sc[pi];
+      dst[tab.off[pi] + (((long)c * Rc + i) * Sc + j) * O + o] = w[s_];
+    }
   }
 }
 
@@ -626,13 +634,12 @@ int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH
 }
 
 template <typename T>
-int run_relayout_phase(const void* w, void* dst, int O, int C, int R, int S, int kh0, int kw0, int sh, int sw,
-                       int Rc, int Sc, hipStream_t st) {
+int run_relayout_phase(const void* w, void* dst, int O, int C, int R, int S, int sh, int sw, const PhaseTable& tab,
+                       hipStream_t st) {
   using E = typename Elem<T>::storage;
-  const long total = (long)C * Rc * Sc * O;
+  const long total = (long)O * C * R * S;
   if (total <= 0) return VH_OK;
-  relayout_phase_kernel<T><<<grid_for(total), 256, 0, st>>>((const E*)w, (E*)dst, O, C, R, S, kh0, kw0, sh, sw,
-                                                             Rc, Sc);
+  relayout_phase_kernel<T><<<grid_for(total), 256, 0, st>>>((const E*)w, (E*)dst, O, C, R, S, sh, sw, tab);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -758,7 +765,7 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
   template int run_col2im<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \
                              hipStream_t);                                                              \
   template int run_relayout<T>(const void*, void*, int, int, int, int, hipStream_t, int);               \
-  template int run_relayout_phase<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,  \
+  template int run_relayout_phase<T>(const void*, void*, int, int, int, int, int, int, const PhaseTable&, \
                                      hipStream_t);                                                      \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \

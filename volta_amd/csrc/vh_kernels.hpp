@@ -44,10 +44,16 @@ int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int
                int WO, hipStream_t st);
 template <typename T>
 int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip = 0);
-// Weights of one stride phase of an input gradient: dst[c][i][j][o] = w[o][c][kh0+sh*i][kw0+sw*j].
+// Weights of the stride phases of an input gradient in one pass: phase p is
+// dst + off[p]: [c][i][j][o] = w[o][c][kh0[p] + sh*i][kw0[p] + sw*j], i < rc[p], j < sc[p].
+struct PhaseTable {
+  int n;
+  int kh0[16], kw0[16], rc[16], sc[16];
+  long off[16];
+};
 template <typename T>
-int run_relayout_phase(const void* w, void* dst, int O, int C, int R, int S, int kh0, int kw0, int sh, int sw,
-                       int Rc, int Sc, hipStream_t st);
+int run_relayout_phase(const void* w, void* dst, int O, int C, int R, int S, int sh, int sw, const PhaseTable& tab,
+                       hipStream_t st);
 size_t channel_sum_ws(int N, int C, int HW, int* nslice);
 template <typename T>
 int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st);
