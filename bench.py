@@ -210,23 +210,64 @@ def profile_op(torch, layers, name, reps):
 
 def config_steps(torch, vnn, dev, steps, warmup):
     """Fwd+bwd step of each BASELINE config (synthetic inputs of the config's
-    shapes, the library's MI355X algorithm choice), one JSON line per config."""
+    shapes, the library's MI355X algorithm choice), one JSON line per config.
+    configs[0] and configs[4] run their whole graphs: convolutions with ReLU
+    between them, the sum loss, its seeded gradient (dY = 1) and the backward
+    chain; configs[3] runs each ConvTranspose2d layer's forward and backward."""
     g = torch.Generator().manual_seed(3)
     dts = {"f32": torch.float32, "bf16": torch.bfloat16}
 
-    def conv_layer(dt, N, C, O, H, K, S, P, first):
-        conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dts[dt], generator=g)
-        x = torch.randn((N, C, H, H), generator=g).to(dev, dts[dt])
-        HO = conv_out(H, K, S, P)
-        dy = torch.randn((N, O, HO, HO), generator=g).to(dev, dts[dt])
-        y = torch.empty((N, O, HO, HO), device=dev, dtype=dts[dt])
-        outs = (None if first else torch.empty_like(x), torch.empty_like(conv.weight), torch.empty_like(conv.bias))
-        passes = 2 if first else 3
-        fl = passes * 2.0 * N * O * C * K * K * HO * HO
+    def chain(dt, N, H, specs, tail=None):
+        """conv (-> ReLU) layers in sequence; specs = (C, O, K, S, P) per layer.
+        Returns run() and the step's algorithmic FLOPs (the first layer has no dX)."""
+        convs, acts, pre, douts = [], [], [], []
+        x = torch.randn((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
+        if dt == "bf16" and H == 256:  # configs[4] input ~U[0,1)
+            x = torch.rand((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
+        acts.append(x)
+        fl = 0.0
+        h = H
+        for li, (C, O, K, S, P) in enumerate(specs):
+            conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dts[dt], generator=g)
+            ho = conv_out(h, K, S, P)
+            y = torch.empty((N, O, ho, ho), device=dev, dtype=dts[dt])
+            convs.append(conv)
+            pre.append(y)
+            if li + 1 < len(specs):
+                acts.append(torch.empty_like(y))
+            fl += (2 if li == 0 else 3) * 2.0 * N * O * C * K * K * ho * ho
+            h = ho
+        relu = vnn.ReLU()
+        outs = [(None if li == 0 else torch.empty_like(acts[li]), torch.empty_like(c.weight), torch.empty_like(c.bias))
+                for li, c in enumerate(convs)]
+        dpre = [torch.empty_like(y) for y in pre]
+        loss = torch.empty((1,), device=dev, dtype=torch.float32)
+        top = pre[-1]
+        tail_out = tail_dout = None
+        if tail is not None:
+            tail_out = torch.empty(tail[1], device=dev, dtype=dts[dt])
+            tail_dout = torch.empty_like(tail_out)
 
         def run():
-            conv.forward(x, out=y)
-            conv.backward(dy, x, input_grad=not first, weight_grad=True, outs=outs)
+            for li, conv in enumerate(convs):
+                conv.forward(acts[li], out=pre[li])
+                if li + 1 < len(convs):
+                    relu.forward(pre[li], out=acts[li + 1])
+            last = pre[-1]
+            if tail is not None:
+                tail[0].forward(last, out=tail_out)
+                last = tail_out
+            vnn.sum_loss(last, out=loss)
+            if tail is not None:
+                vnn.sum_loss_backward(tail_out, 1.0, out=tail_dout)
+                tail[0].backward(tail_dout, out=dpre[-1])
+            else:
+                vnn.sum_loss_backward(top, 1.0, out=dpre[-1])
+            for li in range(len(convs) - 1, -1, -1):
+                dx, dw, db = outs[li]
+                convs[li].backward(dpre[li], acts[li], input_grad=li > 0, weight_grad=True, outs=(dx, dw, db))
+                if li > 0:
+                    relu.backward(dx, pre[li - 1], out=dpre[li - 1])
         return run, fl
 
     def convt_layer(dt, N, CI, CO, H, K, S, P):
@@ -243,22 +284,19 @@ def config_steps(torch, vnn, dev, steps, warmup):
             ct.backward(dy, x, outs=outs)
         return run, fl
 
+    ps = vnn.PixelShuffle(3)
     cfgs = {
-        "configs[0] MNIST-CNN f32 N=64": ("f32", [conv_layer("f32", 64, 1, 32, 28, 3, 1, 1, True),
-                                                 conv_layer("f32", 64, 32, 64, 28, 3, 1, 1, False)]),
+        "configs[0] MNIST-CNN f32 N=64 (conv-ReLU-conv, sum loss)":
+            ("f32", [chain("f32", 64, 28, [(1, 32, 3, 1, 1), (32, 64, 3, 1, 1)])]),
         "configs[3] DCGAN ConvTranspose2d f32 N=128": ("f32", [convt_layer("f32", 128, 100, 512, 1, 4, 1, 0),
                                                                convt_layer("f32", 128, 512, 256, 4, 4, 2, 1),
                                                                convt_layer("f32", 128, 256, 128, 8, 4, 2, 1),
                                                                convt_layer("f32", 128, 128, 64, 16, 4, 2, 1),
                                                                convt_layer("f32", 128, 64, 3, 32, 4, 2, 1)]),
-        "configs[4] super-resolution bf16 N=16 256x256": ("bf16", [
-            conv_layer("bf16", 16, 3, 64, 256, 5, 1, 2, True), conv_layer("bf16", 16, 64, 64, 256, 3, 1, 1, False),
-            conv_layer("bf16", 16, 64, 32, 256, 3, 1, 1, False), conv_layer("bf16", 16, 32, 27, 256, 3, 1, 1, False)]),
+        "configs[4] super-resolution bf16 N=16 256x256 (conv/ReLU chain, PixelShuffle, sum loss)":
+            ("bf16", [chain("bf16", 16, 256, [(3, 64, 5, 1, 2), (64, 64, 3, 1, 1), (64, 32, 3, 1, 1),
+                                              (32, 27, 3, 1, 1)], tail=(ps, (16, 3, 768, 768)))]),
     }
-    ps = vnn.PixelShuffle(3)
-    xs = torch.randn((16, 27, 256, 256), generator=g).to(dev, torch.bfloat16)
-    dys = torch.randn((16, 3, 768, 768), generator=g).to(dev, torch.bfloat16)
-    cfgs["configs[4] super-resolution bf16 N=16 256x256"][1].append((lambda: (ps.forward(xs), ps.backward(dys)), 0.0))
     for name, (dt, layers) in cfgs.items():
         def step(layers=layers):
             for run, _ in layers:

@@ -225,6 +225,24 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
                               int64_t batch, int64_t channels, int64_t height, int64_t width,
                               int64_t upscale, void* stream);
 
+/* ---- Glue of the config graphs (ReLU between layers, the sum loss, its seed) ---- */
+#define VH_UNARY_RELU 0
+/* gpu_ops.rs:171 gpu_unary(input, "relu") (unary.rs:272): y = max(x, 0), NaN -> 0.
+ * Only VH_UNARY_RELU is on this path; other ops return VH_ERR_UNSUPPORTED. */
+int vh_unary(int dtype, int op, const void* input, void* output, int64_t n, void* stream);
+/* gpu_ops.rs:186 gpu_unary_backward(out_grad, x, "relu") (unary.rs:150-155):
+ * grad_input = x > 0 ? out_grad : 0, with x the forward input. */
+int vh_unary_backward(int dtype, int op, const void* out_grad, const void* input, void* grad_input,
+                      int64_t n, void* stream);
+/* gpu_ops.rs:118 gpu_sum_reduce (ReduceOp::Sum, reduce.rs:160-180): the fp32 sum of
+ * the n elements, written to `result` (one float in device memory; the reference
+ * returns it to the host).  Fixed summation order for a given n. */
+int vh_sum_reduce(int dtype, const void* input, int64_t n, float* result, void* stream);
+/* gpu_ops.rs:452 gpu_sum_backward(grad, size) (SumGradFn, reduce.rs:22-45): every
+ * element = grad (rounded to dtype).  With grad = 1 it is the autograd seed
+ * (autograd.rs:49-62). */
+int vh_sum_backward(int dtype, float grad, void* grad_input, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,6 +42,9 @@ def lib():
         _lib = ctypes.CDLL(_LIB_PATH)
         _lib.or_auto_select.restype = ctypes.c_int
         _lib.or_auto_select.argtypes = [_SZ] * 5 + [ctypes.c_int]
+        _lib.or_sum.restype = ctypes.c_float
+        _lib.or_sum.argtypes = [_FP, _SZ]
+        _lib.or_sum_backward.argtypes = [ctypes.c_float, _FP, _SZ]
     return _lib
 
 
@@ -280,6 +283,32 @@ def pixel_shuffle_backward(dy, r):
     H, W = HR // r, WR // r
     dx = np.empty((B, C * r * r, H, W), np.float32)
     lib().or_pixel_shuffle_backward(_p(dy), _p(dx), *map(_SZ, (B, C, H, W, r)))
+    return dx
+
+
+def relu(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().or_relu(_p(x), _p(y), _SZ(x.size))
+    return y
+
+
+def relu_backward(g, x):
+    g, x = _f32(g), _f32(x)
+    dx = np.empty_like(x)
+    lib().or_relu_backward(_p(g), _p(x), _p(dx), _SZ(x.size))
+    return dx
+
+
+def sum_all(x) -> float:
+    """Volta's CPU Sum: one f32 accumulator in index order."""
+    x = _f32(x)
+    return float(lib().or_sum(_p(x), _SZ(x.size)))
+
+
+def sum_backward(grad: float, shape):
+    dx = np.empty(shape, np.float32)
+    lib().or_sum_backward(ctypes.c_float(grad), _p(dx), _SZ(dx.size))
     return dx
 
 

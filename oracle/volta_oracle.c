@@ -632,6 +632,35 @@ void or_pixel_shuffle_backward(const float *dy, float *dx, size_t B, size_t C,
 }
 
 /* ---------------------------------------------------------------------------
+ * Glue of the config graphs (not contractions).
+ * ReLU forward, unary.rs:272: y = x.max(0.0) -- Rust's f32::max returns the
+ * other operand for a NaN, so NaN -> 0; for x = -0.0 either zero is allowed
+ * (the doc of f32::max), this restatement returns +0.
+ * ReLU backward, unary.rs:150-155: dx = x > 0 ? g : 0 (x is the forward input).
+ * Sum, reduce.rs:160-180 (ReduceOp::Sum on the CPU): data.iter().sum(), one f32
+ * accumulator in index order.  SumGradFn, reduce.rs:22-45: every element of
+ * the input gradient is the upstream scalar (the autograd seed is 1.0,
+ * autograd.rs:49-62).
+ * ------------------------------------------------------------------------- */
+void or_relu(const float *x, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = x[i] > 0.0f ? x[i] : 0.0f;
+}
+
+void or_relu_backward(const float *g, const float *x, float *dx, size_t n) {
+    for (size_t i = 0; i < n; ++i) dx[i] = x[i] > 0.0f ? g[i] : 0.0f;
+}
+
+float or_sum(const float *x, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += x[i];
+    return s;
+}
+
+void or_sum_backward(float grad, float *dx, size_t n) {
+    for (size_t i = 0; i < n; ++i) dx[i] = grad;
+}
+
+/* ---------------------------------------------------------------------------
  * bf16 storage conversion: Storage::to_dtype(BF16) goes through
  * half::bf16::from_f32 (storage.rs:503-505, half 2.7.1), round-to-nearest-even
  * with NaN kept quiet.  The bf16 oracle is f32 math on inputs rounded this way.

@@ -329,3 +329,69 @@ def test_pixel_shuffle_exact(shape, dt):
     assert np.array_equal(host(y), oracle.pixel_shuffle(x, r))
     dy, dyt = prep(g.standard_normal(y.shape), dt)
     assert np.array_equal(host(ps.backward(dyt)), oracle.pixel_shuffle_backward(dy, r))
+
+
+# ------------------------------------------------------------------ glue: ReLU, sum loss
+GLUE_SIZES = [1, 7, 8, 1000, 4099, 1 << 20]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("n", GLUE_SIZES)
+def test_relu_fwd_bwd_exact(n, dt):
+    g = rng(n)
+    x, xt = prep(g.standard_normal(n), dt)
+    special = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0], np.float32)
+    if n >= 8:
+        x[:5] = special
+        xt[:5] = torch.from_numpy(special).to(DEV, DTYPES[dt])
+    y = ops.gpu_unary(xt, "relu")
+    assert np.array_equal(host(y), oracle.relu(x), equal_nan=True)
+    dy, dyt = prep(g.standard_normal(n), dt)
+    dx = ops.gpu_unary_backward(dyt, xt, "relu")
+    assert np.array_equal(host(dx), oracle.relu_backward(dy, x))
+    # unaligned views take the element path
+    if n >= 16:
+        yv = torch.empty(n + 1, dtype=DTYPES[dt], device=DEV)[1:]
+        relu = vnn.ReLU()
+        relu.forward(xt, out=yv)
+        assert np.array_equal(host(yv), oracle.relu(x), equal_nan=True)
+
+
+def test_unary_other_ops_are_unsupported():
+    x = torch.ones(8, device=DEV)
+    with pytest.raises(ValueError):
+        ops.gpu_unary(x, "exp")
+    y = torch.empty_like(x)
+    assert volta_amd.lib().vh_unary(volta_amd.F32, 7, x.data_ptr(), y.data_ptr(), 8,
+                                    torch.cuda.current_stream().cuda_stream) == volta_amd._lib.VH_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("n", GLUE_SIZES + [37 << 20])
+def test_sum_loss_and_seed(n, dt):
+    g = rng(n + 1)
+    x, xt = prep(g.standard_normal(n), dt)
+    got = ops.gpu_sum_reduce(xt)
+    exact = float(np.sum(x.astype(np.float64)))
+    scale = float(np.abs(x).sum())
+    # fp32 accumulation in a fixed order: the gate's scaled error, f32 bar
+    assert abs(got - exact) <= 1e-6 * scale + 1e-30, (got, exact)
+    # and close to Volta's own sequential f32 sum (both within n*eps of exact)
+    if n <= (1 << 20):
+        assert abs(got - oracle.sum_all(x)) <= n * 2 ** -24 * scale
+    # deterministic: the same value twice
+    assert ops.gpu_sum_reduce(xt) == got
+    # the loss's gradient / the autograd seed
+    for grad in (1.0, 0.1, -3.0):
+        dy = vnn.sum_loss_backward(xt, grad)
+        want = oracle.round_bf16(np.full(n, grad, np.float32)) if dt == "bf16" else np.full(n, grad, np.float32)
+        assert np.array_equal(host(dy), want)
+
+
+def test_sum_loss_known_answers():
+    # test_sum_backward_gpu (src/lib.rs:3528-3550): x = 1..6, sum 21, grad all ones
+    x = torch.tensor([[1.0, 2.0, 3.0], [4.0, 5.0, 6.0]], device=DEV)
+    assert host(vnn.sum_loss(x)).tolist() == [21.0]
+    assert host(ops.gpu_sum_backward(1.0, 6)).tolist() == [1.0] * 6
+    assert ops.gpu_sum_reduce(torch.tensor([42.0], device=DEV)) == 42.0
+    assert ops.gpu_sum_reduce(torch.empty(0, device=DEV)) == 0.0

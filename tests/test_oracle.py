@@ -299,6 +299,50 @@ def test_pixel_shuffle_vs_torch():
     assert np.array_equal(orc.pixel_shuffle_backward(dy, 3), F.pixel_unshuffle(torch.from_numpy(dy), 3).numpy())
 
 
+# ----------------------------------------------------------------- glue: ReLU, sum loss
+def test_relu_known_answers_and_special_values():
+    # src/lib.rs:4332-4336 (relu_forward)
+    assert orc.relu(np.array([1.0, -2.0, 0.0, 3.5], np.float32)).tolist() == [1.0, 0.0, 0.0, 3.5]
+    x = np.array([np.nan, np.inf, -np.inf, -0.0, 1e-45, -1e-45], np.float32)
+    y = orc.relu(x)
+    # Rust f32::max(NaN, 0) = 0 (the non-NaN operand); +inf kept; subnormals kept
+    assert y.tolist() == [0.0, np.inf, 0.0, 0.0, np.float32(1e-45), 0.0]
+    z = randn(4096)
+    assert np.array_equal(orc.relu(z), torch.relu(torch.from_numpy(z)).numpy())
+
+
+def test_relu_backward_vs_autograd_and_gradcheck_points():
+    # relu_gradcheck (src/lib.rs:4406-4411) points, away from 0
+    x = np.array([-1.5, -0.5, 0.5, 1.5], np.float32)
+    assert orc.relu_backward(np.ones(4, np.float32), x).tolist() == [0.0, 0.0, 1.0, 1.0]
+    x = randn(3000)
+    g = randn(3000)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_()
+    torch.relu(xt).backward(t64(g))
+    assert np.array_equal(orc.relu_backward(g, x), xt.grad.numpy().astype(np.float32))
+    # at exactly 0 the reference passes no gradient (x > 0 is false)
+    assert orc.relu_backward(np.ones(2, np.float32), np.array([0.0, -0.0], np.float32)).tolist() == [0.0, 0.0]
+
+
+def test_sum_known_answers_and_float64_bound():
+    # test_scalar_sum (src/lib.rs:2701-2712), test_sum_backward (src/lib.rs:145-151)
+    assert orc.sum_all(np.array([42.0], np.float32)) == 42.0
+    assert orc.sum_all(np.array([1.0, 2.0, 3.0], np.float32)) == 6.0
+    assert orc.sum_backward(1.0, (3,)).tolist() == [1.0, 1.0, 1.0]
+    # integers below 2^24 add exactly in f32: closed form n(n-1)/2
+    assert orc.sum_all(np.arange(4096, dtype=np.float32)) == 4096 * 4095 / 2
+    # one f32 accumulator in index order: within n * eps * sum|x| of the exact sum,
+    # and equal to a literal Python loop in float32
+    x = randn(20000)
+    exact = float(np.sum(x.astype(np.float64)))
+    assert abs(orc.sum_all(x) - exact) <= x.size * 2 ** -24 * float(np.abs(x).sum())
+    acc = np.float32(0)
+    for v in x[:2000]:
+        acc = np.float32(acc + v)
+    assert orc.sum_all(x[:2000]) == float(acc)
+    assert np.array_equal(orc.sum_backward(2.5, (2, 3)), np.full((2, 3), 2.5, np.float32))
+
+
 # ----------------------------------------------------------------- bf16 rounding
 def test_bf16_rne_matches_torch():
     vals = np.concatenate([randn(4096) * 1e3, np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875,

@@ -27,6 +27,7 @@ BF16 = 1
 
 ALGO_DIRECT, ALGO_IM2COL, ALGO_IGEMM, ALGO_AUTO = 0, 1, 2, 3
 POLICY_FASTEST, POLICY_GENERIC = 0, 1
+UNARY_RELU = 0
 
 
 class VoltaHipError(RuntimeError):
@@ -75,6 +76,10 @@ SIGNATURES = {
     "vh_linear_backward": [_INT, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_pixel_shuffle": [_INT, _P, _P] + [_I64] * 5 + [_P],
     "vh_pixel_shuffle_backward": [_INT, _P, _P] + [_I64] * 5 + [_P],
+    "vh_unary": [_INT, _INT, _P, _P, _I64, _P],
+    "vh_unary_backward": [_INT, _INT, _P, _P, _P, _I64, _P],
+    "vh_sum_reduce": [_INT, _P, _I64, _P, _P],
+    "vh_sum_backward": [_INT, ctypes.c_float, _P, _I64, _P],
 }
 
 _lib = None

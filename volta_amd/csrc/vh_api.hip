@@ -1058,4 +1058,51 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
                      (int)width, (int)upscale, 1, S(stream));
 }
 
+// ------------------------------------------------------------------ glue of the config graphs
+int vh_unary(int dtype, int op, const void* input, void* output, int64_t n, void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(dtype));
+  if (op != VH_UNARY_RELU) return set_error(VH_ERR_UNSUPPORTED, "unary op %d: only ReLU is on this path", op);
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!input || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return VH_DISPATCH(dtype, run_relu, input, nullptr, output, (long)n, S(stream));
+}
+
+int vh_unary_backward(int dtype, int op, const void* out_grad, const void* input, void* grad_input, int64_t n,
+                      void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(dtype));
+  if (op != VH_UNARY_RELU) return set_error(VH_ERR_UNSUPPORTED, "unary op %d: only ReLU is on this path", op);
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!out_grad || !input || !grad_input) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return VH_DISPATCH(dtype, run_relu, input, out_grad, grad_input, (long)n, S(stream));
+}
+
+int vh_sum_reduce(int dtype, const void* input, int64_t n, float* result, void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(dtype));
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (!input && n > 0) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  if (!result) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  hipStream_t st = S(stream);
+  void* ws;
+  VH_TRY(ws_get(st, sum_ws_bytes((long)n), &ws));
+  return VH_DISPATCH(dtype, run_sum, input, (long)n, result, (float*)ws, st);
+}
+
+int vh_sum_backward(int dtype, float grad, void* grad_input, int64_t n, void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(dtype));
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!grad_input) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return VH_DISPATCH(dtype, run_fill, grad_input, (long)n, grad, S(stream));
+}
+
 }  // extern "C"

@@ -540,6 +540,66 @@ __global__ __launch_bounds__(256) void pixel_shuffle_vec_kernel(const typename E
   }
 }
 
+// ============================================================== glue: ReLU, sum loss
+// ReLU: y = x > 0 ? x : +0 (NaN -> 0), backward dx = x > 0 ? g : 0; 16-byte
+// vectors when the range allows, one element per lane otherwise.
+template <typename T>
+__device__ __forceinline__ bool pos(typename Elem<T>::storage v) {
+  return Elem<T>::to_f32(v) > 0.f;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void relu_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                   const typename Elem<T>::storage* __restrict__ g,
+                                                   typename Elem<T>::storage* __restrict__ y, long n, int vec) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  const long nv = vec ? n / VE : 0;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < nv; i += (long)gridDim.x * 256) {
+    S xv[VE], gv[VE], out[VE];
+    *reinterpret_cast<uint4*>(xv) = reinterpret_cast<const uint4*>(x)[i];
+    if (g) *reinterpret_cast<uint4*>(gv) = reinterpret_cast<const uint4*>(g)[i];
+#pragma unroll
+    for (int j = 0; j < VE; ++j) out[j] = pos<T>(xv[j]) ? (g ? gv[j] : xv[j]) : S(0);
+    reinterpret_cast<uint4*>(y)[i] = *reinterpret_cast<const uint4*>(out);
+  }
+  for (long i = nv * VE + (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+    y[i] = pos<T>(x[i]) ? (g ? g[i] : x[i]) : S(0);
+}
+
+// Sum of n elements: block b adds the contiguous slice b (lanes stride the
+// slice, then a fixed butterfly and wave order) into part[b]; a second pass
+// adds the partials in index order.  The order depends only on n.
+template <typename T>
+__global__ __launch_bounds__(256) void sum_slices_kernel(const typename Elem<T>::storage* __restrict__ x, long n,
+                                                         long per, float* __restrict__ part) {
+  const long b = (long)blockIdx.x * per, e = min(n, b + per);
+  float s = 0.f;
+  for (long i = b + threadIdx.x; i < e; i += 256) s += Elem<T>::to_f32(x[i]);
+  s = wave_sum(s);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(256) void sum_partials_scalar_kernel(const float* __restrict__ part, int nb,
+                                                                  float* __restrict__ out) {
+  float s = 0.f;
+  for (int i = threadIdx.x; i < nb; i += 256) s += part[i];
+  s = wave_sum(s);
+  __shared__ float red[4];
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) out[0] = (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void fill_kernel(typename Elem<T>::storage* __restrict__ y, long n, float v) {
+  const typename Elem<T>::storage e = Elem<T>::from_f32(v);
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) y[i] = e;
+}
+
 // ============================================================== typed launchers
 template <typename T>
 int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st) {
@@ -750,6 +810,40 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
   return VH_OK;
 }
 
+template <typename T>
+int run_relu(const void* x, const void* g, void* y, long n, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  if (n <= 0) return VH_OK;
+  const bool vec = ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)g) & 15) == 0);
+  relu_kernel<T><<<grid_for(vec ? n / (16 / (long)sizeof(S)) + 1 : n), 256, 0, st>>>((const S*)x, (const S*)g, (S*)y,
+                                                                                      n, vec ? 1 : 0);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+size_t sum_ws_bytes(long n) { return (size_t)std::max<long>(1, std::min<long>(1024, (n + 4095) / 4096)) * 4; }
+
+template <typename T>
+int run_sum(const void* x, long n, float* out, float* ws, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  const int nb = (int)std::max<long>(1, std::min<long>(1024, (n + 4095) / 4096));
+  const long per = (n + nb - 1) / nb;
+  sum_slices_kernel<T><<<nb, 256, 0, st>>>((const S*)x, n, per, ws);
+  VH_LAUNCH_CHECK();
+  sum_partials_scalar_kernel<<<1, 256, 0, st>>>(ws, nb, out);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_fill(void* y, long n, float v, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  if (n <= 0) return VH_OK;
+  fill_kernel<T><<<grid_for(n), 256, 0, st>>>((S*)y, n, v);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 #define VH_INST(T)                                                                                      \
   template int run_direct_fwd<T>(const void*, const void*, const void*, void*, const ConvGeom&, hipStream_t); \
   template int run_col2im_t<T>(const float*, void*, int, int, int, int, int, int, int, int, int, int, int, int,  \
@@ -769,7 +863,10 @@ int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int
                                      hipStream_t);                                                      \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
-  template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);
+  template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);     \
+  template int run_relu<T>(const void*, const void*, void*, long, hipStream_t);                         \
+  template int run_sum<T>(const void*, long, float*, float*, hipStream_t);                              \
+  template int run_fill<T>(void*, long, float, hipStream_t);
 VH_INST(float)
 VH_INST(bf16)
 #undef VH_INST

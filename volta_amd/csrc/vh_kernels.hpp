@@ -44,6 +44,15 @@ int run_col2im(const void* col, void* x, int B, int C, int H, int W, int KH, int
                int WO, hipStream_t st);
 template <typename T>
 int run_relayout(const void* src, void* dst, int A, int B, int RS, int swap, hipStream_t st, int flip = 0);
+// Glue: ReLU (g == nullptr) or its backward (dx = x > 0 ? g : 0); sum of n
+// elements into *out (device) with a fixed order (ws: sum_ws_bytes(n)); fill.
+template <typename T>
+int run_relu(const void* x, const void* g, void* y, long n, hipStream_t st);
+size_t sum_ws_bytes(long n);
+template <typename T>
+int run_sum(const void* x, long n, float* out, float* ws, hipStream_t st);
+template <typename T>
+int run_fill(void* y, long n, float v, hipStream_t st);
 // Weights of the stride phases of an input gradient in one pass: phase p is
 // dst + off[p]: [c][i][j][o] = w[o][c][kh0[p] + sh*i][kw0[p] + sw*j], i < rc[p], j < sc[p].
 struct PhaseTable {

@@ -17,6 +17,7 @@ from typing import Optional, Tuple
 
 import torch
 
+from . import _lib
 from ._lib import ALGO_AUTO, ALGO_DIRECT, ALGO_IGEMM, ALGO_IM2COL, check, lib
 from .ops import _same_dtype, ptr, stream_ptr
 
@@ -215,3 +216,38 @@ class PixelShuffle:
         check(lib().vh_pixel_shuffle_backward(_same_dtype(out_grad), ptr(out_grad), ptr(dx), B, C, H, W, r,
                                               stream_ptr(out_grad.device)))
         return dx
+
+
+class ReLU:
+    """The ReLU between the config graphs' layers: forward max(x, 0)
+    (unary.rs:272), backward out_grad where the forward input is positive
+    (unary.rs:150-155)."""
+
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        y = out if out is not None else torch.empty_like(x)
+        check(lib().vh_unary(_same_dtype(x), _lib.UNARY_RELU, ptr(x), ptr(y), x.numel(), stream_ptr(x.device)))
+        return y
+
+    __call__ = forward
+
+    def backward(self, out_grad: torch.Tensor, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        dx = out if out is not None else torch.empty_like(x)
+        check(lib().vh_unary_backward(_same_dtype(out_grad, x), _lib.UNARY_RELU, ptr(out_grad), ptr(x), ptr(dx),
+                                      x.numel(), stream_ptr(x.device)))
+        return dx
+
+
+def sum_loss(y: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Loss = sum of every element of y (reduce.rs:160-180), as a one-element
+    fp32 device tensor (no host round trip)."""
+    res = out if out is not None else torch.empty((1,), dtype=torch.float32, device=y.device)
+    check(lib().vh_sum_reduce(_same_dtype(y), ptr(y), y.numel(), ptr(res), stream_ptr(y.device)))
+    return res
+
+
+def sum_loss_backward(y: torch.Tensor, grad: float = 1.0, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """dLoss/dy for the sum loss: every element = grad (SumGradFn, reduce.rs:22-45;
+    grad = 1 is the autograd seed, autograd.rs:49-62)."""
+    dy = out if out is not None else torch.empty_like(y)
+    check(lib().vh_sum_backward(_same_dtype(y), float(grad), ptr(dy), y.numel(), stream_ptr(y.device)))
+    return dy

@@ -188,3 +188,59 @@ def gpu_igemm_backward_weight(out_grad, input, batch_size, in_channels, out_chan
             pad_h, pad_w, h_out, w_out)
     return _conv_call("vh_igemm_backward_weight", out_grad, input,
                       (out_channels, in_channels, kernel_h, kernel_w), dims)
+
+
+# ---------------------------------------------------------------- glue: ReLU, sum loss
+_UNARY_OPS = {"relu": _lib.UNARY_RELU}
+
+
+def _unary_code(op: str) -> int:
+    try:
+        return _UNARY_OPS[op]
+    except KeyError:
+        raise ValueError(f"unary op {op!r}: only 'relu' is on this path") from None
+
+
+@_optional
+def gpu_unary(input: torch.Tensor, op: str):
+    """gpu_ops.rs:171 -- elementwise op (ReLU: max(x, 0), unary.rs:272)."""
+    code = _unary_code(op)
+    x = input.contiguous()
+    y = torch.empty_like(x)
+    _call("vh_unary", dtype_code(x), code, ptr(x), ptr(y), x.numel(), stream_ptr(x.device))
+    return y
+
+
+@_optional
+def gpu_unary_backward(out_grad: torch.Tensor, x: torch.Tensor, op: str):
+    """gpu_ops.rs:186 -- ReLU: out_grad where x > 0, else 0 (unary.rs:150-155)."""
+    code = _unary_code(op)
+    dt = _same_dtype(out_grad, x)
+    if out_grad.numel() != x.numel():
+        raise ValueError("gpu_unary_backward: out_grad and x differ in size")
+    dx = torch.empty_like(x)
+    _call("vh_unary_backward", dt, code, ptr(out_grad), ptr(x), ptr(dx), x.numel(), stream_ptr(x.device))
+    return dx
+
+
+@_optional
+def gpu_sum_reduce(data: torch.Tensor):
+    """gpu_ops.rs:118 -- the fp32 sum of every element, returned to the host."""
+    out = torch.empty((1,), dtype=torch.float32, device=data.device)
+    _call("vh_sum_reduce", dtype_code(data), ptr(data), data.numel(), ptr(out), stream_ptr(data.device))
+    return float(out.item())
+
+
+def gpu_sum_backward(grad: float, input_size: int, dtype=torch.float32, device="cuda:0"):
+    """gpu_ops.rs:452 -- a buffer of `input_size` elements equal to `grad`
+    (SumGradFn; the autograd seed when grad = 1).  None without a device."""
+    if not torch.cuda.is_available():
+        return None
+    out = torch.empty((input_size,), dtype=dtype, device=device)
+    try:
+        _call("vh_sum_backward", _DTYPES[dtype], float(grad), ptr(out), input_size, stream_ptr(out.device))
+    except VoltaHipError as e:
+        if e.status in (_lib.VH_ERR_NO_DEVICE, _lib.VH_ERR_OOM):
+            return None
+        raise
+    return out
