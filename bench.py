@@ -218,56 +218,52 @@ def config_steps(torch, vnn, dev, steps, warmup):
     dts = {"f32": torch.float32, "bf16": torch.bfloat16}
 
     def chain(dt, N, H, specs, tail=None):
-        """conv (-> ReLU) layers in sequence; specs = (C, O, K, S, P) per layer.
-        Returns run() and the step's algorithmic FLOPs (the first layer has no dX)."""
-        convs, acts, pre, douts = [], [], [], []
-        x = torch.randn((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
+        """conv -> ReLU -> ... -> conv layers in sequence; specs = (C, O, K, S, P) per
+        layer.  Each ReLU is fused into the producing conv's epilogue
+        (vh_conv2d_forward_relu) and its backward into the next layer's input
+        gradient (vh_conv2d_backward_relu).  Returns run() and the step's
+        algorithmic FLOPs (the first layer has no dX)."""
+        convs, acts = [], []
         if dt == "bf16" and H == 256:  # configs[4] input ~U[0,1)
             x = torch.rand((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
+        else:
+            x = torch.randn((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
         acts.append(x)
         fl = 0.0
         h = H
         for li, (C, O, K, S, P) in enumerate(specs):
             conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dts[dt], generator=g)
             ho = conv_out(h, K, S, P)
-            y = torch.empty((N, O, ho, ho), device=dev, dtype=dts[dt])
             convs.append(conv)
-            pre.append(y)
-            if li + 1 < len(specs):
-                acts.append(torch.empty_like(y))
+            acts.append(torch.empty((N, O, ho, ho), device=dev, dtype=dts[dt]))  # relu(y), or y for the last
             fl += (2 if li == 0 else 3) * 2.0 * N * O * C * K * K * ho * ho
             h = ho
-        relu = vnn.ReLU()
-        outs = [(None if li == 0 else torch.empty_like(acts[li]), torch.empty_like(c.weight), torch.empty_like(c.bias))
-                for li, c in enumerate(convs)]
-        dpre = [torch.empty_like(y) for y in pre]
+        grads = [torch.empty_like(a) for a in acts]  # grads[i]: gradient w.r.t. acts[i] (pre-ReLU for i > 0)
+        wouts = [(torch.empty_like(c.weight), torch.empty_like(c.bias)) for c in convs]
         loss = torch.empty((1,), device=dev, dtype=torch.float32)
-        top = pre[-1]
         tail_out = tail_dout = None
         if tail is not None:
             tail_out = torch.empty(tail[1], device=dev, dtype=dts[dt])
             tail_dout = torch.empty_like(tail_out)
+        L = len(convs)
 
         def run():
             for li, conv in enumerate(convs):
-                conv.forward(acts[li], out=pre[li])
-                if li + 1 < len(convs):
-                    relu.forward(pre[li], out=acts[li + 1])
-            last = pre[-1]
+                conv.forward(acts[li], out=acts[li + 1], relu=li + 1 < L)
+            last = acts[L]
             if tail is not None:
                 tail[0].forward(last, out=tail_out)
-                last = tail_out
-            vnn.sum_loss(last, out=loss)
-            if tail is not None:
+                vnn.sum_loss(tail_out, out=loss)
                 vnn.sum_loss_backward(tail_out, 1.0, out=tail_dout)
-                tail[0].backward(tail_dout, out=dpre[-1])
+                tail[0].backward(tail_dout, out=grads[L])
             else:
-                vnn.sum_loss_backward(top, 1.0, out=dpre[-1])
-            for li in range(len(convs) - 1, -1, -1):
-                dx, dw, db = outs[li]
-                convs[li].backward(dpre[li], acts[li], input_grad=li > 0, weight_grad=True, outs=(dx, dw, db))
-                if li > 0:
-                    relu.backward(dx, pre[li - 1], out=dpre[li - 1])
+                vnn.sum_loss(last, out=loss)
+                vnn.sum_loss_backward(last, 1.0, out=grads[L])
+            for li in range(L - 1, -1, -1):
+                dw, db = wouts[li]
+                # grads[li] for li > 0 is the gradient before the ReLU that produced acts[li]
+                convs[li].backward(grads[li + 1], acts[li], input_grad=li > 0, weight_grad=True,
+                                   outs=(grads[li] if li > 0 else None, dw, db), relu_input=li > 0)
         return run, fl
 
     def convt_layer(dt, N, CI, CO, H, K, S, P):

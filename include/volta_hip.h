@@ -225,6 +225,26 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
                               int64_t batch, int64_t channels, int64_t height, int64_t width,
                               int64_t upscale, void* stream);
 
+/* Fused forms for the config graphs' conv -> ReLU chains (no single counterpart in
+ * the reference, which runs Conv2d::forward then relu, and ReLU's backward after the
+ * next layer's input gradient; same results):
+ * vh_conv2d_forward_relu = vh_conv2d_forward followed by ReLU (unary.rs:272), the
+ * ReLU applied in the convolution's epilogue; */
+int vh_conv2d_forward_relu(int dtype, int algo, const void* input, const void* weight,
+                           const void* bias, void* output, int64_t batch, int64_t in_channels,
+                           int64_t out_channels, int64_t height, int64_t width, int64_t kernel_h,
+                           int64_t kernel_w, int64_t stride_h, int64_t stride_w, int64_t pad_h,
+                           int64_t pad_w, int* algo_used, void* stream);
+/* vh_conv2d_backward_relu = vh_conv2d_backward for a layer whose input came out of a
+ * ReLU, with that ReLU's backward (unary.rs:150-155) applied to grad_input:
+ * grad_input = input > 0 ? dX : 0 (the ReLU's output is positive exactly where its
+ * input was), in the input-gradient epilogue. */
+int vh_conv2d_backward_relu(int dtype, int algo, const void* out_grad, const void* input,
+                            const void* weight, void* grad_input, void* grad_weight, void* grad_bias,
+                            int64_t batch, int64_t in_channels, int64_t out_channels, int64_t height,
+                            int64_t width, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                            int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream);
+
 /* ---- Glue of the config graphs (ReLU between layers, the sum loss, its seed) ---- */
 #define VH_UNARY_RELU 0
 /* gpu_ops.rs:171 gpu_unary(input, "relu") (unary.rs:272): y = max(x, 0), NaN -> 0.

@@ -395,3 +395,47 @@ def test_sum_loss_known_answers():
     assert host(ops.gpu_sum_backward(1.0, 6)).tolist() == [1.0] * 6
     assert ops.gpu_sum_reduce(torch.tensor([42.0], device=DEV)) == 42.0
     assert ops.gpu_sum_reduce(torch.empty(0, device=DEV)) == 0.0
+
+
+# ------------------------------------------------------------------ fused conv -> ReLU
+RELU_CASES = [
+    # (B, C, O, H, W, K, S, P)
+    (2, 32, 64, 28, 28, 3, 1, 1),    # config 1 conv2 / halo kernel (bf16)
+    (2, 64, 64, 20, 24, 3, 1, 1),
+    (1, 3, 64, 24, 32, 5, 1, 2),     # config 5 conv1 shape: one partial channel group
+    (2, 64, 128, 16, 16, 1, 2, 0),   # strided 1x1 (bf16 pointwise kernels: separate ReLU pass)
+    (2, 16, 24, 11, 9, 3, 2, 1),     # strided 3x3: stride phases
+    (2, 1, 32, 12, 12, 3, 1, 1),     # one input channel (MI355X selector: direct)
+]
+
+
+@pytest.mark.parametrize("case", RELU_CASES, ids=_conv_ids)
+@pytest.mark.parametrize("algo", [vnn.ConvAlgo.Auto, vnn.ConvAlgo.IGEMM, vnn.ConvAlgo.Im2col])
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_conv2d_fused_relu_fwd_and_masked_dgrad(case, algo, dt):
+    B, C, O, H, W, K, S, P = case
+    g = rng(sum(case) + 11)
+    # the layer input came out of a ReLU: non-negative, about half zeros
+    x, xt = prep(np.maximum(g.standard_normal((B, C, H, W)), 0), dt)
+    w, wt = prep(g.standard_normal((O, C, K, K)) * np.sqrt(2.0 / (C * K * K)), dt)
+    b, bt = prep(g.uniform(-1, 1, (O,)), dt)
+    conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=DEV, dtype=DTYPES[dt])
+    conv.weight, conv.bias = wt, bt
+    conv.set_algo(algo)
+    kw = dict(stride=(S, S), pad=(P, P))
+    bb = b[None, :, None, None]
+    ref, scale = ref_and_scale(oracle.direct_conv, x, w, **kw)
+    y = conv.forward(xt, relu=True)
+    got = host(y)
+    assert (got >= 0).all()
+    assert_parity(got, np.maximum(ref + bb, 0), scale + np.abs(bb), dt, "relu(y)")
+    dy, dyt = prep(g.standard_normal(got.shape), dt)
+    dx, dw, db = conv.backward(dyt, xt, relu_input=True)
+    dref, dscale = ref_and_scale(oracle.direct_conv_backward_input, dy, w, x.shape, **kw)
+    mask = x > 0
+    gdx = host(dx)
+    assert (gdx[~mask] == 0).all()
+    assert_parity(gdx, np.where(mask, dref, 0), dscale, dt, "masked dx")
+    # the weight and bias gradients are those of the plain backward
+    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw)
+    check(db, oracle.conv_bias_grad, (dy,), dt, "db")

@@ -177,11 +177,21 @@ static bool is_strided_pointwise(const ConvDims& d) {
 
 // Forward pass as implicit GEMM: rows = output channels (A = weight in
 // [O][kh][kw][C] order), columns = output positions (B = im2col gather of x).
+// ReLU applied in place after a pass whose kernel has no fused epilogue for it.
+static int relu_after(int dt, void* y, long n, hipStream_t st) {
+  return VH_DISPATCH(dt, run_relu, y, nullptr, y, n, st);
+}
+// grad = mask > 0 ? grad : 0 in place (the ReLU backward of the layer below).
+static int mask_after(int dt, const void* mask, void* grad, long n, hipStream_t st) {
+  return VH_DISPATCH(dt, run_relu, mask, grad, grad, n, st);
+}
+
+// act: 1 = ReLU on the output (fused into the epilogue where the kernel has it).
 static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, void* y, const ConvDims& d,
-                     hipStream_t st) {
+                     hipStream_t st, int act = 0) {
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths) {
     int r = pw_conv_bf16_fwd(x, w, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
-    if (r != VH_ERR_UNSUPPORTED) return r;
+    if (r != VH_ERR_UNSUPPORTED) return r == VH_OK && act ? relu_after(dt, y, d.B * d.O * d.HO * d.WO, st) : r;
   }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
@@ -211,13 +221,14 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   void* wt = at(ws, o_w);
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
     int r = halo_conv_bf16(x, w, 0, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
-                           (int)d.KW, (int)d.PH, (int)d.PW, st);
+                           (int)d.KW, (int)d.PH, (int)d.PW, st, act);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wt, (int)d.O, (int)d.C, (int)RS, 0, st));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wt, (int)(RS * d.C), (int)d.O, ((RS * d.C) % vec) == 0};
   p.args.b = Operand{x, 0, p.args.N, 0};
+  p.args.act = act;
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
@@ -234,7 +245,7 @@ struct DgradPhase {
 };
 
 static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias, void* dx, const ConvDims& d,
-                        hipStream_t st) {
+                        hipStream_t st, const void* mask = nullptr) {
   const int SH = (int)d.SH, SW = (int)d.SW;
   std::vector<DgradPhase> ph;
   PhaseTable tab{};
@@ -303,6 +314,8 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
     p.args.d = dx;
     p.args.bias = bias;
     p.args.bias_mode = bias ? 1 : 0;
+    p.args.act = mask ? 2 : 0;
+    p.args.mask = mask;
     p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
     igemm_prepare(p);
     p.args.a = Operand{wp, std::max(K, 1), (int)d.C, (K % vec) == 0};
@@ -314,7 +327,10 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
 
 // Input gradient as implicit GEMM: rows = input channels (A = weight in
 // [C][kh][kw][O] order), columns = input positions (B = gather of dY).
-static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st) {
+// mask: the layer input, when it came from a ReLU: dx is zeroed where it is not
+// positive (the ReLU backward of the layer below, fused where the kernel has it).
+static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st,
+                       const void* mask = nullptr) {
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
@@ -341,22 +357,25 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && d.PH <= d.KH - 1 && d.PW <= d.KW - 1 && g_fast_paths) {
     // stride 1: dX = conv(dY, W rotated 180 degrees with O and C swapped), pad K-1-p
     int r = halo_conv_bf16(dy, w, 1, wd, nullptr, dx, (int)d.B, (int)d.O, (int)d.HO, (int)d.WO, (int)d.C,
-                           (int)d.KH, (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st);
+                           (int)d.KH, (int)d.KW, (int)(d.KH - 1 - d.PH), (int)(d.KW - 1 - d.PW), st,
+                           mask ? 2 : 0, mask);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths && ((uintptr_t)dx & 3) == 0) {
     VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
     int r = pw_conv_bf16_dgrad(dy, wd, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
-    if (r != VH_ERR_UNSUPPORTED) return r;
+    if (r != VH_ERR_UNSUPPORTED) return r == VH_OK && mask ? mask_after(dt, mask, dx, d.B * d.C * d.H * d.W, st) : r;
   }
   if ((d.SH > 1 || d.SW > 1) && g_fast_paths) {
-    int r = dgrad_phases(dt, dy, w, nullptr, dx, d, st);  // unsupported only beyond 16 phases
+    int r = dgrad_phases(dt, dy, w, nullptr, dx, d, st, mask);  // unsupported only beyond 16 phases
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
   const int vec = dt == VH_BF16 ? 8 : 4;
   p.args.a = Operand{wd, (int)(RS * d.O), (int)d.C, ((RS * d.O) % vec) == 0};
   p.args.b = Operand{dy, 0, p.args.N, 0};
+  p.args.act = mask ? 2 : 0;
+  p.args.mask = mask;
   return run_igemm(p, (float*)at(ws, o_g), st);
 }
 
@@ -869,9 +888,8 @@ static int layer_dims(ConvDims& d) {
   return check_conv(d, true);
 }
 
-int vh_conv2d_forward(int dtype, int algo, const void* input, const void* weight, const void* bias, void* output,
-                      VH_LAYER_ARGS, int* algo_used, void* stream) {
-  VH_ENTRY();
+static int conv2d_forward_impl(int dtype, int algo, const void* input, const void* weight, const void* bias,
+                               void* output, VH_LAYER_ARGS, int* algo_used, void* stream, int act) {
   VH_TRY(check_dtype(dtype));
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
              pad_h, pad_w, 0, 0};
@@ -884,15 +902,33 @@ int vh_conv2d_forward(int dtype, int algo, const void* input, const void* weight
   if (batch == 0) return VH_OK;
   if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
-  if (algo == VH_ALGO_IGEMM) return igemm_fwd(dtype, input, weight, bias, output, d, st);
-  if (algo == VH_ALGO_IM2COL) return im2col_fwd(dtype, input, weight, bias, output, d, st);
-  ConvGeom g = geom_of(d);
-  return VH_DISPATCH(dtype, run_direct_fwd, input, weight, bias, output, g, st);
+  if (algo == VH_ALGO_IGEMM) return igemm_fwd(dtype, input, weight, bias, output, d, st, act);
+  if (algo == VH_ALGO_IM2COL) {
+    VH_TRY(im2col_fwd(dtype, input, weight, bias, output, d, st));
+  } else {
+    ConvGeom g = geom_of(d);
+    VH_TRY(VH_DISPATCH(dtype, run_direct_fwd, input, weight, bias, output, g, st));
+  }
+  return act ? relu_after(dtype, output, d.B * d.O * d.HO * d.WO, st) : VH_OK;
 }
 
-int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
-                       void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS, void* stream) {
+int vh_conv2d_forward(int dtype, int algo, const void* input, const void* weight, const void* bias, void* output,
+                      VH_LAYER_ARGS, int* algo_used, void* stream) {
   VH_ENTRY();
+  return conv2d_forward_impl(dtype, algo, input, weight, bias, output, batch, in_channels, out_channels, height,
+                             width, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, algo_used, stream, 0);
+}
+
+int vh_conv2d_forward_relu(int dtype, int algo, const void* input, const void* weight, const void* bias,
+                           void* output, VH_LAYER_ARGS, int* algo_used, void* stream) {
+  VH_ENTRY();
+  return conv2d_forward_impl(dtype, algo, input, weight, bias, output, batch, in_channels, out_channels, height,
+                             width, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, algo_used, stream, 1);
+}
+
+static int conv2d_backward_impl(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
+                                void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS, void* stream,
+                                bool relu_input) {
   VH_TRY(check_dtype(dtype));
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
              pad_h, pad_w, 0, 0};
@@ -900,12 +936,14 @@ int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* in
   if (algo < VH_ALGO_DIRECT || algo > VH_ALGO_IGEMM) return set_error(VH_ERR_BAD_ARG, "bad algorithm %d", algo);
   hipStream_t st = S(stream);
   if (batch == 0) return VH_OK;
-  if (!out_grad || (grad_input && !weight) || (grad_weight && !input))
+  if (!out_grad || (grad_input && !weight) || (grad_weight && !input) || (relu_input && grad_input && !input))
     return set_error(VH_ERR_BAD_ARG, "null pointer");
+  const void* mask = relu_input && grad_input ? input : nullptr;
   if (algo == VH_ALGO_IM2COL) {
     if (grad_input || grad_weight) VH_TRY(im2col_bwd(dtype, out_grad, input, weight, grad_input, grad_weight, d, st));
+    if (mask) VH_TRY(mask_after(dtype, mask, grad_input, d.B * d.C * d.H * d.W, st));
   } else if (algo == VH_ALGO_IGEMM) {
-    if (grad_input) VH_TRY(igemm_dgrad(dtype, out_grad, weight, grad_input, d, st));
+    if (grad_input) VH_TRY(igemm_dgrad(dtype, out_grad, weight, grad_input, d, st, mask));
     if (grad_weight) {
       bool db_done = false;
       VH_TRY(igemm_wgrad(dtype, out_grad, input, grad_weight, grad_bias, &db_done, d, st));
@@ -914,10 +952,27 @@ int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* in
   } else {
     ConvGeom g = geom_of(d);
     if (grad_input) VH_TRY(VH_DISPATCH(dtype, run_direct_dgrad, out_grad, weight, grad_input, g, st));
+    if (mask) VH_TRY(mask_after(dtype, mask, grad_input, d.B * d.C * d.H * d.W, st));
     if (grad_weight) VH_TRY(direct_wgrad(dtype, out_grad, input, grad_weight, d, st));
   }
   if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.O, d.HO * d.WO, st));
   return VH_OK;
+}
+
+int vh_conv2d_backward(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
+                       void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS, void* stream) {
+  VH_ENTRY();
+  return conv2d_backward_impl(dtype, algo, out_grad, input, weight, grad_input, grad_weight, grad_bias, batch,
+                              in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+                              pad_h, pad_w, stream, false);
+}
+
+int vh_conv2d_backward_relu(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
+                            void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS, void* stream) {
+  VH_ENTRY();
+  return conv2d_backward_impl(dtype, algo, out_grad, input, weight, grad_input, grad_weight, grad_bias, batch,
+                              in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+                              pad_h, pad_w, stream, true);
 }
 
 static int convt_dims(ConvDims& d, long B, long CI, long CO, long H, long W, long KH, long KW, long SH, long SW,

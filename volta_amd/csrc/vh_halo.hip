@@ -57,6 +57,8 @@ struct HaloArgs {
   int y_bytes;           // size of y in bytes (< 2^31)
   int w_bytes;           // size of wt in bytes
   int tiles_m, tiles_o;  // grid = tiles_m * tiles_o blocks
+  int act;               // epilogue: 0 none, 1 ReLU, 2 zero where mask <= 0 (mask laid out like y)
+  const uint16_t* mask;
   int stages;            // LDS stages (1 when there is a single channel group)
   FastDiv fPQ, fQ;              // P*TW, TW
   FastDiv fW2, fRowsMax, fHp;   // item decomposition (Wp/2, rows_max, Hp)
@@ -369,6 +371,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         (lane >> 5) * 4 * PQ2
                   : (int)0x80000000u;
   }
+  const __amdgpu_buffer_rsrc_t mrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(a.act == 2 ? a.mask : a.y), (short)0, a.y_bytes, 0x00020000);
+  // fp32 result + bias, then the fused activation: ReLU (NaN -> 0, as fmaxf),
+  // or the ReLU backward of the layer below (zero where its output, the mask,
+  // is not positive).  The mask values are all loaded before the first store
+  // (a load may not pass a store to possibly the same memory).
+  uint32_t keep[FM][FN] = {};  // bit v: mask value of accumulator v is positive
+  if (a.act == 2) {
+    uint16_t mv[FM][FN][16];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) mv[i][j][v] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, yoff[j], orow * PQ2, 0);
+      }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) keep[i][j] |= (bf16_to_f32(mv[i][j][v]) > 0.f ? 1u : 0u) << v;
+  }
+  auto epi = [&](float val, int i, int j, int v) {
+    if (a.act == 1) val = fmaxf(val, 0.f);
+    else if (a.act == 2 && !((keep[i][j] >> v) & 1u)) val = 0.f;
+    return __builtin_bit_cast(uint16_t, (__bf16)val);
+  };
   float bv[FM][16];
 #pragma unroll
   for (int i = 0; i < FM; ++i)
@@ -385,8 +416,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);  // wave-uniform part of o
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][v] + bv[i][v])),
-                                                yrsrc, yoff[j], orow * PQ2, 0);
+          __builtin_amdgcn_raw_buffer_store_b16(epi(acc[i][j][v] + bv[i][v], i, j, v), yrsrc, yoff[j], orow * PQ2, 0);
       }
   } else {
 #pragma unroll
@@ -398,8 +428,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           if (ok)
-            __builtin_amdgcn_raw_buffer_store_b16(
-                __builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][v] + bv[i][v])), yrsrc, yoff[j], orow * PQ2, 0);
+            __builtin_amdgcn_raw_buffer_store_b16(epi(acc[i][j][v] + bv[i][v], i, j, v), yrsrc, yoff[j],
+                                                  orow * PQ2, 0);
       }
   }
 }
@@ -442,7 +472,7 @@ int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
 size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)((C + 15) / 16 * 16) * O * R * S * 2; }
 
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
-                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st) {
+                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st, int act, const void* mask) {
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0) return VH_ERR_UNSUPPORTED;
   if (C < 1 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
@@ -454,6 +484,8 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.wt = (const uint16_t*)wt;
   a.bias = (const uint16_t*)bias;
   a.y = (uint16_t*)y;
+  a.act = act;
+  a.mask = (const uint16_t*)mask;
   a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph; a.pw = pw;
   a.Hp = H + 2 * ph;  // = P + R - 1
   const long xb = (long)N * C * H * W * 2;

@@ -63,6 +63,8 @@ struct IgemmArgs {
   int wg_c, wg_rs;   // OK_WGRAD_OIHW: C and R*S
   int sub_sh, sub_sw, sub_a, sub_b, sub_H, sub_W;  // OK_NCHW_SUB: strides, phase, full extents
   FastDiv f_wsub;    // OK_NCHW_SUB: divide by the phase's width
+  int act;           // epilogue: 0 none, 1 ReLU, 2 zero where mask <= 0 (mask laid out like d)
+  const void* mask;
   ConvGeom g;
 };
 
@@ -268,7 +270,38 @@ template <> struct Mma<float> {
 
 // ---------------------------------------------------------------- output store
 template <typename T, int OUT>
-__device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int col, float v) {
+__device__ __forceinline__ long out_index(const IgemmArgs& args, int row, int col) {
+  if (OUT == OK_DENSE) return (long)row * args.ldd + col;
+  if (OUT == OK_DENSE_T) return (long)col * args.ldd + row;
+  if (OUT == OK_NCHW) {
+    uint32_t n, hw;
+    args.f_hwo.divmod((uint32_t)col, n, hw);
+    return ((long)n * args.M + row) * args.hwo + hw;
+  }
+  if (OUT == OK_NCHW_SUB) {
+    uint32_t n, hw, hh, ww;
+    args.f_hwo.divmod((uint32_t)col, n, hw);
+    args.f_wsub.divmod(hw, hh, ww);
+    return (((long)n * args.M + row) * args.sub_H + args.sub_sh * (int)hh + args.sub_a) * args.sub_W +
+           args.sub_sw * (int)ww + args.sub_b;
+  }
+  uint32_t rs, c;  // OK_WGRAD_OIHW
+  args.f_cw.divmod((uint32_t)col, rs, c);
+  return ((long)row * args.wg_c + c) * args.wg_rs + rs;
+}
+
+// Epilogue mask (act 2): true where the mask value at the output element is positive.
+template <typename T, int OUT>
+__device__ __forceinline__ bool mask_keep(const IgemmArgs& args, int row, int col) {
+  using S = typename Elem<T>::storage;
+  if (row >= args.M || col >= args.N) return false;
+  return Elem<T>::to_f32(reinterpret_cast<const S*>(args.mask)[out_index<T, OUT>(args, row, col)]) > 0.f;
+}
+
+// keep: the act-2 mask test for this element (computed by mask_keep, possibly
+// ahead of earlier stores).
+template <typename T, int OUT>
+__device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int col, float v, bool keep = true) {
   using S = typename Elem<T>::storage;
   if (row >= args.M || col >= args.N) return;
   if (OUT == OK_PARTIAL) {
@@ -279,26 +312,9 @@ __device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int co
   if (args.bias_mode == 1) v += Elem<T>::to_f32(reinterpret_cast<const S*>(args.bias)[row]);
   else if (args.bias_mode == 2) v += Elem<T>::to_f32(reinterpret_cast<const S*>(args.bias)[col]);
   S* d = reinterpret_cast<S*>(args.d);
-  long idx;
-  if (OUT == OK_DENSE) {
-    idx = (long)row * args.ldd + col;
-  } else if (OUT == OK_DENSE_T) {
-    idx = (long)col * args.ldd + row;
-  } else if (OUT == OK_NCHW) {
-    uint32_t n, hw;
-    args.f_hwo.divmod((uint32_t)col, n, hw);
-    idx = ((long)n * args.M + row) * args.hwo + hw;
-  } else if (OUT == OK_NCHW_SUB) {
-    uint32_t n, hw, hh, ww;
-    args.f_hwo.divmod((uint32_t)col, n, hw);
-    args.f_wsub.divmod(hw, hh, ww);
-    idx = (((long)n * args.M + row) * args.sub_H + args.sub_sh * (int)hh + args.sub_a) * args.sub_W +
-          args.sub_sw * (int)ww + args.sub_b;
-  } else {  // OK_WGRAD_OIHW
-    uint32_t rs, c;
-    args.f_cw.divmod((uint32_t)col, rs, c);
-    idx = ((long)row * args.wg_c + c) * args.wg_rs + rs;
-  }
+  const long idx = out_index<T, OUT>(args, row, col);
+  if (args.act == 1) v = fmaxf(v, 0.f);
+  else if (args.act == 2 && !keep) v = 0.f;
   d[idx] = Elem<T>::from_f32(v);
 }
 
@@ -410,6 +426,18 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
     __syncthreads();
   }
 
+  // the act-2 mask values are read before the first store (a load may not pass
+  // a store to possibly the same memory, so interleaving would serialise them)
+  bool keep[FM][FN][MM::NACC];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < MM::NACC; ++v)
+        keep[i][j][v] = OUT != OK_PARTIAL && args.act == 2 &&
+                        mask_keep<T, OUT>(args, m0 + wm + i * MM::TM + MM::acc_row(lane, v),
+                                          n0 + wn + j * MM::TN + MM::acc_col(lane));
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -417,7 +445,7 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
 #pragma unroll
       for (int v = 0; v < MM::NACC; ++v)
         store_out<T, OUT>(args, m0 + wm + i * MM::TM + MM::acc_row(lane, v),
-                          n0 + wn + j * MM::TN + MM::acc_col(lane), acc[i][j][v]);
+                          n0 + wn + j * MM::TN + MM::acc_col(lane), acc[i][j][v], keep[i][j][v]);
 }
 
 // Split-K reduction: out(row, col) = sum_z ws[z][row][col] (+ bias), stored by
@@ -426,7 +454,8 @@ template <typename T, int OUT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(IgemmArgs args, const float* ws, int splits) {
   const long total = (long)args.M * args.N;
   reduce_splits_block(ws, splits, total, [&](long i, float s) {
-    store_out<T, OUT>(args, (int)(i / args.N), (int)(i % args.N), s);
+    const int row = (int)(i / args.N), col = (int)(i % args.N);
+    store_out<T, OUT>(args, row, col, s, args.act == 2 && mask_keep<T, OUT>(args, row, col));
   });
 }
 

@@ -84,7 +84,8 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
 // the shape is outside the kernel's envelope.
 size_t halo_conv_bf16_ws(int C, int O, int R, int S);
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
-                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st);
+                   int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st, int act = 0,
+                   const void* mask = nullptr);
 
 // ---- stride-1 bf16 weight gradient (vh_wgrad.hip) ----
 // Workspace bytes needed (0 if the shape is outside the kernel's envelope).

@@ -75,12 +75,14 @@ class Conv2d:
         B, C, O, H, W, KH, KW, SH, SW, PH, PW = self._dims(x)
         return (B, O, conv_out(H, KH, SH, PH), conv_out(W, KW, SW, PW))
 
-    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None, relu: bool = False) -> torch.Tensor:
+        """relu=True: the layer followed by ReLU, fused (vh_conv2d_forward_relu)."""
         dt = _same_dtype(x, self.weight, self.bias)
         y = out if out is not None else torch.empty(self.output_shape(x), dtype=x.dtype, device=x.device)
         used = ctypes.c_int(-1)
-        check(lib().vh_conv2d_forward(dt, int(self.algo), ptr(x), ptr(self.weight), ptr(self.bias), ptr(y),
-                                      *self._dims(x), ctypes.byref(used), stream_ptr(x.device)))
+        fn = lib().vh_conv2d_forward_relu if relu else lib().vh_conv2d_forward
+        check(fn(dt, int(self.algo), ptr(x), ptr(self.weight), ptr(self.bias), ptr(y), *self._dims(x),
+                 ctypes.byref(used), stream_ptr(x.device)))
         self.last_algo = ConvAlgo(used.value)
         return y
 
@@ -88,8 +90,10 @@ class Conv2d:
 
     def backward(self, out_grad: torch.Tensor, x: torch.Tensor, input_grad: bool = True,
                  weight_grad: bool = True, algo: Optional[ConvAlgo] = None,
-                 outs: Optional[Tuple] = None):
-        """Returns (grad_input, grad_weight, grad_bias); None where not requested."""
+                 outs: Optional[Tuple] = None, relu_input: bool = False):
+        """Returns (grad_input, grad_weight, grad_bias); None where not requested.
+        relu_input=True: x came out of a ReLU; grad_input gets that ReLU's backward
+        (zero where x <= 0), fused (vh_conv2d_backward_relu)."""
         algo = ConvAlgo(algo if algo is not None else (self.last_algo if self.last_algo is not None else self.algo))
         if algo == ConvAlgo.Auto:
             B, C, O, H, W, KH, KW, SH, SW, PH, PW = self._dims(x)
@@ -101,8 +105,9 @@ class Conv2d:
             dx = torch.empty_like(x) if input_grad else None
             dw = torch.empty_like(self.weight) if weight_grad else None
             db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
-        check(lib().vh_conv2d_backward(dt, int(algo), ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw),
-                                       ptr(db), *self._dims(x), stream_ptr(x.device)))
+        fn = lib().vh_conv2d_backward_relu if relu_input else lib().vh_conv2d_backward
+        check(fn(dt, int(algo), ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw), ptr(db), *self._dims(x),
+                 stream_ptr(x.device)))
         return dx, dw, db
 
 
