@@ -263,6 +263,22 @@ int vh_sum_reduce(int dtype, const void* input, int64_t n, float* result, void* 
  * (autograd.rs:49-62). */
 int vh_sum_backward(int dtype, float grad, void* grad_input, int64_t n, void* stream);
 
+/* ---- The step after the weight gradient ---- */
+/* autograd.rs:158-184 accumulate_grad (gpu_add, gpu_ops.rs:17): existing += new_grad,
+ * in place (the reference allocates the sum and drops the old buffer). */
+int vh_grad_accumulate(int dtype, void* existing, const void* new_grad, int64_t n, void* stream);
+#define VH_OPT_SGD 0
+#define VH_OPT_SGD_MOMENTUM 1
+#define VH_OPT_ADAM 2
+/* gpu_ops.rs:496 gpu_optimizer_step (optimizer_step.wgsl; SGD::step's GPU path,
+ * sgd.rs:94-180): one update of n f32 parameters in place.  g = grad (+ weight_decay *
+ * param); SGD: param -= lr*g; momentum: s1 = beta1*s1 - lr*g, param += s1 (s1 = the
+ * velocity); Adam: s1/s2 = first/second moments, bias correction with step t.
+ * state1 may be NULL for op 0, state2 for ops 0 and 1. */
+int vh_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps,
+                      float weight_decay, float* params, const float* grads, float* state1,
+                      float* state2, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ def lib():
         _lib.or_sum.restype = ctypes.c_float
         _lib.or_sum.argtypes = [_FP, _SZ]
         _lib.or_sum_backward.argtypes = [ctypes.c_float, _FP, _SZ]
+        _lib.or_optimizer_step.argtypes = [ctypes.c_int] + [ctypes.c_float] * 6 + [_FP, _FP, _FP, _FP, _SZ]
     return _lib
 
 
@@ -310,6 +311,25 @@ def sum_backward(grad: float, shape):
     dx = np.empty(shape, np.float32)
     lib().or_sum_backward(ctypes.c_float(grad), _p(dx), _SZ(dx.size))
     return dx
+
+
+def add(a, b):
+    """gpu_add / accumulate_grad: a + b (f32)."""
+    out = _f32(a).copy()
+    b = _f32(b)
+    lib().or_add_inplace(_p(out), _p(b), _SZ(out.size))
+    return out
+
+
+def optimizer_step(op, lr, param, grad, s1=None, s2=None, beta1=0.0, beta2=0.0, t=0.0, eps=0.0, weight_decay=0.0):
+    """optimizer_step.wgsl on copies; returns (param, s1, s2)."""
+    param = _f32(param).copy()
+    grad = _f32(grad)
+    s1 = np.zeros_like(param) if s1 is None else _f32(s1).copy()
+    s2 = np.zeros_like(param) if s2 is None else _f32(s2).copy()
+    lib().or_optimizer_step(op, lr, beta1, beta2, t, eps, weight_decay, _p(param), _p(grad), _p(s1), _p(s2),
+                            _SZ(param.size))
+    return param, s1, s2
 
 
 def round_bf16(a) -> np.ndarray:

@@ -661,6 +661,41 @@ void or_sum_backward(float grad, float *dx, size_t n) {
 }
 
 /* ---------------------------------------------------------------------------
+ * The step after the weight gradient.
+ * Gradient accumulation, autograd.rs:158-184: existing += new (gpu_add).
+ * Optimizer step, optimizer_step.wgsl (the GPU path of SGD::step, sgd.rs:94-180;
+ * op 0 SGD, 1 SGD + momentum, 2 Adam), per element, f32, unfused:
+ *   g = grad (+ weight_decay * param when weight_decay != 0)
+ *   0: param -= lr * g
+ *   1: v = beta1 * v - lr * g; param += v
+ *   2: m = beta1*m + (1-beta1)*g; v = beta2*v + (1-beta2)*g*g;
+ *      param -= lr * (m / (1 - beta1^t)) / (sqrt(v / (1 - beta2^t)) + eps)
+ * ------------------------------------------------------------------------- */
+void or_add_inplace(float *a, const float *b, size_t n) {
+    for (size_t i = 0; i < n; ++i) a[i] += b[i];
+}
+
+void or_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps, float wd,
+                       float *param, const float *grad, float *s1, float *s2, size_t n) {
+    const float mh = 1.0f / (1.0f - powf(beta1, t)), vh = 1.0f / (1.0f - powf(beta2, t));
+    for (size_t i = 0; i < n; ++i) {
+        float g = grad[i];
+        if (wd != 0.0f) g = g + wd * param[i];
+        if (op == 0) {
+            param[i] = param[i] - lr * g;
+        } else if (op == 1) {
+            s1[i] = beta1 * s1[i] - lr * g;
+            param[i] = param[i] + s1[i];
+        } else {
+            s1[i] = beta1 * s1[i] + (1.0f - beta1) * g;
+            s2[i] = beta2 * s2[i] + (1.0f - beta2) * g * g;
+            const float m_hat = s1[i] * mh, v_hat = s2[i] * vh;
+            param[i] = param[i] - lr * m_hat / (sqrtf(v_hat) + eps);
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------
  * bf16 storage conversion: Storage::to_dtype(BF16) goes through
  * half::bf16::from_f32 (storage.rs:503-505, half 2.7.1), round-to-nearest-even
  * with NaN kept quiet.  The bf16 oracle is f32 math on inputs rounded this way.

@@ -439,3 +439,40 @@ def test_conv2d_fused_relu_fwd_and_masked_dgrad(case, algo, dt):
     # the weight and bias gradients are those of the plain backward
     check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw)
     check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+
+
+# ------------------------------------------------------------------ the step after dW
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_grad_accumulate_matches_oracle(dt):
+    g = rng(5)
+    for n in (1, 1000, 782336):
+        a, at = prep(g.standard_normal(n), dt)
+        b, bt = prep(g.standard_normal(n), dt)
+        got = host(ops.gpu_add(at, bt))
+        want = oracle.add(a, b)
+        want = oracle.round_bf16(want) if dt == "bf16" else want
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("op", [0, 1, 2])
+@pytest.mark.parametrize("wd", [0.0, 0.01])
+def test_optimizer_step_matches_oracle(op, wd):
+    g = rng(op * 10 + int(wd * 100))
+    n = 782336  # configs[2]'s weight count
+    p0 = g.standard_normal(n).astype(np.float32)
+    gr = g.standard_normal(n).astype(np.float32)
+    s10 = (g.standard_normal(n) * 0.1).astype(np.float32)
+    s20 = (np.abs(g.standard_normal(n)) * 0.01).astype(np.float32)
+    pt, gt, s1t, s2t = (torch.from_numpy(a.copy()).to(DEV) for a in (p0, gr, s10, s20))
+    kw = dict(beta1=0.9, beta2=0.999, t=3.0, eps=1e-8, weight_decay=wd)
+    for step in range(2):  # two steps: the states carry over
+        ops.gpu_optimizer_step(pt, gt, s1t, s2t, op, 1e-2, **kw)
+        p0, s10, s20 = oracle.optimizer_step(op, 1e-2, p0, gr, s10, s20, **kw)
+    got = host(pt)
+    if op < 2:
+        assert np.array_equal(got, p0)  # same formula and order, no contraction: bit-identical
+        if op == 1:
+            assert np.array_equal(host(s1t), s10)
+    else:
+        # Adam: sqrt / division may differ in the last bit
+        assert np.abs(got - p0).max() <= 4 * np.spacing(np.abs(p0)).max()

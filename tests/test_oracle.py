@@ -343,6 +343,46 @@ def test_sum_known_answers_and_float64_bound():
     assert np.array_equal(orc.sum_backward(2.5, (2, 3)), np.full((2, 3), 2.5, np.float32))
 
 
+# ----------------------------------------------------------------- the step after dW
+def test_optimizer_step_reference_known_answers():
+    # tests/test_optimizers.rs:169-197 (SGD), 199-224 (weight decay)
+    p, _, _ = orc.optimizer_step(0, 0.1, np.array([5.0], np.float32), np.array([2.0], np.float32))
+    assert abs(p[0] - 4.8) < 1e-7
+    p, _, _ = orc.optimizer_step(0, 0.1, p, np.array([2.0], np.float32))
+    assert abs(p[0] - np.float32(np.float32(4.8) - np.float32(0.2))) < 1e-7
+    p, _, _ = orc.optimizer_step(0, 0.1, np.array([4.0], np.float32), np.array([1.0], np.float32), weight_decay=0.1)
+    assert abs(p[0] - 3.86) < 1e-7
+    # tests/coverage_fill.rs:46-66 (momentum 0.9, lr 0.1, grad 0.1)
+    p, v, _ = orc.optimizer_step(1, 0.1, np.array([1.0], np.float32), np.array([0.1], np.float32), beta1=0.9)
+    assert abs(p[0] - 0.99) < 1e-6
+    p, v, _ = orc.optimizer_step(1, 0.1, p, np.array([0.1], np.float32), s1=v, beta1=0.9)
+    assert abs(p[0] - 0.971) < 1e-6
+
+
+def test_optimizer_step_vs_float64_formulas():
+    n = 1000
+    p0, g, m0, v0 = randn(n), randn(n), randn(n) * 0.1, np.abs(randn(n)) * 0.01
+    for wd in (0.0, 0.01):
+        ge = g.astype(np.float64) + wd * p0.astype(np.float64)
+        p, _, _ = orc.optimizer_step(0, 0.05, p0, g, weight_decay=wd)
+        assert close(p, p0 - 0.05 * ge, 1e-6)
+        p, v, _ = orc.optimizer_step(1, 0.05, p0, g, s1=m0, beta1=0.9, weight_decay=wd)
+        ve = 0.9 * m0 - 0.05 * ge
+        assert close(v, ve, 1e-6) and close(p, p0 + ve, 1e-6)
+        t = 3.0
+        p, m, v = orc.optimizer_step(2, 1e-3, p0, g, s1=m0, s2=v0, beta1=0.9, beta2=0.999, t=t, eps=1e-8,
+                                     weight_decay=wd)
+        me = 0.9 * m0 + 0.1 * ge
+        vv = 0.999 * v0 + 0.001 * ge * ge
+        pe = p0 - 1e-3 * (me / (1 - 0.9 ** t)) / (np.sqrt(vv / (1 - 0.999 ** t)) + 1e-8)
+        assert close(m, me, 1e-6) and close(v, vv, 1e-5) and close(p, pe, 1e-6)
+
+
+def test_grad_accumulate():
+    a, b = randn(500), randn(500)
+    assert np.array_equal(orc.add(a, b), (a + b).astype(np.float32))
+
+
 # ----------------------------------------------------------------- bf16 rounding
 def test_bf16_rne_matches_torch():
     vals = np.concatenate([randn(4096) * 1e3, np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875,

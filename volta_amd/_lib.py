@@ -28,6 +28,7 @@ BF16 = 1
 ALGO_DIRECT, ALGO_IM2COL, ALGO_IGEMM, ALGO_AUTO = 0, 1, 2, 3
 POLICY_FASTEST, POLICY_GENERIC = 0, 1
 UNARY_RELU = 0
+OPT_SGD, OPT_SGD_MOMENTUM, OPT_ADAM = 0, 1, 2
 
 
 class VoltaHipError(RuntimeError):
@@ -82,6 +83,8 @@ SIGNATURES = {
     "vh_unary_backward": [_INT, _INT, _P, _P, _P, _I64, _P],
     "vh_sum_reduce": [_INT, _P, _I64, _P, _P],
     "vh_sum_backward": [_INT, ctypes.c_float, _P, _I64, _P],
+    "vh_grad_accumulate": [_INT, _P, _P, _I64, _P],
+    "vh_optimizer_step": [_INT] + [ctypes.c_float] * 6 + [_P, _P, _P, _P, _I64, _P],
 }
 
 _lib = None

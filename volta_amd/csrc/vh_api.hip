@@ -1113,6 +1113,30 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
                      (int)width, (int)upscale, 1, S(stream));
 }
 
+// ------------------------------------------------------------------ the step after dW
+int vh_grad_accumulate(int dtype, void* existing, const void* new_grad, int64_t n, void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(dtype));
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!existing || !new_grad) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return VH_DISPATCH(dtype, run_add_inplace, existing, new_grad, (long)n, S(stream));
+}
+
+int vh_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps, float weight_decay,
+                      float* params, const float* grads, float* state1, float* state2, int64_t n, void* stream) {
+  VH_ENTRY();
+  if (op < VH_OPT_SGD || op > VH_OPT_ADAM) return set_error(VH_ERR_BAD_ARG, "bad optimizer op %d", op);
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!params || !grads || (op >= VH_OPT_SGD_MOMENTUM && !state1) || (op == VH_OPT_ADAM && !state2))
+    return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return run_optimizer_step(op, lr, beta1, beta2, t, eps, weight_decay, params, grads, state1, state2, (long)n,
+                            S(stream));
+}
+
 // ------------------------------------------------------------------ glue of the config graphs
 int vh_unary(int dtype, int op, const void* input, void* output, int64_t n, void* stream) {
   VH_ENTRY();

@@ -3,6 +3,7 @@
 #include "vh_kernels.hpp"
 
 #include <algorithm>
+#include <cmath>
 
 namespace vh {
 
@@ -594,6 +595,44 @@ __global__ __launch_bounds__(256) void sum_partials_scalar_kernel(const float* _
   if (threadIdx.x == 0) out[0] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// ============================================================== the step after dW
+// a += b (gradient accumulation).
+template <typename T>
+__global__ __launch_bounds__(256) void add_inplace_kernel(typename Elem<T>::storage* __restrict__ a,
+                                                          const typename Elem<T>::storage* __restrict__ b, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+    a[i] = Elem<T>::from_f32(Elem<T>::to_f32(a[i]) + Elem<T>::to_f32(b[i]));
+}
+
+// One optimizer update per element, f32, the formulas of the WGSL optimizer
+// step in the same order, without contraction into FMAs.
+__global__ __launch_bounds__(256) void optimizer_step_kernel(float* __restrict__ param,
+                                                             const float* __restrict__ grad, float* __restrict__ s1,
+                                                             float* __restrict__ s2, int op, float lr, float beta1,
+                                                             float beta2, float mh, float vh, float eps, float wd,
+                                                             long n) {
+#pragma clang fp contract(off)
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) {
+    float g = grad[i];
+    float p = param[i];
+    if (wd != 0.f) g = g + wd * p;
+    if (op == 0) {
+      p = p - lr * g;
+    } else if (op == 1) {
+      const float v = beta1 * s1[i] - lr * g;
+      s1[i] = v;
+      p = p + v;
+    } else {
+      const float m = beta1 * s1[i] + (1.f - beta1) * g;
+      const float v = beta2 * s2[i] + (1.f - beta2) * g * g;
+      s1[i] = m;
+      s2[i] = v;
+      p = p - lr * (m * mh) / (sqrtf(v * vh) + eps);
+    }
+    param[i] = p;
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void fill_kernel(typename Elem<T>::storage* __restrict__ y, long n, float v) {
   const typename Elem<T>::storage e = Elem<T>::from_f32(v);
@@ -844,6 +883,26 @@ int run_fill(void* y, long n, float v, hipStream_t st) {
   return VH_OK;
 }
 
+template <typename T>
+int run_add_inplace(void* a, const void* b, long n, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  if (n <= 0) return VH_OK;
+  add_inplace_kernel<T><<<grid_for(n), 256, 0, st>>>((S*)a, (const S*)b, n);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps, float wd, float* param,
+                       const float* grad, float* s1, float* s2, long n, hipStream_t st) {
+  if (n <= 0) return VH_OK;
+  // the bias-correction factors are per step, not per element: computed once here
+  const float mh = op == 2 ? 1.0f / (1.0f - powf(beta1, t)) : 1.f;
+  const float vh = op == 2 ? 1.0f / (1.0f - powf(beta2, t)) : 1.f;
+  optimizer_step_kernel<<<grid_for(n), 256, 0, st>>>(param, grad, s1, s2, op, lr, beta1, beta2, mh, vh, eps, wd, n);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 #define VH_INST(T)                                                                                      \
   template int run_direct_fwd<T>(const void*, const void*, const void*, void*, const ConvGeom&, hipStream_t); \
   template int run_col2im_t<T>(const float*, void*, int, int, int, int, int, int, int, int, int, int, int, int,  \
@@ -866,7 +925,8 @@ int run_fill(void* y, long n, float v, hipStream_t st) {
   template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);     \
   template int run_relu<T>(const void*, const void*, void*, long, hipStream_t);                         \
   template int run_sum<T>(const void*, long, float*, float*, hipStream_t);                              \
-  template int run_fill<T>(void*, long, float, hipStream_t);
+  template int run_fill<T>(void*, long, float, hipStream_t);                                            \
+  template int run_add_inplace<T>(void*, const void*, long, hipStream_t);
 VH_INST(float)
 VH_INST(bf16)
 #undef VH_INST

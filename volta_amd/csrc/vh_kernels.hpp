@@ -53,6 +53,12 @@ template <typename T>
 int run_sum(const void* x, long n, float* out, float* ws, hipStream_t st);
 template <typename T>
 int run_fill(void* y, long n, float v, hipStream_t st);
+// The step after dW: a += b; one optimizer update (op 0 SGD, 1 SGD + momentum,
+// 2 Adam) over n f32 parameters.
+template <typename T>
+int run_add_inplace(void* a, const void* b, long n, hipStream_t st);
+int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps, float wd, float* param,
+                       const float* grad, float* s1, float* s2, long n, hipStream_t st);
 // Weights of the stride phases of an input gradient in one pass: phase p is
 // dst + off[p]: [c][i][j][o] = w[o][c][kh0[p] + sh*i][kw0[p] + sw*j], i < rc[p], j < sc[p].
 struct PhaseTable {

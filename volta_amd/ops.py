@@ -244,3 +244,28 @@ def gpu_sum_backward(grad: float, input_size: int, dtype=torch.float32, device="
             return None
         raise
     return out
+
+
+# ---------------------------------------------------------------- the step after dW
+@_optional
+def gpu_add(a: torch.Tensor, b: torch.Tensor):
+    """gpu_ops.rs:17 as used by accumulate_grad (autograd.rs:158-184): a + b."""
+    dt = _same_dtype(a, b)
+    if a.numel() != b.numel():
+        raise ValueError("gpu_add: size mismatch")
+    out = a.clone()
+    _call("vh_grad_accumulate", dt, ptr(out), ptr(b), out.numel(), stream_ptr(a.device))
+    return out
+
+
+@_optional
+def gpu_optimizer_step(params: torch.Tensor, grads: torch.Tensor, state1: torch.Tensor, state2: torch.Tensor,
+                       op: int, lr: float, beta1: float = 0.0, beta2: float = 0.0, t: float = 0.0, eps: float = 0.0,
+                       weight_decay: float = 0.0):
+    """gpu_ops.rs:496 -- updates params (and the states) in place; f32 tensors."""
+    for x in (params, grads, state1, state2):
+        if x.dtype != torch.float32:
+            raise TypeError("gpu_optimizer_step takes float32 tensors")
+    _call("vh_optimizer_step", op, lr, beta1, beta2, t, eps, weight_decay, ptr(params), ptr(grads), ptr(state1),
+          ptr(state2), params.numel(), stream_ptr(params.device))
+    return ()
