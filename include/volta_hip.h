@@ -263,6 +263,17 @@ int vh_sum_reduce(int dtype, const void* input, int64_t n, float* result, void* 
  * (autograd.rs:49-62). */
 int vh_sum_backward(int dtype, float grad, void* grad_input, int64_t n, void* stream);
 
+/* ---- Device storage: dtype and layout (the reference keeps device data f32 and
+ * NCHW, storage.rs:570-597; these let it stay bf16 and convert layouts on the GPU) ---- */
+/* n elements: bf16 -> f32 exact, f32 -> bf16 round-to-nearest-even (as half::bf16::from_f32,
+ * storage.rs:503-505); equal dtypes copy. */
+int vh_cast(int src_dtype, int dst_dtype, const void* src, void* dst, int64_t n, void* stream);
+/* [B][C][H][W] <-> [B][H][W][C]; src and dst must not overlap. */
+int vh_nchw_to_nhwc(int dtype, const void* src, void* dst, int64_t batch, int64_t channels,
+                    int64_t height, int64_t width, void* stream);
+int vh_nhwc_to_nchw(int dtype, const void* src, void* dst, int64_t batch, int64_t channels,
+                    int64_t height, int64_t width, void* stream);
+
 /* ---- The step after the weight gradient ---- */
 /* autograd.rs:158-184 accumulate_grad (gpu_add, gpu_ops.rs:17): existing += new_grad,
  * in place (the reference allocates the sum and drops the old buffer). */

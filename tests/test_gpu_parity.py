@@ -476,3 +476,29 @@ def test_optimizer_step_matches_oracle(op, wd):
     else:
         # Adam: sqrt / division may differ in the last bit
         assert np.abs(got - p0).max() <= 4 * np.spacing(np.abs(p0)).max()
+
+
+# ------------------------------------------------------------------ device storage: dtype and layout
+def test_casts_match_bf16_rne():
+    g = rng(77)
+    x = np.concatenate([g.standard_normal(100000).astype(np.float32) * 1e3,
+                        np.array([0.0, -0.0, 1.00390625, 1.01171875, 3.4e38, -3.4e38, 1e-40, np.inf, -np.inf,
+                                  np.nan], np.float32)])
+    xt = torch.from_numpy(x).to(DEV)
+    b = ops.to_dtype(xt, torch.bfloat16)
+    bits = b.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(bits[:-1], oracle.bf16_bits(x)[:-1])
+    assert np.isnan(host(b)[-1])
+    back = host(ops.to_dtype(b, torch.float32))
+    assert np.array_equal(back[:-1], oracle.round_bf16(x)[:-1])
+    assert np.array_equal(host(ops.to_dtype(xt, torch.float32)), x, equal_nan=True)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("shape", [(2, 3, 5, 7), (1, 64, 56, 56), (3, 33, 17, 9), (16, 27, 256, 256)])
+def test_layout_transforms_exact(shape, dt):
+    g = rng(sum(shape))
+    x, xt = prep(g.standard_normal(shape), dt)
+    y = ops.nchw_to_nhwc(xt)
+    assert np.array_equal(host(y), np.ascontiguousarray(x.transpose(0, 2, 3, 1)))
+    assert np.array_equal(host(ops.nhwc_to_nchw(y)), x)

@@ -83,6 +83,9 @@ SIGNATURES = {
     "vh_unary_backward": [_INT, _INT, _P, _P, _P, _I64, _P],
     "vh_sum_reduce": [_INT, _P, _I64, _P, _P],
     "vh_sum_backward": [_INT, ctypes.c_float, _P, _I64, _P],
+    "vh_cast": [_INT, _INT, _P, _P, _I64, _P],
+    "vh_nchw_to_nhwc": [_INT, _P, _P] + [_I64] * 4 + [_P],
+    "vh_nhwc_to_nchw": [_INT, _P, _P] + [_I64] * 4 + [_P],
     "vh_grad_accumulate": [_INT, _P, _P, _I64, _P],
     "vh_optimizer_step": [_INT] + [ctypes.c_float] * 6 + [_P, _P, _P, _P, _I64, _P],
 }

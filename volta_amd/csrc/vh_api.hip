@@ -1113,6 +1113,41 @@ int vh_pixel_shuffle_backward(int dtype, const void* out_grad, void* grad_input,
                      (int)width, (int)upscale, 1, S(stream));
 }
 
+// ------------------------------------------------------------------ storage: casts and layouts
+int vh_cast(int src_dtype, int dst_dtype, const void* src, void* dst, int64_t n, void* stream) {
+  VH_ENTRY();
+  VH_TRY(check_dtype(src_dtype));
+  VH_TRY(check_dtype(dst_dtype));
+  if (n < 0) return set_error(VH_ERR_BAD_SHAPE, "negative element count");
+  VH_TRY(check_sizes({(long)n}));
+  if (n == 0) return VH_OK;
+  if (!src || !dst) return set_error(VH_ERR_BAD_ARG, "null pointer");
+  return run_cast(src_dtype, dst_dtype, src, dst, (long)n, S(stream));
+}
+
+static int layout_transform(int dtype, const void* src, void* dst, int64_t B, int64_t C, int64_t H, int64_t W,
+                            bool to_nhwc, void* stream) {
+  VH_TRY(check_dtype(dtype));
+  if (B < 0 || C <= 0 || H <= 0 || W <= 0) return set_error(VH_ERR_BAD_SHAPE, "bad NCHW geometry");
+  VH_TRY(check_sizes({(long)(B * C * H * W)}));
+  if (B == 0) return VH_OK;
+  if (!src || !dst || src == dst) return set_error(VH_ERR_BAD_ARG, "null or aliased pointer");
+  const int R = to_nhwc ? (int)C : (int)(H * W), Cc = to_nhwc ? (int)(H * W) : (int)C;
+  return VH_DISPATCH(dtype, run_batched_transpose, src, dst, (int)B, R, Cc, S(stream));
+}
+
+int vh_nchw_to_nhwc(int dtype, const void* src, void* dst, int64_t batch, int64_t channels, int64_t height,
+                    int64_t width, void* stream) {
+  VH_ENTRY();
+  return layout_transform(dtype, src, dst, batch, channels, height, width, true, stream);
+}
+
+int vh_nhwc_to_nchw(int dtype, const void* src, void* dst, int64_t batch, int64_t channels, int64_t height,
+                    int64_t width, void* stream) {
+  VH_ENTRY();
+  return layout_transform(dtype, src, dst, batch, channels, height, width, false, stream);
+}
+
 // ------------------------------------------------------------------ the step after dW
 int vh_grad_accumulate(int dtype, void* existing, const void* new_grad, int64_t n, void* stream) {
   VH_ENTRY();

@@ -595,6 +595,39 @@ __global__ __launch_bounds__(256) void sum_partials_scalar_kernel(const float* _
   if (threadIdx.x == 0) out[0] = (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// ============================================================== storage: casts and layouts
+// dtype conversion: bf16 -> f32 exact, f32 -> bf16 round-to-nearest-even (NaN kept quiet).
+template <typename From, typename To>
+__global__ __launch_bounds__(256) void cast_kernel(const typename Elem<From>::storage* __restrict__ src,
+                                                   typename Elem<To>::storage* __restrict__ dst, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+    dst[i] = Elem<To>::from_f32(Elem<From>::to_f32(src[i]));
+}
+
+// out[b][c][r] = in[b][r][c] for B matrices of R x Cc (NCHW <-> NHWC: R = C, Cc =
+// H*W or the reverse); 32 x 32 tiles through LDS, both sides coalesced.
+template <typename T>
+__global__ __launch_bounds__(256) void batched_transpose_kernel(const typename Elem<T>::storage* __restrict__ in,
+                                                                typename Elem<T>::storage* __restrict__ out, int R,
+                                                                int Cc) {
+  using S = typename Elem<T>::storage;
+  __shared__ S t[32][33];
+  const long off = (long)blockIdx.z * R * Cc;
+  const int r0 = blockIdx.y * 32, c0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+  for (int k = 0; k < 32; k += 8) {
+    const int r = r0 + ty + k, c = c0 + tx;
+    if (r < R && c < Cc) t[ty + k][tx] = in[off + (long)r * Cc + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 32; k += 8) {
+    const int c = c0 + ty + k, r = r0 + tx;
+    if (c < Cc && r < R) out[off + (long)c * R + r] = t[tx][ty + k];
+  }
+}
+
 // ============================================================== the step after dW
 // a += b (gradient accumulation).
 template <typename T>
@@ -892,6 +925,31 @@ int run_add_inplace(void* a, const void* b, long n, hipStream_t st) {
   return VH_OK;
 }
 
+int run_cast(int from, int to, const void* src, void* dst, long n, hipStream_t st) {
+  if (n <= 0) return VH_OK;
+  if (from == to) {
+    VH_HIP_CHECK(hipMemcpyAsync(dst, src, (size_t)n * (from == VH_BF16 ? 2 : 4), hipMemcpyDeviceToDevice, st));
+    return VH_OK;
+  }
+  if (from == VH_F32)
+    cast_kernel<float, bf16><<<grid_for(n), 256, 0, st>>>((const float*)src, (uint16_t*)dst, n);
+  else
+    cast_kernel<bf16, float><<<grid_for(n), 256, 0, st>>>((const uint16_t*)src, (float*)dst, n);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_batched_transpose(const void* in, void* out, int B, int R, int Cc, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  if ((long)B * R * Cc <= 0) return VH_OK;
+  if ((R + 31) / 32 > 65535 || B > 65535) return set_error(VH_ERR_UNSUPPORTED, "layout transform too large");
+  dim3 grid((unsigned)((Cc + 31) / 32), (unsigned)((R + 31) / 32), (unsigned)B);
+  batched_transpose_kernel<T><<<grid, 256, 0, st>>>((const S*)in, (S*)out, R, Cc);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, float eps, float wd, float* param,
                        const float* grad, float* s1, float* s2, long n, hipStream_t st) {
   if (n <= 0) return VH_OK;
@@ -926,7 +984,8 @@ int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, floa
   template int run_relu<T>(const void*, const void*, void*, long, hipStream_t);                         \
   template int run_sum<T>(const void*, long, float*, float*, hipStream_t);                              \
   template int run_fill<T>(void*, long, float, hipStream_t);                                            \
-  template int run_add_inplace<T>(void*, const void*, long, hipStream_t);
+  template int run_add_inplace<T>(void*, const void*, long, hipStream_t);                              \
+  template int run_batched_transpose<T>(const void*, void*, int, int, int, hipStream_t);
 VH_INST(float)
 VH_INST(bf16)
 #undef VH_INST

@@ -53,6 +53,10 @@ template <typename T>
 int run_sum(const void* x, long n, float* out, float* ws, hipStream_t st);
 template <typename T>
 int run_fill(void* y, long n, float v, hipStream_t st);
+// Storage: dtype casts (f32 -> bf16 RNE) and batched transposes (out[b][c][r] = in[b][r][c]).
+int run_cast(int from, int to, const void* src, void* dst, long n, hipStream_t st);
+template <typename T>
+int run_batched_transpose(const void* in, void* out, int B, int R, int Cc, hipStream_t st);
 // The step after dW: a += b; one optimizer update (op 0 SGD, 1 SGD + momentum,
 // 2 Adam) over n f32 parameters.
 template <typename T>

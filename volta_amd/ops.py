@@ -269,3 +269,25 @@ def gpu_optimizer_step(params: torch.Tensor, grads: torch.Tensor, state1: torch.
     _call("vh_optimizer_step", op, lr, beta1, beta2, t, eps, weight_decay, ptr(params), ptr(grads), ptr(state1),
           ptr(state2), params.numel(), stream_ptr(params.device))
     return ()
+
+
+# ---------------------------------------------------------------- device storage: dtype and layout
+def to_dtype(x: torch.Tensor, dtype) -> torch.Tensor:
+    """Device cast f32 <-> bf16 (RNE), the library's conversion."""
+    out = torch.empty(x.shape, dtype=dtype, device=x.device)
+    _call("vh_cast", dtype_code(x), _DTYPES[dtype], ptr(x), ptr(out), x.numel(), stream_ptr(x.device))
+    return out
+
+
+def nchw_to_nhwc(x: torch.Tensor) -> torch.Tensor:
+    B, C, H, W = x.shape
+    out = torch.empty((B, H, W, C), dtype=x.dtype, device=x.device)
+    _call("vh_nchw_to_nhwc", dtype_code(x), ptr(x), ptr(out), B, C, H, W, stream_ptr(x.device))
+    return out
+
+
+def nhwc_to_nchw(x: torch.Tensor) -> torch.Tensor:
+    B, H, W, C = x.shape
+    out = torch.empty((B, C, H, W), dtype=x.dtype, device=x.device)
+    _call("vh_nhwc_to_nchw", dtype_code(x), ptr(x), ptr(out), B, C, H, W, stream_ptr(x.device))
+    return out
