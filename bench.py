@@ -39,13 +39,20 @@ METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
 # HBM bytes per call of a pass, from two rocprofv3 counter runs of
 # `bench.py --profile-op <pass>` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch,
 # summed over the pass's kernels).  Calibration on the 256 MiB copy of the same
-# runs: WRITE_SIZE reads 262144 KiB (factor 1), FETCH_SIZE 131088 KiB (factor 2).
-# Summary: profiles/c3_wgrad_256_traffic.md.  Keyed by pass name; used for
-# roofline.traffic when that pass is the dominant one.
+# runs (two dispatches of 128 MiB): WRITE_SIZE reads 131080 KiB per dispatch
+# (factor 1), FETCH_SIZE 65550 KiB (factor 2).  Summary:
+# profiles/c3_pass_traffic.md.  Keyed by pass name; used for roofline.traffic
+# when that pass is the dominant one (which of these is the slowest varies by a
+# few percent from run to run).
 MEASURED_TRAFFIC_BYTES = {
-    # wgrad_rows_bf16_kernel: fetch 12746 KiB x2, write 36864 KiB;
-    # wgrad_reduce_bf16_kernel: fetch 18458 KiB x2, write 1152 KiB
-    "3x3 256->256 @14 wgrad": (12746 * 2 + 36864 + 18458 * 2 + 1152) * 1024,
+    # relayout_grouped_kernel: fetch 79.2 KiB x2, write 72; conv_halo_bf16_kernel: fetch 25625.0 x2, write 50176
+    "3x3 64->64 @56 fwd": int(((79.2 + 25625.0) * 2 + 72 + 50176) * 1024),
+    # relayout_grouped_kernel: fetch 214.8 x2, write 72; conv_halo_bf16_kernel: fetch 25620.6 x2, write 50176
+    "3x3 64->64 @56 dgrad": int(((214.8 + 25620.6) * 2 + 72 + 50176) * 1024),
+    # wgrad_rows_bf16_kernel: fetch 25309.2 x2, write 36864; wgrad_reduce_bf16_kernel: fetch 18466.3 x2, write 288
+    "3x3 128->128 @28 wgrad": int(((25309.2 + 18466.3) * 2 + 36864 + 288) * 1024),
+    # wgrad_rows_bf16_kernel: fetch 12769.4 x2, write 36864; wgrad_reduce_bf16_kernel: fetch 18466.5 x2, write 1157.3
+    "3x3 256->256 @14 wgrad": int(((12769.4 + 18466.5) * 2 + 36864 + 1157.3) * 1024),
 }
 
 # (name, C, O, H, K, stride, pad) at N=128
