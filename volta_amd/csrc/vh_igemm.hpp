@@ -167,7 +167,9 @@ struct Loader {
         g.fS.divmod(rs, kh, kw);
         int t = s0 - (int)kh, u = s1 - (int)kw;
         if (t >= 0 && u >= 0) {
-          int p = t / g.sh, q = u / g.sw;
+          // stride 1 (every stride phase is): no division
+          const bool unit = g.sh == 1 && g.sw == 1;
+          int p = unit ? t : t / g.sh, q = unit ? u : u / g.sw;
           if (p * g.sh == t && q * g.sw == u && p < g.P && q < g.Q) {
             const S* src = base + s2 + (int)o0 * PQ + p * g.Q + q;
 #pragma unroll
@@ -184,7 +186,8 @@ struct Loader {
             g.fS.divmod(rs, kh, kw);
             int t = s0 - (int)kh, u = s1 - (int)kw;
             if (t >= 0 && u >= 0) {
-              int p = t / g.sh, q = u / g.sw;
+              const bool unit = g.sh == 1 && g.sw == 1;
+              int p = unit ? t : t / g.sh, q = unit ? u : u / g.sw;
               if (p * g.sh == t && q * g.sw == u && p < g.P && q < g.Q)
                 out[j] = base[s2 + (int)o * PQ + p * g.Q + q];
             }

@@ -142,7 +142,60 @@ __global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restri
   reduce_splits_block(part, splits, n, [&](long i, float s) { out[i] = Elem<T>::from_f32(s); });
 }
 
-// ============================================================== pad / im2col / col2im
+// Weight gradient of the Direct algorithm with all R x S taps per block: block
+// (o*C + c, slice) walks its slice of output positions once (32-bit index
+// math), reads dY once per position and the R x S x values around it, and
+// keeps one accumulator per tap; partials [slice][o][c][r][s].
+template <typename T, int R, int S>
+__global__ __launch_bounds__(256) void direct_wgrad_taps_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                                const typename Elem<T>::storage* __restrict__ x,
+                                                                float* __restrict__ part, ConvGeom g, int slice) {
+  const int oc = blockIdx.x;
+  const int c = oc % g.C, o = oc / g.C;
+  const int npos = g.N * g.P * g.Q;
+  const int b = blockIdx.y * slice, e = min(npos, b + slice);
+  float acc[R * S];
+#pragma unroll
+  for (int t = 0; t < R * S; ++t) acc[t] = 0.f;
+  for (int i = b + threadIdx.x; i < e; i += 256) {
+    uint32_t n, pq, p, q;
+    g.fPQ.divmod((uint32_t)i, n, pq);
+    g.fQ.divmod(pq, p, q);
+    const float gv = Elem<T>::to_f32(dy[(((long)n * g.O + o) * g.P + p) * g.Q + q]);
+    const long xb = ((long)n * g.C + c) * g.H * g.W;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int h = (int)p * g.sh + r - g.ph;
+      if (h < 0 || h >= g.H) continue;
+#pragma unroll
+      for (int s2 = 0; s2 < S; ++s2) {
+        const int w = (int)q * g.sw + s2 - g.pw;
+        if (w >= 0 && w < g.W) acc[r * S + s2] += Elem<T>::to_f32(x[xb + (long)h * g.W + w]) * gv;
+      }
+    }
+  }
+  __shared__ float red[4][R * S];
+#pragma unroll
+  for (int t = 0; t < R * S; ++t) {
+    const float v = wave_sum(acc[t]);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][t] = v;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < R * S; t += 256)
+    part[((long)blockIdx.y * gridDim.x + oc) * (R * S) + t] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+}
+
+static bool direct_wgrad_taps_ok(const ConvGeom& g) {
+  const bool shape = (g.R == 3 && g.S == 3) || (g.R == 5 && g.S == 5) || (g.R == 1 && g.S == 1);
+  return shape && (long)g.N * g.P * g.Q < (1L << 31) && (long)g.O * g.C <= 65535 * 64;
+}
+
+static int direct_wgrad_taps_slices(const ConvGeom& g) {
+  const long npos = (long)g.N * g.P * g.Q, oc = (long)g.O * g.C;
+  return (int)std::max<long>(1, std::min<long>({(1024 + oc - 1) / oc, (npos + 255) / 256, 1024}));
+}
+
+// ============================================================== pad / im2col / col2im// ============================================================== pad / im2col / col2im
 template <typename T>
 __global__ __launch_bounds__(256) void pad_kernel(const typename Elem<T>::storage* __restrict__ x,
                                                   typename Elem<T>::storage* __restrict__ xp, int BC, int H,
@@ -695,6 +748,12 @@ template <typename T>
 size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
   long npos = (long)g.N * g.P * g.Q;
   long nw = (long)g.O * g.C * g.R * g.S;
+  if (direct_wgrad_taps_ok(g)) {
+    const int sl = direct_wgrad_taps_slices(g);
+    *slice_len = (int)((npos + sl - 1) / sl);
+    *slices = (int)((npos + *slice_len - 1) / *slice_len);
+    return (size_t)(*slices) * nw * sizeof(float);
+  }
   int sl = (int)std::min<long>(std::max<long>(1, (2048 + nw - 1) / nw), std::max<long>(1, npos / 1024));
   sl = std::min(sl, 1024);
   int len = (int)((npos + sl - 1) / sl);
@@ -708,8 +767,18 @@ int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g,
                      int slice_len, hipStream_t st) {
   using S = typename Elem<T>::storage;
   long nw = (long)g.O * g.C * g.R * g.S;
-  dim3 grid((unsigned)nw, (unsigned)slices);
-  direct_wgrad_kernel<T><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+  if (direct_wgrad_taps_ok(g)) {
+    dim3 grid((unsigned)(g.O * g.C), (unsigned)slices);
+    if (g.R == 3)
+      direct_wgrad_taps_kernel<T, 3, 3><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+    else if (g.R == 5)
+      direct_wgrad_taps_kernel<T, 5, 5><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+    else
+      direct_wgrad_taps_kernel<T, 1, 1><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+  } else {
+    dim3 grid((unsigned)nw, (unsigned)slices);
+    direct_wgrad_kernel<T><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+  }
   VH_LAUNCH_CHECK();
   sum_partials_kernel<T><<<reduce_splits_grid(nw), 256, 0, st>>>(ws, slices, nw, (S*)dw);
   VH_LAUNCH_CHECK();
