@@ -1,5 +1,6 @@
 // vh_gemm.hip -- instantiations and host dispatch of the MFMA implicit GEMM.
 #include <algorithm>
+#include <type_traits>
 
 #include "vh_kernels.hpp"
 
@@ -28,16 +29,18 @@ struct Tile {
   int bm, bn;
 };
 
-Tile pick_tile(int M, int N) {
+Tile pick_tile(int M, int N, int dtype = VH_F32) {
   Tile t{128, 128};
   if (M <= 64) t.bm = 64;
+  // f32 (16x16 MFMA tiles) also has 32-row tiles: a 32-channel output would
+  // leave half of a 64-row tile empty
+  if (M <= 32 && dtype == VH_F32) t.bm = 32;
   if (N <= 64) t.bn = 64;
   return t;
 }
 
-template <typename T, int AK, int BKIND, int OUT, int BM, int BN>
+template <typename T, int AK, int BKIND, int OUT, int BM, int BN, int BK = bk_for<T>()>
 int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
-  constexpr int BK = bk_for<T>();
   IgemmArgs a = p.args;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   dim3 grid((unsigned)tiles, 1, (unsigned)p.splits);
@@ -64,7 +67,12 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
 
 template <typename T, int AK, int BKIND, int OUT>
 int launch_kinds(IgemmPlan& p, float* ws, hipStream_t st) {
-  Tile t = pick_tile(p.args.M, p.args.N);
+  Tile t = pick_tile(p.args.M, p.args.N, std::is_same<T, float>::value ? VH_F32 : VH_BF16);
+  if constexpr (std::is_same<T, float>::value) {
+    // 32-row tiles take 32-deep K steps so that all 256 threads have a load unit
+    if (t.bm == 32 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 32, 128, 32>(p, ws, st);
+    if (t.bm == 32) return launch_tile<T, AK, BKIND, OUT, 32, 64, 32>(p, ws, st);
+  }
   if (t.bm == 128 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 128, 128>(p, ws, st);
   if (t.bm == 64 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 64, 128>(p, ws, st);
   if (t.bm == 128 && t.bn == 64) return launch_tile<T, AK, BKIND, OUT, 128, 64>(p, ws, st);
@@ -93,7 +101,7 @@ int launch_typed(IgemmPlan& p, float* ws, hipStream_t st) {
 }  // namespace
 
 int pick_splits(int M, int N, int K, int dtype) {
-  Tile t = pick_tile(M, N);
+  Tile t = pick_tile(M, N, dtype);
   const int bk = dtype == VH_BF16 ? 32 : 16;
   long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   // Split K only when the tile grid leaves most of the 256 CUs idle and K is
