@@ -36,6 +36,9 @@ Tile pick_tile(int M, int N, int dtype = VH_F32) {
   // leave half of a 64-row tile empty
   if (M <= 32 && dtype == VH_F32) t.bm = 32;
   if (N <= 64) t.bn = 64;
+  // f32 blocks are latency-bound with one block per CU: narrower tiles when the
+  // wide ones would not give every CU two blocks
+  if (dtype == VH_F32 && t.bn == 128 && (long)((M + t.bm - 1) / t.bm) * ((N + 127) / 128) < 512) t.bn = 64;
   return t;
 }
 
