@@ -82,6 +82,8 @@ def parse():
     ap.add_argument("--configs", action="store_true",
                     help="instead of the headline line, time a fwd+bwd step of every BASELINE config "
                          "(one JSON line each)")
+    ap.add_argument("--config-only", default=None,
+                    help="with --configs: only the config whose name starts with this (e.g. 'configs[4]')")
     ap.add_argument("--profile-op", default=None,
                     help="run only this pass (e.g. '3x3 256->256 @14 wgrad') --steps times, then a "
                          "256 MiB device copy, for rocprofv3 counter runs; prints nothing else")
@@ -215,7 +217,7 @@ def profile_op(torch, layers, name, reps):
     torch.cuda.synchronize()
 
 
-def config_steps(torch, vnn, dev, steps, warmup):
+def config_steps(torch, vnn, dev, steps, warmup, only=None):
     """Fwd+bwd step of each BASELINE config (synthetic inputs of the config's
     shapes, the library's MI355X algorithm choice), one JSON line per config.
     configs[0] and configs[4] run their whole graphs: convolutions with ReLU
@@ -301,6 +303,9 @@ def config_steps(torch, vnn, dev, steps, warmup):
                                               (32, 27, 3, 1, 1)], tail=(ps, (16, 3, 768, 768)))]),
     }
     for name, (dt, layers) in cfgs.items():
+        if only and not name.startswith(only):
+            continue
+
         def step(layers=layers):
             for run, _ in layers:
                 run()
@@ -309,7 +314,9 @@ def config_steps(torch, vnn, dev, steps, warmup):
         tf = fl / (ms * 1e-3) / 1e12
         print(json.dumps({"config": name, "dtype": dt, "ms_per_step": round(ms, 4), "gflop_per_step": round(fl / 1e9, 3),
                           "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_TFLOPS[dt], 2)}), flush=True)
-    print(json.dumps({"config": "configs[1] Linear / square products", **gemm_secondary(torch, vnn, dev)}), flush=True)
+    if not only or "configs[1]".startswith(only):
+        print(json.dumps({"config": "configs[1] Linear / square products", **gemm_secondary(torch, vnn, dev)}),
+              flush=True)
 
 
 def gemm_secondary(torch, vnn, dev, reps=5):
@@ -436,7 +443,7 @@ def main():
         profile_op(torch, layers, args.profile_op, args.steps)
         return
     if args.configs:
-        config_steps(torch, vnn, dev, args.steps, args.warmup)
+        config_steps(torch, vnn, dev, args.steps, args.warmup, args.config_only)
         return
 
     # headline: the training step (forward, then dX and dW in reverse layer

@@ -397,6 +397,23 @@ def test_sum_loss_known_answers():
     assert ops.gpu_sum_reduce(torch.empty(0, device=DEV)) == 0.0
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("off", [1, 3, 8])
+def test_sum_and_seed_on_offset_views(off, dt):
+    # slices that start off a 16-byte boundary take the element-wise path
+    n = 4099
+    g = rng(off)
+    x, xt = prep(g.standard_normal(n + off), dt)
+    got = ops.gpu_sum_reduce(xt[off:])
+    exact = float(np.sum(x[off:].astype(np.float64)))
+    assert abs(got - exact) <= 1e-6 * float(np.abs(x[off:]).sum()), (got, exact)
+    buf = torch.zeros(n + off + 5, dtype=DTYPES[dt], device=DEV)
+    view = buf[off:off + n]
+    ops._call("vh_sum_backward", ops.dtype_code(view), 0.5, ops.ptr(view), n, ops.stream_ptr(view.device))
+    got = host(buf)
+    assert np.all(got[:off] == 0) and np.all(got[off:off + n] == 0.5) and np.all(got[off + n:] == 0)
+
+
 # ------------------------------------------------------------------ fused conv -> ReLU
 RELU_CASES = [
     # (B, C, O, H, W, K, S, P)

@@ -623,13 +623,31 @@ __global__ __launch_bounds__(256) void relu_kernel(const typename Elem<T>::stora
 
 // Sum of n elements: block b adds the contiguous slice b (lanes stride the
 // slice, then a fixed butterfly and wave order) into part[b]; a second pass
-// adds the partials in index order.  The order depends only on n.
+// adds the partials in index order.  When x is 16-byte aligned the slices
+// start on 16-byte boundaries and lanes read whole 16-byte chunks.  The
+// order depends only on n and that alignment.
 template <typename T>
 __global__ __launch_bounds__(256) void sum_slices_kernel(const typename Elem<T>::storage* __restrict__ x, long n,
-                                                         long per, float* __restrict__ part) {
+                                                         long per, float* __restrict__ part, int vec) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
   const long b = (long)blockIdx.x * per, e = min(n, b + per);
   float s = 0.f;
-  for (long i = b + threadIdx.x; i < e; i += 256) s += Elem<T>::to_f32(x[i]);
+  long i0 = b;
+  if (vec) {  // per is a multiple of VE and x is 16-byte aligned: whole 16-byte chunks first
+    const long nv = (e - b) / VE;
+    const uint4* xv = reinterpret_cast<const uint4*>(x + b);
+    for (long k = threadIdx.x; k < nv; k += 256) {
+      S v[VE];
+      *reinterpret_cast<uint4*>(v) = xv[k];
+      float t = 0.f;
+#pragma unroll
+      for (int j = 0; j < VE; ++j) t += Elem<T>::to_f32(v[j]);
+      s += t;
+    }
+    i0 = b + nv * VE;
+  }
+  for (long i = i0 + threadIdx.x; i < e; i += 256) s += Elem<T>::to_f32(x[i]);
   s = wave_sum(s);
   __shared__ float red[4];
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
@@ -720,9 +738,21 @@ __global__ __launch_bounds__(256) void optimizer_step_kernel(float* __restrict__
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void fill_kernel(typename Elem<T>::storage* __restrict__ y, long n, float v) {
-  const typename Elem<T>::storage e = Elem<T>::from_f32(v);
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) y[i] = e;
+__global__ __launch_bounds__(256) void fill_kernel(typename Elem<T>::storage* __restrict__ y, long n, float v,
+                                                   int vec) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  const S e = Elem<T>::from_f32(v);
+  const long nv = vec ? n / VE : 0;
+  if (nv) {
+    S chunk[VE];
+#pragma unroll
+    for (int j = 0; j < VE; ++j) chunk[j] = e;
+    const uint4 c = *reinterpret_cast<const uint4*>(chunk);
+    for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < nv; i += (long)gridDim.x * 256)
+      reinterpret_cast<uint4*>(y)[i] = c;
+  }
+  for (long i = nv * VE + (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) y[i] = e;
 }
 
 // ============================================================== typed launchers
@@ -968,10 +998,14 @@ template <typename T>
 int run_sum(const void* x, long n, float* out, float* ws, hipStream_t st) {
   using S = typename Elem<T>::storage;
   const int nb = (int)std::max<long>(1, std::min<long>(1024, (n + 4095) / 4096));
-  const long per = (n + nb - 1) / nb;
-  sum_slices_kernel<T><<<nb, 256, 0, st>>>((const S*)x, n, per, ws);
+  constexpr long VE = 16 / sizeof(S);
+  const bool vec = ((uintptr_t)x & 15) == 0;
+  long per = std::max<long>(1, (n + nb - 1) / nb);
+  if (vec) per = (per + VE - 1) / VE * VE;  // slices start on 16-byte boundaries
+  const int nb2 = (int)((n + per - 1) / per);
+  sum_slices_kernel<T><<<std::max(nb2, 1), 256, 0, st>>>((const S*)x, n, per, ws, vec ? 1 : 0);
   VH_LAUNCH_CHECK();
-  sum_partials_scalar_kernel<<<1, 256, 0, st>>>(ws, nb, out);
+  sum_partials_scalar_kernel<<<1, 256, 0, st>>>(ws, std::max(nb2, 1), out);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -980,7 +1014,8 @@ template <typename T>
 int run_fill(void* y, long n, float v, hipStream_t st) {
   using S = typename Elem<T>::storage;
   if (n <= 0) return VH_OK;
-  fill_kernel<T><<<grid_for(n), 256, 0, st>>>((S*)y, n, v);
+  const bool vec = ((uintptr_t)y & 15) == 0;
+  fill_kernel<T><<<grid_for(vec ? n / (long)(16 / sizeof(S)) + 1 : n), 256, 0, st>>>((S*)y, n, v, vec ? 1 : 0);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
