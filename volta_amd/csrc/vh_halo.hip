@@ -60,6 +60,8 @@ struct HaloArgs {
   int act;               // epilogue: 0 none, 1 ReLU, 2 zero where mask <= 0 (mask laid out like y)
   const uint16_t* mask;
   int stages;            // LDS stages (1 when there is a single channel group)
+  int vec_epi;           // 1: whole rows, P*Q % 8 == 0 and 16-byte aligned y / mask:
+                         // the epilogue transposes through LDS and stores 8 positions per lane
   FastDiv fPQ, fQ;              // P*TW, TW
   FastDiv fW2, fRowsMax, fHp;   // item decomposition (Wp/2, rows_max, Hp)
   FastDiv fStrips;              // nstrips
@@ -350,12 +352,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
 #undef WSM
 #undef XSM
+  const int PQ = a.P * a.Q;
+  if (a.vec_epi) {
+    // Vector epilogue.  Each wave writes its 64 o x 64 position tile, bias added
+    // and rounded once to bf16 (ReLU applied in fp32 first), into its own LDS
+    // region [o][position] (pitch 72 elements: the two half-waves, 4 rows
+    // apart, fall on disjoint banks), then stores runs of 8 consecutive
+    // positions (16 bytes) per lane.  P*Q % 8 == 0, so a run never crosses an
+    // image and its address is 16-byte aligned.
+    constexpr int EP = 72;
+    __syncthreads();  // every wave has finished reading the last stage
+    uint16_t* eb = reinterpret_cast<uint16_t*>(lds) + wave * (64 * EP);
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int row = i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        const int o = o0 + wm + row;
+        const float bias = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float val = acc[i][j][v] + bias;
+          if (a.act == 1) val = fmaxf(val, 0.f);
+          eb[row * EP + j * 32 + (lane & 31)] = __builtin_bit_cast(uint16_t, (__bf16)val);
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int c = it * 64 + lane, row = c >> 3, k = c & 7;
+      const int o = o0 + wm + row;
+      const int m = m0 + wn + k * 8;
+      if (o < a.O && m < a.M) {
+        uint32_t n, pq;
+        a.fPQ.divmod((uint32_t)m, n, pq);
+        const long off = ((long)n * a.O + o) * PQ + pq;
+        uint4 val = *reinterpret_cast<const uint4*>(eb + row * EP + k * 8);
+        if (a.act == 2) {
+          // zero where the layer's forward output (the mask) is not positive
+          const uint4 mk = *reinterpret_cast<const uint4*>(a.mask + off);
+          uint32_t* vv = reinterpret_cast<uint32_t*>(&val);
+          const uint32_t* mm = reinterpret_cast<const uint32_t*>(&mk);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = bf16_to_f32((uint16_t)(mm[d] & 0xffffu)) > 0.f ? 0x0000ffffu : 0u;
+            const uint32_t hi = bf16_to_f32((uint16_t)(mm[d] >> 16)) > 0.f ? 0xffff0000u : 0u;
+            vv[d] &= lo | hi;
+          }
+        }
+        *reinterpret_cast<uint4*>(a.y + off) = val;
+      }
+    }
+    return;
+  }
   // epilogue: rows = o (acc_row), cols = positions (lane & 31); fp32 bias add,
   // one rounding to bf16, NCHW store (lanes walk consecutive q).  Buffer stores:
   // the per-lane offset is the position (plus 4 rows for the upper half-wave),
   // the output-channel row is a scalar offset; positions past the end carry an
   // out-of-range offset and their stores are dropped.
-  const int PQ = a.P * a.Q;
   const int PQ2 = PQ * 2;
   const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.y, (short)0, a.y_bytes, 0x00020000);
   int yoff[FN];
@@ -552,7 +607,6 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   }
   if (!have) return VH_ERR_UNSUPPORTED;
   const int WM = best.WM, rows_max = best.rows_max;
-  const size_t lds = best.lds;
   a.TW = best.TW;
   a.nstrips = (Q + a.TW - 1) / a.TW;
   a.Wp = best.Wp;
@@ -568,6 +622,11 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.fW2 = FastDiv((uint32_t)a.npairs);
   a.rows_max = rows_max;
   a.fRowsMax = FastDiv((uint32_t)rows_max);
+  // vector epilogue: whole rows, runs of 8 positions inside one image, aligned
+  // output (and mask); its LDS (4 waves x 64 x 72 bf16) reuses the stages
+  a.vec_epi = (whole && (P * Q) % 8 == 0 && ((uintptr_t)y & 15) == 0 && (act != 2 || ((uintptr_t)mask & 15) == 0))
+                  ? 1 : 0;
+  const size_t lds = a.vec_epi ? std::max<size_t>(best.lds, 4 * 64 * 72 * 2) : best.lds;
   VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
