@@ -252,6 +252,8 @@ HALO_CASES = [
     (1, 20, 30, 6, 166, 3, 1, 0),    # wide rows, no padding, 2-element chunks
     (2, 27, 32, 16, 16, 3, 1, 1),    # C not a multiple of 16: partial last channel group (forward)
     (2, 32, 27, 12, 12, 3, 1, 1),    # O = 27: partial channel group in the input gradient
+    (84, 17, 20, 56, 56, 3, 1, 1),   # >= 1024 blocks, two channel groups: one LDS stage, 3 blocks per CU
+    (4, 18, 17, 256, 256, 3, 1, 1),  # the same over column strips (no vector epilogue)
     (2, 3, 64, 20, 24, 5, 1, 2),     # 3 input channels, 5x5: one partial group, one LDS stage
     (1, 5, 20, 8, 10, 3, 1, 1),      # C = 5 forward; input gradient over 20 = 16 + 4 channels
 ]

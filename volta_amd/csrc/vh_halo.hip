@@ -88,8 +88,12 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-template <int R, int S, int WM, int XI>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv_halo_bf16_kernel(HaloArgs a) {
+// WPE = waves per SIMD the kernel is compiled for.  WPE 2: two LDS stages and
+// (for narrow tiles) two register sets, two blocks per CU.  WPE 3: one LDS
+// stage and one register set (at most 168 VGPRs), three blocks per CU -- more
+// waves to hide the load and LDS latency, for grids of many blocks.
+template <int R, int S, int WM, int XI, int WPE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   extern __shared__ __attribute__((aligned(16))) u32x4 lds[];
@@ -208,7 +212,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // are issued while group kt is multiplied and group kt+1 is written to LDS,
   // so every load has two compute phases to arrive; wide tiles (more than 4 x or 5 weight load
   // items per thread) keep one set to stay within two waves' registers.
-  constexpr int DEPTH = (Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
+  constexpr int DEPTH = (WPE == 2 && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
   u32x4 wreg[DEPTH][Cfg::WITER];
   uint32_t xreg[DEPTH][Cfg::XITER][8];
   auto gload = [&](auto SET, int c0) {
@@ -334,6 +338,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         sstore(I0{}, 0);
         __syncthreads();
         compute(0);
+      }
+    }
+  } else if (WPE == 3) {
+    // one LDS stage: the next group's loads are in flight during the compute;
+    // a barrier before its store (every wave done reading) and one after it
+    gload(I0{}, 0);
+    sstore(I0{}, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 < nk) gload(I0{}, (kt + 1) * 16);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 1 < nk) {
+        __syncthreads();
+        sstore(I0{}, 0);
+        __syncthreads();
       }
     }
   } else {
@@ -492,10 +513,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // ---------------------------------------------------------------- host side
 namespace {
 
-template <int R, int S, int WM, int XI>
+template <int R, int S, int WM, int XI, int WPE = 2>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
-  auto kern = conv_halo_bf16_kernel<R, S, WM, XI>;
+  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE>;
   static bool attr_set = false;
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -510,14 +531,22 @@ int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   return VH_OK;
 }
 
+int halo_xi(const HaloArgs& a) { return (2 * a.rows_max * a.npairs + 255) / 256; }
+
 template <int R, int S, int WM>
 int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
-  const int items = 2 * a.rows_max * a.npairs;
-  const int xi = (items + 255) / 256;
+  const int xi = halo_xi(a);
   if (xi <= 2) return launch_halo<R, S, WM, 2>(a, lds_bytes, st);
   if (xi <= 4) return launch_halo<R, S, WM, 4>(a, lds_bytes, st);
   if (xi <= 6) return launch_halo<R, S, WM, 6>(a, lds_bytes, st);
   return launch_halo<R, S, WM, 8>(a, lds_bytes, st);
+}
+
+// three blocks per CU: the 3x3 load widths that fit 168 VGPRs without spills
+int pick_xi_wpe3(const HaloArgs& a, int WM, size_t lds_bytes, hipStream_t st) {
+  const int xi = halo_xi(a);
+  if (WM == 2) return launch_halo<3, 3, 2, 2, 3>(a, lds_bytes, st);
+  return xi <= 2 ? launch_halo<3, 3, 1, 2, 3>(a, lds_bytes, st) : launch_halo<3, 3, 1, 4, 3>(a, lds_bytes, st);
 }
 
 }  // namespace
@@ -626,8 +655,15 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // output (and mask); its LDS (4 waves x 64 x 72 bf16) reuses the stages
   a.vec_epi = (whole && (P * Q) % 8 == 0 && ((uintptr_t)y & 15) == 0 && (act != 2 || ((uintptr_t)mask & 15) == 0))
                   ? 1 : 0;
-  const size_t lds = a.vec_epi ? std::max<size_t>(best.lds, 4 * 64 * 72 * 2) : best.lds;
+  // Three blocks per CU with one LDS stage pays off for grids of many blocks
+  // with several channel groups (one group is single-stage already).
+  const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
+  const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= 1024 && halo_xi(a) <= (WM == 1 ? 4 : 2);
+  if (wpe3) a.stages = 1;
+  const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
+  const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
   VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
+  if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
     return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \
