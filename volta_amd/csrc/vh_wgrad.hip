@@ -20,8 +20,10 @@
 // in two LDS buffers (loads for step k+1 are in flight while step k runs).
 // Each wave accumulates a 32(o) x 32(c) x 9-tap tile in AGPRs.  Split-K: the
 // grid's z dimension walks disjoint ranges of K steps; partial sums go to an
-// fp32 workspace [split][tap][O][C] and a second kernel adds them in a fixed
-// order and writes dW (OIHW).  The optional bias gradient (sum of dY over
+// fp32 workspace in the accumulators' own layout
+//   [split][tile][wave][tap][row group j][lane][4]   (element v = 4j + k of lane)
+// written as one 16-byte store per lane and (tap, j), and a second kernel adds
+// them in a fixed order and writes dW (OIHW).  The optional bias gradient (sum of dY over
 // positions) is accumulated by the c-tile-0 blocks from the same LDS copy of dY.
 #include <algorithm>
 #include <type_traits>
@@ -61,7 +63,7 @@ struct WgradArgs {
   int cpr_dy, cpr_x;   // chunks of V elements per dY row / per x row
   int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < RL
   int xadv, xcadv;     // the same for x rows (columns < XL)
-  int dy_bytes, x_bytes, part_bytes;  // buffer ranges (< 2^31)
+  int dy_bytes, x_bytes;  // buffer ranges (< 2^31)
   int tiles_o, tiles_c, splits;       // grid = tiles_o * tiles_c * splits blocks
 };
 
@@ -448,24 +450,21 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
 #undef DYS
 #undef XS
 
-  // partial tile store: part[split][tap][o][c], lanes walk c.  Per-lane offset:
-  // column c and the half-wave's 4-row shift; scalar offset: (split, tap, row).
+  // partial tile store in the accumulator layout (rows past O / columns past C
+  // included: the reduction skips them): lane l's elements 4j .. 4j+3 of tap t
+  // form one 16-byte unit; the 64 lanes of one (tap, j) write 1 KB contiguously.
   {
-    const __amdgpu_buffer_rsrc_t pr =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.part, (short)0, a.part_bytes, 0x00020000);
-    const int c = c0 + wc + rl;
-    const int ohalf = (lane >> 5) * 4;
-    const int voff = c < a.C ? (ohalf * a.C + c) * 4 : (int)0x80000000u;
+    float* pb = a.part + ((((long)split * a.tiles_o * a.tiles_c + tile) * 4 + wave) * RS) * 1024 + lane * 4;
 #pragma unroll
     for (int t = 0; t < RS; ++t)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int orow = o0 + wo + (v >> 2) * 8 + (v & 3);
-        if (orow + ohalf < a.O) {
-          const float val = acc[t][v];  // (a bit_cast of the vector element itself reads element 0)
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), pr, voff,
-                                                (((split * RS + t) * a.O) + orow) * a.C * 4, 0);
-        }
+      for (int j = 0; j < 4; ++j) {
+        float4 u;
+        u.x = acc[t][4 * j];
+        u.y = acc[t][4 * j + 1];
+        u.z = acc[t][4 * j + 2];
+        u.w = acc[t][4 * j + 3];
+        *reinterpret_cast<float4*>(pb + (t * 4 + j) * 256) = u;
       }
   }
   if (do_bias) {
@@ -492,6 +491,34 @@ __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __r
       const int o = (int)(t % O);
       const int tap = (int)(t / O);
       dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
+    }, (int)blockIdx.x, nbw);
+  } else {
+    reduce_splits_block(bpart, splits, (long)O, [&](long i, float s) { db[i] = f32_to_bf16(s); },
+                        (int)blockIdx.x - nbw, (int)gridDim.x - nbw);
+  }
+}
+
+// The same for partials in the row kernel's accumulator layout (see the top of
+// this file): element i of a split is ((((tile * 4 + wave) * RS + tap) * 4 + j)
+// * 64 + lane) * 4 + k, i.e. dW[o][c][tap] with
+//   o = o-tile * 64 + (wave / 2) * 32 + 8 j + 4 (lane / 32) + k,
+//   c = c-tile * 64 + (wave % 2) * 32 + lane % 32   (tile = c-tile * tiles_o + o-tile).
+__global__ __launch_bounds__(256) void wgrad_reduce_frag_bf16_kernel(const float* __restrict__ part, int splits,
+                                                                     int RS, int tiles_o, int O, int C,
+                                                                     uint16_t* __restrict__ dw,
+                                                                     const float* __restrict__ bpart,
+                                                                     uint16_t* __restrict__ db, int nbw, long total) {
+  if ((int)blockIdx.x < nbw) {
+    reduce_splits_block(part, splits, total, [&](long i, float s) {
+      const int k = (int)(i & 3), lane = (int)((i >> 2) & 63), j = (int)((i >> 8) & 3);
+      const long rest = i >> 10;
+      const int tap = (int)(rest % RS);
+      const long tw = rest / RS;
+      const int wave = (int)(tw & 3);
+      const long tile = tw >> 2;
+      const int o = (int)(tile % tiles_o) * 64 + (wave >> 1) * 32 + 8 * j + 4 * (lane >> 5) + k;
+      const int c = (int)(tile / tiles_o) * 64 + (wave & 1) * 32 + (lane & 31);
+      if (o < O && c < C) dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
     }, (int)blockIdx.x, nbw);
   } else {
     reduce_splits_block(bpart, splits, (long)O, [&](long i, float s) { db[i] = f32_to_bf16(s); },
@@ -817,6 +844,11 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
   return VH_ERR_UNSUPPORTED;
 }
 
+// partials of the row kernel: [split][tile][4 waves][tap][1024]
+size_t frag_part_bytes(const WgradPlan& pl, int RS) {
+  return (size_t)pl.splits * pl.tiles_o * pl.tiles_c * 4 * RS * 1024 * sizeof(float);
+}
+
 template <int PW>
 int launch_pw(const WgradPlan& pl, hipStream_t st) {
   return pl.a.V == 8 ? launch_v<PW, 8>(pl, st) : pl.a.V == 4 ? launch_v<PW, 4>(pl, st) : launch_v<PW, 2>(pl, st);
@@ -834,7 +866,7 @@ size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, in
   }
   WgradPlan pl;
   if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return 0;
-  size_t b = (size_t)pl.splits * R * S * O * C * sizeof(float);
+  size_t b = frag_part_bytes(pl, R * S);
   if (bias) b += (size_t)pl.splits * O * sizeof(float) + 256;
   return b;
 }
@@ -864,23 +896,21 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return VH_ERR_UNSUPPORTED;
   {
     const long dyb = (long)N * O * pl.a.P * pl.a.Q * 2, xb = (long)N * C * H * W * 2;
-    const long pb = (long)pl.splits * R * S * O * C * 4;
-    if (dyb >= (1L << 31) - 16 || xb >= (1L << 31) - 16 || pb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
+    if (dyb >= (1L << 31) - 16 || xb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
     pl.a.dy_bytes = (int)dyb;
     pl.a.x_bytes = (int)xb;
-    pl.a.part_bytes = (int)pb;
   }
   pl.a.dy = (const uint16_t*)dy;
   pl.a.x = (const uint16_t*)x;
   pl.a.part = ws;
-  const size_t pbytes = (size_t)pl.splits * R * S * O * C * sizeof(float);
+  const size_t pbytes = frag_part_bytes(pl, R * S);
   pl.a.dbias_part = db ? (float*)((char*)ws + ((pbytes + 255) & ~size_t(255))) : nullptr;
   int rc = pl.a.pw == 0 ? launch_pw<0>(pl, st) : pl.a.pw == 1 ? launch_pw<1>(pl, st) : launch_pw<2>(pl, st);
   if (rc) return rc;
-  const long total = (long)R * S * O * C;
+  const long total = (long)(pbytes / sizeof(float) / pl.splits);
   const int nbw = reduce_splits_grid(total), nbb = db ? reduce_splits_grid(O) : 0;
-  wgrad_reduce_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, pl.splits, R * S, O, C, (uint16_t*)dw, pl.a.dbias_part,
-                                                      (uint16_t*)db, nbw);
+  wgrad_reduce_frag_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, pl.splits, R * S, pl.tiles_o, O, C, (uint16_t*)dw,
+                                                           pl.a.dbias_part, (uint16_t*)db, nbw, total);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
