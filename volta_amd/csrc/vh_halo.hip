@@ -88,15 +88,29 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// LDS units (16 bytes) per stage of the fused form: two stages of 38.9 KB, two
+// blocks per CU.
+constexpr int kFusedStageUnits = 2432;
+
 // WPE = waves per SIMD the kernel is compiled for.  WPE 2: two LDS stages and
 // (for narrow tiles) two register sets, two blocks per CU.  WPE 3: one LDS
 // stage and one register set (at most 168 VGPRs), three blocks per CU -- more
 // waves to hide the load and LDS latency, for grids of many blocks.
-template <int R, int S, int WM, int XI, int WPE>
+// FUSED (WPE 2, two register sets, C a multiple of 16, stages of at most
+// kFusedStageUnits): the two LDS stages are separate static arrays, so the
+// compiler can tell that the stores into one stage do not alias the fragment
+// reads of the other, and each channel group's global loads and the previous
+// group's LDS stores are interleaved with its MFMAs instead of running as
+// phases of their own.
+template <int R, int S, int WM, int XI, int WPE, bool FUSED = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
-  extern __shared__ __attribute__((aligned(16))) u32x4 lds[];
+  constexpr int SU = FUSED ? kFusedStageUnits : 1;
+  __shared__ __attribute__((aligned(16))) u32x4 lds0[SU];
+  __shared__ __attribute__((aligned(16))) u32x4 lds1[SU];
+  extern __shared__ __attribute__((aligned(16))) u32x4 lds_dyn[];
+  u32x4* const lds = FUSED ? lds0 : lds_dyn;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -114,9 +128,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   const int w_units = BM * Cfg::WPU;       // 16-byte units per weight stage
   const int stage = w_units + 2 * cells + 2;  // uint4 per stage; the last 2 units are a
                                               // sink for stores of unused load items
-  // stage st: weights at lds + st*stage, x halo right after them
-#define WSM(st) (lds + (st) * stage)
-#define XSM(st) (lds + (st) * stage + w_units)
+  // stage st: weights at the stage's start, x halo right after them
+#define WSM(st) (FUSED ? ((st) ? lds1 : lds0) : lds + (st) * stage)
+#define XSM(st) (WSM(st) + w_units)
 
   // first ext row this block needs: output row of its first position
   uint32_t n_a, pq_a, p_a, q_a;
@@ -138,7 +152,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     for (int i = tid; i < 2 * a.stages * a.rows_max; i += 256) {
       uint32_t sh, e;
       a.fRowsMax.divmod((uint32_t)i, sh, e);
-      u32x4* rowp = lds + (sh >> 1) * stage + w_units + (sh & 1) * cells + e * Wp;
+      u32x4* rowp = XSM(sh >> 1) + (sh & 1) * cells + e * Wp;
       for (int pc = 0; pc < padc; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
     }
   }
@@ -160,22 +174,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   const int HW = a.H * a.W;
 
   // x load items (fixed for the whole block; only the channel group moves):
-  // item -> (half, ext row e, column pair wi).  x_voff is the byte offset of the
-  // item's first element at channel 0 (+8 channels for the upper half), or an
-  // offset past the end of the buffer for rows outside the image.
+  // item -> (half, ext row e, column pair wi).  The first XITER/2 items of a
+  // thread are in the lower half-plane (channels 0-7 of the group), the others
+  // in the upper one, so a channel's validity is uniform per load.  x_voff is
+  // the byte offset of the item's first element at channel 0 (+8 channels for
+  // the upper half), or an offset past the end of the buffer for rows outside
+  // the image.
   const int HW2 = HW * 2;  // bytes per channel plane
   const __amdgpu_buffer_rsrc_t xrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  // zero-length buffer: every load through it returns 0 (masked channels and groups)
+  const __amdgpu_buffer_rsrc_t zrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, 0, 0x00020000);
+  constexpr int XH = Cfg::XITER / 2;  // items per thread per half-plane
   int x_voff[Cfg::XITER], x_loff[Cfg::XITER];
 #pragma unroll
   for (int it = 0; it < Cfg::XITER; ++it) {
-    // item -> (half, e, wi) over a rows_max-row grid; rows e >= rows are skipped
-    uint32_t i = (uint32_t)(tid + it * 256);
-    uint32_t wi, t, e, half;
-    a.fW2.divmod(i, t, wi);
-    a.fRowsMax.divmod(t, half, e);
+    const int half = it < XH ? 0 : 1;
+    const uint32_t i = (uint32_t)(tid + (it - half * XH) * 256);
+    uint32_t wi, e;
+    a.fW2.divmod(i, e, wi);
     int voff = (int)0x80000000u, loff = -1;
-    if (half < 2u && (int)e < rows) {
+    if ((int)e < rows) {
       uint32_t eg = (uint32_t)(e_start + (int)e), vimg, hr, n, strip;
       a.fHp.divmod(eg, vimg, hr);
       a.fStrips.divmod(vimg, n, strip);
@@ -184,7 +203,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
       const int col = (int)strip * a.TW + a.lcol0 + 2 * (int)wi;
       if (h >= 0 && h < a.H && col >= 0 && col < a.W)
         voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + col) * 2);
-      loff = (int)half * cells + (int)e * Wp + a.lcell0 + 2 * (int)wi;
+      loff = half * cells + (int)e * Wp + a.lcell0 + 2 * (int)wi;
     }
     x_voff[it] = voff;
     x_loff[it] = loff >= 0 ? loff : 2 * cells;  // unused items store to the sink
@@ -213,33 +232,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // so every load has two compute phases to arrive; wide tiles (more than 4 x or 5 weight load
   // items per thread) keep one set to stay within two waves' registers.
   constexpr int DEPTH = (WPE == 2 && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
+  static_assert(!FUSED || DEPTH == 2, "the fused form keeps two register sets");
   u32x4 wreg[DEPTH][Cfg::WITER];
   uint32_t xreg[DEPTH][Cfg::XITER][8];
+  // Loads of channel group c0 .. c0+15.  Every load is issued (no branches, so
+  // the compiler's wait counts stay exact across the pipeline): channels past C
+  // and groups past the last one read through the zero-length buffer.
   auto gload = [&](auto SET, int c0) {
     constexpr int sI = decltype(SET)::value;
+    const int crem = a.C - c0;  // channels left from c0 (<= 0 past the last group)
+    // the fused form loads only whole groups inside C (C % 16 == 0, c0 < C)
 #pragma unroll
     for (int it = 0; it < Cfg::WITER; ++it)
-      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_goff[it], c0 * OG2, 0));
-    if (c0 + 16 <= a.C) {
+      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   FUSED || crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
 #pragma unroll
-      for (int it = 0; it < Cfg::XITER; ++it) {
-        // invalid items carry an out-of-range offset: the buffer load returns 0
+    for (int it = 0; it < Cfg::XITER; ++it) {
+      const int half = it < XH ? 0 : 1;
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(xrsrc, x_voff[it], (c0 + j) * HW2, 0);
-      }
-    } else {
-      // last, partial channel group (C not a multiple of 16): channels past C
-      // load as zero (their padded weights are zero too); the upper half-plane
-      // items (LDS offset >= cells) hold channels c0 + 8 + j
-#pragma unroll
-      for (int it = 0; it < Cfg::XITER; ++it) {
-        const int lim = a.C - c0 - (x_loff[it] >= cells ? 8 : 0);
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          xreg[sI][it][j] =
-              __builtin_amdgcn_raw_buffer_load_b32(xrsrc, j < lim ? x_voff[it] : (int)0x80000000u, (c0 + j) * HW2, 0);
-      }
+      for (int j = 0; j < 8; ++j)
+        xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(FUSED || j + 8 * half < crem ? xrsrc : zrsrc,
+                                                               x_voff[it], (c0 + j) * HW2, 0);
     }
   };
   auto sstore = [&](auto SET, int st) {
@@ -305,14 +318,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   const int nk = (a.C + 15) / 16;
   if constexpr (DEPTH == 2) {
     gload(I0{}, 0);
-    if (nk > 1) gload(I1{}, 16);
+    gload(I1{}, FUSED && nk < 2 ? 0 : 16);  // all zeros when there is a single group
     __builtin_amdgcn_sched_barrier(0);
     sstore(I0{}, 0);
     __syncthreads();
     int kt = 0;
+    // Fused form: one channel group = the MFMAs of stage ST, with the loads of
+    // group +2 and the LDS stores of group +1 (into the other stage) placed
+    // between them: per tap, 4 MFMAs with 3 global loads, one LDS store and
+    // the fragment reads of the tap after next in the gaps.
+    auto fused = [&](auto ST, auto LSET, int lc0, auto SSET) {
+      constexpr int st = decltype(ST)::value;
+      gload(LSET, lc0);
+      sstore(SSET, 1 - st);
+      compute(st);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (FM + FN), 0);  // fragment reads of taps 0, 1
+#pragma unroll
+      for (int t = 0; t < RS; ++t) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global loads
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (t + 2 < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);  // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        if (t + 2 < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    };
+    if constexpr (FUSED) {
+      for (; kt + 3 < nk; kt += 2) {
+        fused(I0{}, I0{}, (kt + 2) * 16, I1{});
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        fused(I1{}, I1{}, (kt + 3) * 16, I0{});
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+      }
+    }
     // sched_barrier(0) keeps the compiler from sinking the loads to their
     // use (which would leave them no time to arrive)
-    for (; kt + 3 < nk; kt += 2) {
+    for (; !FUSED && kt + 3 < nk; kt += 2) {
       gload(I0{}, (kt + 2) * 16);
       __builtin_amdgcn_sched_barrier(0);
       compute(0);
@@ -327,7 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
       __syncthreads();
     }
     const int rem = nk - kt;  // 1, 2 or 3 groups left
-    if (rem == 3) gload(I0{}, (kt + 2) * 16);
+    if (!FUSED || rem == 3) gload(I0{}, (kt + 2) * 16);  // zeros unless rem == 3
     __builtin_amdgcn_sched_barrier(0);
     compute(0);
     if (rem >= 2) {
@@ -513,25 +559,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 // ---------------------------------------------------------------- host side
 namespace {
 
-template <int R, int S, int WM, int XI, int WPE = 2>
+template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
-  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE>;
+  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED>;
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
+    // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
+    if (!FUSED)
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                160 * 1024);
     attr_set = true;
   }
   HaloArgs g = a;
   g.tiles_m = (a.M + Cfg::BN - 1) / Cfg::BN;
   g.tiles_o = (a.O + Cfg::BM - 1) / Cfg::BM;
-  kern<<<dim3((unsigned)(g.tiles_m * g.tiles_o)), 256, lds_bytes, st>>>(g);
+  kern<<<dim3((unsigned)(g.tiles_m * g.tiles_o)), 256, FUSED ? 0 : lds_bytes, st>>>(g);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
 
-int halo_xi(const HaloArgs& a) { return (2 * a.rows_max * a.npairs + 255) / 256; }
+// x load items per thread: an even count, half of them per half-plane
+int halo_xi(const HaloArgs& a) { return 2 * ((a.rows_max * a.npairs + 255) / 256); }
 
 template <int R, int S, int WM>
 int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
@@ -612,7 +661,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     }
     const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * Wp + 2) * 16;
     const size_t lds = a.stages * stage;
-    if (lds > 160 * 1024 || (2 * rows_max * npairs + 255) / 256 > 8) return false;
+    if (lds > 160 * 1024 || 2 * ((rows_max * npairs + 255) / 256) > 8) return false;
     c = Cand{TW, WM, rows_max, Wp, lds, (long)nstrips * TW};
     return true;
   };
@@ -664,6 +713,14 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
   VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
   if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
+  // Fused form (two register sets, whole channel groups, stages and the
+  // vector epilogue within the static stage size): 3x3, 64 x 256 tiles with
+  // at most 4 x items per thread.
+  const int stage_units = WM * 64 * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
+  if (R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
+      stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16)) {
+    return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, 2, true>(a, lds, st) : launch_halo<3, 3, 1, 4, 2, true>(a, lds, st);
+  }
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
     return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \
