@@ -122,14 +122,20 @@ __device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, co
 // Load items: thread t serves row owner t/4 (an o of the dY tile, a c of the x
 // tile) and takes that owner's chunks t%4, t%4 + 4, ...; chunk k of a dY owner
 // is row k / cpr, column (k % cpr) * V.  Offsets advance incrementally.
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH>
-__global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
+// PC (whole rows): 512 threads, waves 0-3 multiply (consumers), waves 4-7 only
+// load and store into LDS (producers, threads 256-511 serving the item map of
+// threads 0-255).  Neither role holds the other's registers, so two waves fit
+// per SIMD and the loads run beside the MFMAs of the other role.
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH, bool PC = false>
+__global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   static_assert(R == 3 && S == 3, "3x3 windows");
   constexpr int RS = R * S;
   constexpr int TO = 64, TC = 64;  // block tile (o, c)
   using VT = typename VecT<V>::t;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63;
+  static_assert(!PC || !SEG, "producer / consumer split: whole rows only");
+  const bool producer = PC && threadIdx.x >= 256;
+  const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wo = (wave >> 1) * 32, wc = (wave & 1) * 32;
   // logical block -> (o tile, c tile, split): the tiles of one split (which
@@ -151,7 +157,8 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   const int nsteps = max(0, step_e - step_b);
 
   // zero both stages once: gaps and padding are never written by the loader
-  for (int i = tid; i < 2 * stage / 8; i += 256) reinterpret_cast<u32x4w*>(smem)[i] = u32x4w{0u, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < 2 * stage / 8; i += PC ? 512 : 256)
+    reinterpret_cast<u32x4w*>(smem)[i] = u32x4w{0u, 0u, 0u, 0u};
 
   const int PQ = a.P * a.Q, HW = a.H * a.W;
   const int own = tid >> 2, sub = tid & 3;
@@ -303,10 +310,13 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   };
 
   f32x16 acc[RS];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int t = 0; t < RS; ++t)
+    for (int t = 0; t < RS; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
+      for (int v = 0; v < 16; ++v) acc[t][v] = 0.f;
+  };
+  if (!PC) zero_acc();
   float dbias = 0.f;
   const bool do_bias = a.dbias_part != nullptr && tile_c == 0;
 
@@ -388,7 +398,42 @@ __global__ __launch_bounds__(256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   };
 
   __syncthreads();
-  if constexpr (DEPTH == 2) {
+  if constexpr (PC) {
+    // One barrier per step on both sides.  Step ks is multiplied from LDS
+    // buffer ks & 1 while the producers store step ks+1 into the other buffer
+    // (read by the consumers before the previous barrier) and load later steps.
+    if (producer) {
+      if (nsteps > 0) {
+        gload(I0{}, step_b);
+        if (DEPTH == 2 && nsteps > 1) gload(I1{}, step_b + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        sstore(I0{}, 0);
+        if (DEPTH == 1 && nsteps > 1) gload(I0{}, step_b + 1);
+        if (DEPTH == 2 && nsteps > 2) gload(I0{}, step_b + 2);
+      }
+      __syncthreads();
+      for (int ks = 0; ks < nsteps; ks += 2) {
+        // odd step ks+1 -> buffer 1 (register set 1 with two sets)
+        if (ks + 1 < nsteps) sstore(I1{}, 1);
+        if (DEPTH == 2 && ks + 3 < nsteps) gload(I1{}, step_b + ks + 3);
+        if (DEPTH == 1 && ks + 2 < nsteps) gload(I0{}, step_b + ks + 2);
+        __syncthreads();
+        if (ks + 1 >= nsteps) break;
+        // even step ks+2 -> buffer 0 (register set 0)
+        if (ks + 2 < nsteps) sstore(I0{}, 0);
+        if (DEPTH == 2 && ks + 4 < nsteps) gload(I0{}, step_b + ks + 4);
+        if (DEPTH == 1 && ks + 3 < nsteps) gload(I0{}, step_b + ks + 3);
+        __syncthreads();
+      }
+      return;
+    }
+    zero_acc();
+    __syncthreads();
+    for (int ks = 0; ks < nsteps; ++ks) {
+      compute(ks & 1);
+      __syncthreads();
+    }
+  } else if constexpr (DEPTH == 2) {
     // invariant at an even ks: LDS buffer 0 holds step ks, register set 1
     // step ks+1 (in flight), set 0 is free; the steady-state loads are
     // unconditional so that each wait covers only the older set
@@ -808,9 +853,9 @@ int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
   return VH_OK;
 }
 
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1, bool PC = false>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
-  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH>;
+  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH, PC>;
   static bool attr = false;
   if (!attr) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -818,7 +863,7 @@ int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
     attr = true;
   }
   dim3 grid((unsigned)(pl.tiles_o * pl.tiles_c * pl.splits));
-  kern<<<grid, 256, pl.lds, st>>>(pl.a);
+  kern<<<grid, PC ? 512 : 256, pl.lds, st>>>(pl.a);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -829,6 +874,18 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
   const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
   // two register sets when they fit (16-byte items: at most 6 + 6; 4- and
   // 8-byte items of whole rows: 16 + 16)
+  // whole rows: producer / consumer blocks (the producers' register sets: two
+  // for 4- and 8-byte items, one closer-fitting set for 16-byte items)
+  if (!seg) {
+    if constexpr (V == 8) {
+      if (pl.nd <= 8 && pl.nx <= 8) return launch_wgrad<3, 3, PW, V, 8, 8, false, 1, true>(pl, st);
+      if (pl.nd <= 8 && pl.nx <= 12) return launch_wgrad<3, 3, PW, V, 8, 12, false, 1, true>(pl, st);
+      if (pl.nd <= 12 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 12, 16, false, 1, true>(pl, st);
+      if (pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 1, true>(pl, st);
+    } else {
+      if (pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 2, true>(pl, st);
+    }
+  }
   if constexpr (V == 8) {
     if (pl.nd <= 6 && pl.nx <= 6)
       return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2>(pl, st) : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
