@@ -68,9 +68,10 @@ __device__ __forceinline__ u32x2p evens(u32x4p v) {
 // ------------------------------------------------------------------ forward
 // Block: the weight tile W[o0 .. o0+MT*32)[0 .. C) is copied to LDS once (odd
 // 16-byte pitch), then each of the 4 waves computes MT*32 output channels for
-// PT tiles of 32 output positions.  B fragment: 8 channels of one position (8
+// PT_FWD tiles of 32 output positions.  B fragment: 8 channels of one position (8
 // two-byte loads, channel planes apart); A fragment: one ds_read_b128.
-constexpr int PT = 2;  // position tiles per wave
+constexpr int PT_FWD = 1;  // position tiles per wave (one: twice the blocks in flight, measured faster)
+constexpr int PT_DG = 2;   // position tiles per wave of the input gradient
 
 template <int MT>
 __global__ __launch_bounds__(256) void pw_fwd_bf16_kernel(PwArgs a) {
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(256) void pw_fwd_bf16_kernel(PwArgs a) {
   const int PQ2 = PQ * 2;
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t yr = rsrc(a.out, a.out_bytes);
-  for (int t = 0; t < PT; ++t) {
-    const uint32_t pos = (((uint32_t)blockIdx.x * PT + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+  for (int t = 0; t < PT_FWD; ++t) {
+    const uint32_t pos = (((uint32_t)blockIdx.x * PT_FWD + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
     const bool valid = pos < (uint32_t)a.npos;
     uint32_t n, pq, p, q;
     a.fPQ.divmod(valid ? pos : 0u, n, pq);
@@ -170,8 +171,8 @@ __global__ __launch_bounds__(256) void pw_dgrad_bf16_kernel(PwArgs a) {
   const int HW2 = a.H * a.W * 2;
   const __amdgpu_buffer_rsrc_t dr = rsrc(a.dy, a.dy_bytes);
   const __amdgpu_buffer_rsrc_t xr = rsrc(a.out, a.out_bytes);
-  for (int t = 0; t < PT; ++t) {
-    const uint32_t pos = (((uint32_t)blockIdx.x * PT + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
+  for (int t = 0; t < PT_DG; ++t) {
+    const uint32_t pos = (((uint32_t)blockIdx.x * PT_DG + t) * 4u + (uint32_t)wave) * 32u + (uint32_t)col;
     const bool valid = pos < (uint32_t)a.npos;
     uint32_t n, pq, p, q;
     a.fPQ.divmod(valid ? pos : 0u, n, pq);
@@ -385,7 +386,7 @@ int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, in
   a.bias = (const uint16_t*)bias;
   a.out = y;
   a.out_bytes = a.dy_bytes;
-  dim3 grid((a.npos + PT * 128 - 1) / (PT * 128), (O + 127) / 128);
+  dim3 grid((a.npos + PT_FWD * 128 - 1) / (PT_FWD * 128), (O + 127) / 128);
   const size_t lds = (size_t)(O <= 64 ? 64 : 128) * ((C / 8) | 1) * 16;
   if (O <= 64) {
     grid.y = (O + 63) / 64;
@@ -406,7 +407,7 @@ int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, i
   a.out = dx;
   a.out_bytes = a.x_bytes;
   const bool s2 = S == 2 && W % 2 == 0;
-  dim3 grid((a.npos + PT * 128 - 1) / (PT * 128), (C + 127) / 128);
+  dim3 grid((a.npos + PT_DG * 128 - 1) / (PT_DG * 128), (C + 127) / 128);
   const size_t lds = (size_t)(C <= 64 ? 64 : 128) * ((O / 8) | 1) * 16;
   if (C <= 64) {
     grid.y = (C + 63) / 64;
