@@ -92,6 +92,12 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 // blocks per CU.
 constexpr int kFusedStageUnits = 2432;
 
+// Grids of at least this many tiles (3x3, several channel groups) use one LDS
+// stage and three blocks per CU.
+#ifndef VH_HALO_WPE3_MIN_TILES
+#define VH_HALO_WPE3_MIN_TILES 1024
+#endif
+
 // WPE = waves per SIMD the kernel is compiled for.  WPE 2: two LDS stages and
 // (for narrow tiles) two register sets, two blocks per CU.  WPE 3: one LDS
 // stage and one register set (at most 168 VGPRs), three blocks per CU -- more
@@ -707,7 +713,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
   const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
-  const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= 1024 && halo_xi(a) <= (WM == 1 ? 4 : 2);
+  const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= VH_HALO_WPE3_MIN_TILES && halo_xi(a) <= (WM == 1 ? 4 : 2);
   if (wpe3) a.stages = 1;
   const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
   const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
