@@ -51,12 +51,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, bytes, 0x00020000);
 }
 
-template <int BM, int BN, bool BIAS>
-__global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(DenseArgs g) {
+// PC: 512 threads; waves 0-3 only multiply (consumers, the accumulators),
+// waves 4-7 only load the next stages into registers and store them into the
+// other LDS buffer (producers, threads 256-511 serving the load map of threads
+// 0-255).  Neither role holds the other's registers, so two waves run per SIMD
+// and the loads leave the multiplying waves' instruction stream.
+template <int BM, int BN, bool BIAS, bool PC = false>
+__global__ __launch_bounds__(PC ? 512 : 256)
+void gemm_nt_bf16_kernel(DenseArgs g) {
   using Cfg = DenseCfg<BM, BN>;
   constexpr int FM = Cfg::FM, FN = Cfg::FN, PU = Cfg::PU, STAGE = Cfg::STAGE;
   extern __shared__ __attribute__((aligned(16))) u32x4d lds[];
-  const int tid = threadIdx.x, lane = tid & 63;
+  const bool producer = PC && threadIdx.x >= 256;
+  const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
   const int lb = xcd_block(g.tiles_m * g.tiles_n);
@@ -100,10 +107,13 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(DenseArgs g) {
   };
 
   f32x16 acc[FM][FN];
+  auto zero_acc = [&]() {
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+      for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+  };
+  if (!PC) zero_acc();
   const int row_l = lane & 31, half_l = lane >> 5;
   auto compute = [&](int st) {
     const u32x4d* ap = lds + st * STAGE + (wm + row_l) * PU + half_l;
@@ -126,6 +136,35 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(DenseArgs g) {
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   const int nk = (g.K + Cfg::BK - 1) / Cfg::BK;
+  if constexpr (PC) {
+    // one barrier per stage on both sides; stage k is multiplied from buffer
+    // k & 1 while the producers store stage k+1 into the other buffer (read
+    // by the consumers before the previous barrier) and load stage k+3
+    if (producer) {
+      gload(I0{}, 0);
+      if (nk > 1) gload(I1{}, Cfg::BK);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+      if (nk > 2) gload(I0{}, 2 * Cfg::BK);
+      __syncthreads();
+      for (int kt = 0; kt < nk; kt += 2) {
+        if (kt + 1 < nk) sstore(I1{}, 1);
+        if (kt + 3 < nk) gload(I1{}, (kt + 3) * Cfg::BK);
+        __syncthreads();
+        if (kt + 1 >= nk) break;
+        if (kt + 2 < nk) sstore(I0{}, 0);
+        if (kt + 4 < nk) gload(I0{}, (kt + 4) * Cfg::BK);
+        __syncthreads();
+      }
+      return;
+    }
+    zero_acc();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      compute(kt & 1);
+      __syncthreads();
+    }
+  } else {
   // invariant at an even stage k: LDS buffer 0 holds stage k, register set 1
   // holds stage k+1 (in flight), set 0 is free
   gload(I0{}, 0);
@@ -161,6 +200,7 @@ __global__ __launch_bounds__(256) void gemm_nt_bf16_kernel(DenseArgs g) {
       __syncthreads();
       compute(0);
     }
+  }
   }
 
   // epilogue: fp32 (+ bias), one rounding, row-major stores (lanes walk columns)
@@ -217,10 +257,10 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 
 bool fits(long bytes) { return bytes >= 0 && bytes < (1L << 31) - 64; }
 
-template <int BM, int BN, bool BIAS>
+template <int BM, int BN, bool BIAS, bool PC = false>
 int launch_nt(const DenseArgs& a0, hipStream_t st) {
   using Cfg = DenseCfg<BM, BN>;
-  auto kern = gemm_nt_bf16_kernel<BM, BN, BIAS>;
+  auto kern = gemm_nt_bf16_kernel<BM, BN, BIAS, PC>;
   static bool attr = false;
   const size_t lds = (size_t)2 * Cfg::STAGE * 16;
   if (!attr) {
@@ -231,7 +271,7 @@ int launch_nt(const DenseArgs& a0, hipStream_t st) {
   DenseArgs a = a0;
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
-  kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), 256, lds, st>>>(a);
+  kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), PC ? 512 : 256, lds, st>>>(a);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -261,10 +301,12 @@ int dense_nt_bf16(const void* a, int lda, const void* b, int ldb, void* c, int l
   g.a_bytes = (int)((long)M * lda * 2);
   g.b_bytes = (int)((long)N * ldb * 2);
   g.c_bytes = (int)((long)M * ldc * 2);
-  // 128 x 256 tiles (one block per CU, 64 x 128 per wave) when the grid still
-  // fills the chip, else 128 x 128 (two blocks per CU)
+  // 128 x 256 tiles (one block per CU, producer / consumer form, 64 x 128 per
+  // consumer wave) when the grid still fills the chip, else 128 x 128 (two
+  // blocks per CU of four waves that both load and multiply: already two waves
+  // per SIMD, and measured as fast as or faster than a split form)
   const long big = (long)((M + 127) / 128) * ((N + 255) / 256);
-  if (big >= 256) return bias ? launch_nt<128, 256, true>(g, st) : launch_nt<128, 256, false>(g, st);
+  if (big >= 256) return bias ? launch_nt<128, 256, true, true>(g, st) : launch_nt<128, 256, false, true>(g, st);
   return bias ? launch_nt<128, 128, true>(g, st) : launch_nt<128, 128, false>(g, st);
 }
 
