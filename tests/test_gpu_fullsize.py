@@ -88,6 +88,29 @@ def test_config3_resnet_block_bf16(layer):
               dw_images=(3, 127), bias=False)
 
 
+def test_config3_split_tail_bias_relu_bf16():
+    """64@56 at N=128 runs 1568 tiles on 768 block slots: the last 32 tiles run
+    as channel-group pieces whose fp32 sums a second kernel adds (with the bias
+    and the fused ReLU).  The last images lie in those tiles."""
+    g = np.random.default_rng(11)
+    B, C, O, H = 128, 64, 64, 56
+    x, xt = prep(g.standard_normal((B, C, H, H)), "bf16")
+    w, wt = prep(g.standard_normal((O, C, 3, 3)) * np.sqrt(2.0 / (C * 9)), "bf16")
+    b, bt = prep(g.uniform(-0.5, 0.5, (O,)), "bf16")
+    conv = vnn.Conv2d(C, O, 3, 1, 1, use_bias=True, device=DEV, dtype=torch.bfloat16)
+    conv.weight, conv.bias = wt, bt
+    conv.set_algo(vnn.ConvAlgo.IGEMM)
+    y = host(conv.forward(xt))
+    yr = host(conv.forward(xt, relu=True))
+    # ReLU before the one rounding equals ReLU of the rounded value, bit for bit
+    assert np.array_equal(yr, np.maximum(y, 0)), "fused ReLU differs from ReLU of the plain forward"
+    kw = dict(stride=(1, 1), pad=(1, 1))
+    bb = b[None, :, None, None]
+    for i in (0, 124, 125, 126, 127):
+        ref, sc = scaled(oracle.direct_conv, (x[i:i + 1], w), kw)
+        assert_parity(y[i:i + 1], ref + bb, sc + np.abs(bb), "bf16", f"y[{i}]")
+
+
 # ------------------------------------------------------------------ config 1 (f32, whole batch vs oracle)
 def test_config1_mnist_cnn_f32():
     for C, O in ((1, 32), (32, 64)):
