@@ -19,6 +19,7 @@
 // of one fragment read walk consecutive 16-byte cells: lanes 0-31 read plane 0,
 // lanes 32-63 plane 1, each at consecutive positions / output channels.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "vh_kernels.hpp"
@@ -606,6 +607,38 @@ int pick_xi_wpe3(const HaloArgs& a, int WM, size_t lds_bytes, hipStream_t st) {
 
 }  // namespace
 
+// Exact maximum number of ext rows any block of BN positions spans (positions
+// of P x TW virtual images, Hp ext rows per image, R taps).  The scan over all
+// blocks costs tens of microseconds of host time at the configs' sizes, so the
+// results are kept per shape (a small table, replaced round-robin).
+static int halo_rows_max(long Mv, int BN, long PQv, int TW, int Hp, int R) {
+  struct Entry {
+    long Mv, PQv;
+    int BN, TW, Hp, R, rows_max;
+  };
+  static std::mutex mu;
+  static Entry table[64];
+  static int used = 0, next = 0;
+  {
+    std::lock_guard<std::mutex> lk(mu);
+    for (int i = 0; i < used; ++i) {
+      const Entry& e = table[i];
+      if (e.Mv == Mv && e.PQv == PQv && e.BN == BN && e.TW == TW && e.Hp == Hp && e.R == R) return e.rows_max;
+    }
+  }
+  int rows_max = 0;
+  for (long m0 = 0; m0 < Mv; m0 += BN) {
+    const long ml = std::min(m0 + BN, Mv) - 1;
+    const long ra = (m0 / PQv) * Hp + (m0 % PQv) / TW, rb = (ml / PQv) * Hp + (ml % PQv) / TW;
+    rows_max = std::max(rows_max, (int)(rb + R - ra));
+  }
+  std::lock_guard<std::mutex> lk(mu);
+  table[next] = Entry{Mv, PQv, BN, TW, Hp, R, rows_max};
+  next = (next + 1) % 64;
+  if (used < 64) ++used;
+  return rows_max;
+}
+
 // Returns VH_ERR_UNSUPPORTED (without launching) when the shape is outside what
 // the halo kernel handles; the caller then uses the generic implicit GEMM.
 size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)((C + 15) / 16 * 16) * O * R * S * 2; }
@@ -658,13 +691,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     const int Wp = whole ? W + 2 * pw : (TW + S - 1 + cs + 1) & ~1;
     const int npairs = whole ? W / 2 : Wp / 2;
     const long PQv = (long)P * TW;
-    // exact maximum number of ext rows over all blocks
-    int rows_max = 0;
-    for (long m0 = 0; m0 < Mv; m0 += BN) {
-      const long ml = std::min(m0 + BN, Mv) - 1;
-      const long ra = (m0 / PQv) * a.Hp + (m0 % PQv) / TW, rb = (ml / PQv) * a.Hp + (ml % PQv) / TW;
-      rows_max = std::max(rows_max, (int)(rb + R - ra));
-    }
+    const int rows_max = halo_rows_max(Mv, BN, PQv, TW, a.Hp, R);
     const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * Wp + 2) * 16;
     const size_t lds = a.stages * stage;
     if (lds > 160 * 1024 || 2 * ((rows_max * npairs + 255) / 256) > 8) return false;
