@@ -362,8 +362,7 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths && ((uintptr_t)dx & 3) == 0) {
-    VH_TRY(VH_DISPATCH(dt, run_relayout, w, wd, (int)d.O, (int)d.C, (int)RS, 1, st, 0));
-    int r = pw_conv_bf16_dgrad(dy, wd, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
+    int r = pw_conv_bf16_dgrad(dy, w, dx, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH, st);
     if (r != VH_ERR_UNSUPPORTED) return r == VH_OK && mask ? mask_after(dt, mask, dx, d.B * d.C * d.H * d.W, st) : r;
   }
   if ((d.SH > 1 || d.SW > 1) && g_fast_paths) {

@@ -115,13 +115,13 @@ int dense_nt_bf16(const void* a, int lda, const void* b, int ldb, void* c, int l
 int transpose_bf16(const void* in, int ldi, void* out, int R, int Cc, hipStream_t st);
 
 // ---- strided 1x1 bf16 convolutions, pad 0 (vh_pointwise.hip) ----
-// w is the OIHW weight itself ([O][C]); wt its transpose [C][O].  Each returns
-// VH_ERR_UNSUPPORTED without launching when the shape is outside its envelope
-// (stride >= 2; forward C % 16 == 0 and C <= 248, dgrad O % 16 == 0 and
-// O <= 248, wgrad stride 2, W % 8 == 0, output rows a multiple of 4).
+// w is the OIHW weight itself ([O][C]).  Each returns VH_ERR_UNSUPPORTED
+// without launching when the shape is outside its envelope (stride >= 2;
+// forward C % 16 == 0 and C <= 248, dgrad O % 16 == 0, O <= 248 and
+// C % 8 == 0, wgrad stride 2, W % 8 == 0, output rows a multiple of 4).
 int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, int B, int C, int H, int W, int O,
                      int S, hipStream_t st);
-int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, int H, int W, int O, int S,
+int pw_conv_bf16_dgrad(const void* dy, const void* w, void* dx, int B, int C, int H, int W, int O, int S,
                        hipStream_t st);
 size_t pw_conv_bf16_wgrad_ws(int B, int C, int H, int W, int O, int S);
 int pw_conv_bf16_wgrad(const void* dy, const void* x, void* dw, int B, int C, int H, int W, int O, int S,

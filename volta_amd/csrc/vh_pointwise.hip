@@ -158,12 +158,20 @@ __global__ __launch_bounds__(256) void pw_dgrad_bf16_kernel(PwArgs a) {
   const int c0 = blockIdx.y * MT * 32;
   const int OU = a.O / 8, WPU = OU | 1;
   {
+    // A = W^T: the block's rows c0 .. c0+MT*32 of [C][O], transposed on the way
+    // into LDS from the layer's W [O][C] (C % 8 == 0): each 16-byte unit of W
+    // (8 consecutive c of one o) is scattered down column o of 8 LDS rows
     const __amdgpu_buffer_rsrc_t wr = rsrc(a.w, a.w_bytes);
-    for (int u = tid; u < MT * 32 * OU; u += 256) {
-      const int r = u / OU, ou = u - r * OU;
-      const int c = c0 + r;
-      wlds[r * WPU + ou] = __builtin_bit_cast(
-          u32x4p, __builtin_amdgcn_raw_buffer_load_b128(wr, c < a.C ? (c * a.O + ou * 8) * 2 : kOutOfRange, 0, 0));
+    uint16_t* w16 = reinterpret_cast<uint16_t*>(wlds);
+    constexpr int NCU = MT * 4;  // 8-channel units per block row range
+    for (int u = tid; u < a.O * NCU; u += 256) {
+      const int cu = u / a.O, o = u - cu * a.O;  // lanes along o: one LDS row per wave
+      const int c = c0 + cu * 8;
+      const u32x4p v = __builtin_bit_cast(
+          u32x4p, __builtin_amdgcn_raw_buffer_load_b128(wr, c < a.C ? (o * a.C + c) * 2 : kOutOfRange, 0, 0));
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        w16[(cu * 8 + e) * (WPU * 8) + o] = (uint16_t)((v[e >> 1] >> (16 * (e & 1))) & 0xffffu);
     }
   }
   __syncthreads();
@@ -398,12 +406,13 @@ int pw_conv_bf16_fwd(const void* x, const void* w, const void* bias, void* y, in
   return VH_OK;
 }
 
-int pw_conv_bf16_dgrad(const void* dy, const void* wt, void* dx, int B, int C, int H, int W, int O, int S,
+int pw_conv_bf16_dgrad(const void* dy, const void* w, void* dx, int B, int C, int H, int W, int O, int S,
                        hipStream_t st) {
-  if (!envelope(B, C, H, W, O, S) || O % 16 != 0 || O > 248) return VH_ERR_UNSUPPORTED;  // LDS weight tile
+  if (!envelope(B, C, H, W, O, S) || O % 16 != 0 || O > 248 || C % 8 != 0)  // LDS weight tile, 16-byte W units
+    return VH_ERR_UNSUPPORTED;
   PwArgs a = base_args(B, C, H, W, O, S);
   a.dy = dy;
-  a.w = wt;
+  a.w = w;
   a.out = dx;
   a.out_bytes = a.x_bytes;
   const bool s2 = S == 2 && W % 2 == 0;
