@@ -421,6 +421,8 @@ RELU_CASES = [
     # (B, C, O, H, W, K, S, P)
     (2, 32, 64, 28, 28, 3, 1, 1),    # config 1 conv2 / halo kernel (bf16)
     (2, 64, 64, 20, 24, 3, 1, 1),
+    (2, 64, 64, 14, 14, 3, 1, 1),    # P*Q % 8 == 4 and
+    (2, 32, 64, 7, 14, 3, 1, 1),     # P*Q % 4 == 2: halo epilogue position by position
     (1, 3, 64, 24, 32, 5, 1, 2),     # config 5 conv1 shape: one partial channel group
     (2, 64, 128, 16, 16, 1, 2, 0),   # strided 1x1 (bf16 pointwise kernels: separate ReLU pass)
     (2, 16, 24, 11, 9, 3, 2, 1),     # strided 3x3: stride phases
