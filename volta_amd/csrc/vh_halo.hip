@@ -63,6 +63,8 @@ struct HaloArgs {
   int stages;            // LDS stages (1 when there is a single channel group)
   int vec_epi;           // 1: whole rows, P*Q % 8 == 0 and 16-byte aligned y / mask:
                          // the epilogue transposes through LDS and stores 8 positions per lane
+  int pair_epi;          // 1: Q even, 4-byte aligned y / mask: lane pairs exchange values and
+                         // store two positions of one row per lane (no LDS)
   FastDiv fPQ, fQ;              // P*TW, TW
   FastDiv fW2, fRowsMax, fHp;   // item decomposition (Wp/2, rows_max, Hp)
   FastDiv fStrips;              // nstrips
@@ -427,6 +429,83 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 #undef WSM
 #undef XSM
   const int PQ = a.P * a.Q;
+  if (a.pair_epi) {
+    // Pair epilogue.  Accumulator v of a lane is output row (v>>2)*8 + (v&3)
+    // (+4 in the upper half-wave) at the lane's position.  Lanes 2m and 2m+1
+    // hold consecutive positions (the same image row: Q and every tile start
+    // are even); they swap one value of the rows v and v+1 (v even) so that the
+    // even lane holds row v and the odd lane row v+1, each at both positions,
+    // and store them as one dword: 32 dword stores per lane, no LDS.  fp32
+    // bias add and activation before the single rounding to bf16.
+    const int PQ2 = PQ * 2;
+    const bool odd = lane & 1;
+    const __amdgpu_buffer_rsrc_t yrsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.y, (short)0, a.y_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t mrsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(a.act == 2 ? a.mask : a.y), (short)0, a.y_bytes, 0x00020000);
+    int yoff[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      // the pair's first (even) position
+      uint32_t m = (uint32_t)(m0 + wn + j * 32 + (lane & 30)), vimg, pq, p, ql, n, strip;
+      a.fPQ.divmod(m, vimg, pq);
+      a.fQ.divmod(pq, p, ql);
+      a.fStrips.divmod(vimg, n, strip);
+      const int q = (int)strip * a.TW + (int)ql;
+      yoff[j] = (int)m < a.M && q < a.Q
+                    ? (int)((n * (uint32_t)a.O * (uint32_t)PQ + p * (uint32_t)a.Q + (uint32_t)q) * 2u) +
+                          ((lane >> 5) * 4 + (lane & 1)) * PQ2
+                    : (int)0x80000000u;
+    }
+    float bv[FM][16];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
+        bv[i][v] = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
+      }
+    // the ReLU-backward mask of the dwords this lane stores, all loaded before the first store
+    uint32_t mk[FM][FN][8];
+    if (a.act == 2) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int vp = 0; vp < 8; ++vp) {
+          const int orow = o0 + wm + i * 32 + (vp >> 1) * 8 + (vp & 1) * 2;
+#pragma unroll
+          for (int j = 0; j < FN; ++j) mk[i][j][vp] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, yoff[j], orow * PQ2, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int vp = 0; vp < 8; ++vp) {
+        const int v = 2 * vp;  // rows v, v+1 = orow, orow+1
+        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);  // wave-uniform part of o
+        const bool ok = full_o || orow + (lane >> 5) * 4 + (lane & 1) < a.O;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          float a0 = acc[i][j][v] + bv[i][v], a1 = acc[i][j][v + 1] + bv[i][v + 1];
+          if (a.act == 1) {
+            a0 = fmaxf(a0, 0.f);
+            a1 = fmaxf(a1, 0.f);
+          }
+          // the even lane needs its partner's row-v value, the odd lane its partner's row-(v+1) value
+          const float recv = __builtin_bit_cast(
+              float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, odd ? a0 : a1), 0xB1, 0xF, 0xF, false));
+          const float lo = odd ? recv : a0, hi = odd ? a1 : recv;
+          uint32_t d = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+          if (a.act == 2) {
+            const uint32_t m = mk[i][j][vp];
+            d &= (bf16_to_f32((uint16_t)(m & 0xffffu)) > 0.f ? 0x0000ffffu : 0u) |
+                 (bf16_to_f32((uint16_t)(m >> 16)) > 0.f ? 0xffff0000u : 0u);
+          }
+          if (ok) __builtin_amdgcn_raw_buffer_store_b32(d, yrsrc, yoff[j], orow * PQ2, 0);
+        }
+      }
+    return;
+  }
   if (a.vec_epi) {
     // Vector epilogue.  Each wave writes its 64 o x 64 position tile, bias added
     // and rounded once to bf16 (ReLU applied in fp32 first), into its own LDS
@@ -737,6 +816,11 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // output (and mask); its LDS (4 waves x 64 x 72 bf16) reuses the stages
   a.vec_epi = (whole && (P * Q) % 8 == 0 && ((uintptr_t)y & 15) == 0 && (act != 2 || ((uintptr_t)mask & 15) == 0))
                   ? 1 : 0;
+  // else the pair epilogue: even Q and strip width, 4-byte aligned output (and mask).
+  // (Where both apply, the vector form measured 1-4 us faster on 64@56 and 128@28.)
+  a.pair_epi = (!a.vec_epi && Q % 2 == 0 && a.TW % 2 == 0 && ((uintptr_t)y & 3) == 0 &&
+                (act != 2 || ((uintptr_t)mask & 3) == 0))
+                   ? 1 : 0;
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
   const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
