@@ -33,6 +33,7 @@ namespace vh {
   } while (0)
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 struct HaloArgs {
   const uint16_t* x;     // [N][C][H][W]
@@ -111,9 +112,15 @@ constexpr int kFusedStageUnits = 2432;
 // reads of the other, and each channel group's global loads and the previous
 // group's LDS stores are interleaved with its MFMAs instead of running as
 // phases of their own.
-template <int R, int S, int WM, int XI, int WPE, bool FUSED = false>
+// WD (fused form: 3x3, 64-channel tiles, C % 16 == 0): the weights are read straight from
+// the layer's W [O][C][3][3] instead of a channel-grouped copy, so the forward
+// needs no relayout launch.  Thread t stages output channel o0 + t/4, channels
+// 4 (t%4) .. +3 of the group: 36 contiguous bf16 (9 dword-pair loads), repacked
+// per tap into one 8-byte LDS store of 4 channels.
+template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
+  static_assert(!WD || (R == 3 && S == 3 && WM == 1), "direct weight staging: 3x3, 64-channel tiles");
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int SU = FUSED ? kFusedStageUnits : 1;
   __shared__ __attribute__((aligned(16))) u32x4 lds0[SU];
@@ -225,8 +232,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   const __amdgpu_buffer_rsrc_t wrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.wt, (short)0, a.w_bytes, 0x00020000);
   int w_goff[Cfg::WITER], w_loff[Cfg::WITER];
+  // WD: byte offset of the thread's 36 weights at channel group 0 (group
+  // offset c0 * 18), and the LDS byte offset of its tap-0 store
+  int wd_goff = 0, wd_loff = 0;
+  if constexpr (WD) {
+    const int o = tid >> 2, q = tid & 3;
+    wd_goff = o0 + o < a.O ? ((o0 + o) * a.C + 4 * q) * 18 : (int)0x80000000u;
+    wd_loff = (o * Cfg::WPU + (q >> 1)) * 16 + (q & 1) * 8;
+  }
 #pragma unroll
-  for (int it = 0; it < Cfg::WITER; ++it) {
+  for (int it = 0; it < (WD ? 0 : Cfg::WITER); ++it) {
     const int u = tid + it * 256;
     const int o = u / (RS * 2), rem = u % (RS * 2);
     const int og = o0 + o;
@@ -242,7 +257,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // items per thread) keep one set to stay within two waves' registers.
   constexpr int DEPTH = (WPE == 2 && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
   static_assert(!FUSED || DEPTH == 2, "the fused form keeps two register sets");
-  u32x4 wreg[DEPTH][Cfg::WITER];
+  u32x4 wreg[DEPTH][WD ? 1 : Cfg::WITER];
+  u32x2 wdr[DEPTH][WD ? 9 : 1];
   uint32_t xreg[DEPTH][Cfg::XITER][8];
   // Loads of channel group c0 .. c0+15.  Every load is issued (no branches, so
   // the compiler's wait counts stay exact across the pipeline): channels past C
@@ -251,10 +267,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     constexpr int sI = decltype(SET)::value;
     const int crem = a.C - c0;  // channels left from c0 (<= 0 past the last group)
     // the fused form loads only whole groups inside C (C % 16 == 0, c0 < C)
+    if constexpr (WD) {
 #pragma unroll
-    for (int it = 0; it < Cfg::WITER; ++it)
-      wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   FUSED || crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
+      for (int j = 0; j < 9; ++j)
+        wdr[sI][j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   FUSED || crem > 0 ? wrsrc : zrsrc, wd_goff + 8 * j, c0 * 18, 0));
+    } else {
+#pragma unroll
+      for (int it = 0; it < Cfg::WITER; ++it)
+        wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                     FUSED || crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
+    }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       const int half = it < XH ? 0 : 1;
@@ -268,8 +291,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     constexpr int sI = decltype(SET)::value;
     // unconditional stores (masked items go to the sink), so the wait for the
     // older register set does not also wait for the loads issued after it
+    if constexpr (WD) {
+      // dword k of the 18 loaded holds elements 2k, 2k+1 (element e = channel
+      // e / 9, tap e % 9); tap t takes elements t, 9+t, 18+t, 27+t
+      auto dw = [&](int k) { return wdr[sI][k >> 1][k & 1]; };
+      auto two = [&](int e0, int e1) {  // bf16 e0 low, e1 high
+        const uint32_t sel = (2u * (e0 & 1)) | ((2u * (e0 & 1) + 1u) << 8) | ((4u + 2u * (e1 & 1)) << 16) |
+                             ((5u + 2u * (e1 & 1)) << 24);
+        return __builtin_amdgcn_perm(dw(e1 >> 1), dw(e0 >> 1), sel);
+      };
+      char* wb = reinterpret_cast<char*>(WSM(st)) + wd_loff;
 #pragma unroll
-    for (int it = 0; it < Cfg::WITER; ++it) WSM(st)[w_loff[it]] = wreg[sI][it];
+      for (int t = 0; t < 9; ++t) {
+        u32x2 v;
+        v[0] = two(t, 9 + t);
+        v[1] = two(18 + t, 27 + t);
+        *reinterpret_cast<u32x2*>(wb + t * 32) = v;
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < Cfg::WITER; ++it) WSM(st)[w_loff[it]] = wreg[sI][it];
+    }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       {
@@ -336,6 +378,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     // group +2 and the LDS stores of group +1 (into the other stage) placed
     // between them: per tap, 4 MFMAs with 3 global loads, one LDS store and
     // the fragment reads of the tap after next in the gaps.
+    // LDS stores per group (WD: 9 weight stores + 2 per x item, spread over the taps)
+    constexpr int NDSW = WD ? 9 + 2 * Cfg::XITER : 0;
     auto fused = [&](auto ST, auto LSET, int lc0, auto SSET) {
       constexpr int st = decltype(ST)::value;
       gload(LSET, lc0);
@@ -348,7 +392,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
         __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // global loads
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (t + 2 < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);  // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
+        // LDS stores: one per tap (WD: NDSW spread over the taps)
+        if (WD && t < NDSW % RS) __builtin_amdgcn_sched_group_barrier(0x200, WD ? NDSW / RS + 1 : 1, 0);
+        else __builtin_amdgcn_sched_group_barrier(0x200, WD ? NDSW / RS : 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
         if (t + 2 < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);
@@ -645,10 +691,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 // ---------------------------------------------------------------- host side
 namespace {
 
-template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false>
+template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
-  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED>;
+  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD>;
   static bool attr_set = false;
   if (!attr_set) {
     // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
@@ -828,14 +874,29 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   if (wpe3) a.stages = 1;
   const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
   const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
-  VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
-  if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
   // Fused form (two register sets, whole channel groups, stages and the
   // vector epilogue within the static stage size): 3x3, 64 x 256 tiles with
   // at most 4 x items per thread.
   const int stage_units = WM * 64 * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
-  if (R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
-      stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16)) {
+  const bool fused = !wpe3 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
+                     stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16);
+  // The fused forward reads W [O][C][3][3] directly (no relayout launch).  Each
+  // block then repacks its weights itself: free in the fused form (128@28 and
+  // 256@14 ran as fast as with the grouped copy), 4 us more than the relayout
+  // saves in the three-blocks-per-CU form of 64@56 (1568 blocks, 9 scattered
+  // 8-byte loads per lane and group), which keeps the grouped copy.
+  const bool wd = w_mode == 0 && fused && (long)O * C * 18 < (1L << 31) - 16;
+  if (wd) {
+    a.wt = (const uint16_t*)w;
+    a.w_bytes = O * C * 18;
+  } else {
+    VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
+  }
+  if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
+  if (fused) {
+    if (wd)
+      return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, 2, true, true>(a, lds, st)
+                             : launch_halo<3, 3, 1, 4, 2, true, true>(a, lds, st);
     return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, 2, true>(a, lds, st) : launch_halo<3, 3, 1, 4, 2, true>(a, lds, st);
   }
 #define VH_HALO(RR, SS)                                           \
