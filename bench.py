@@ -45,18 +45,18 @@ METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
 # when that pass is the dominant one (which of these is the slowest varies by a
 # few percent from run to run).
 MEASURED_TRAFFIC_BYTES = {
-    # relayout_grouped_kernel: fetch 84.7 KiB x2, write 72; conv_halo_bf16_kernel<3,3,1,4,3,false>: fetch 25695.6 x2, write 50176
-    "3x3 64->64 @56 fwd": int(((84.7 + 25695.6) * 2 + 72 + 50176) * 1024),
-    # relayout_grouped_kernel: fetch 220.0 x2, write 72; conv_halo_bf16_kernel<3,3,1,4,3,false>: fetch 25677.3 x2, write 50176
-    "3x3 64->64 @56 dgrad": int(((220.0 + 25677.3) * 2 + 72 + 50176) * 1024),
-    # relayout_grouped_kernel: fetch 228.0 x2, write 288; conv_halo_bf16_kernel<3,3,1,2,2,true>: fetch 13862.9 x2, write 25145.6
-    "3x3 128->128 @28 fwd": int(((228.0 + 13862.9) * 2 + 288 + 25145.6) * 1024),
-    # wgrad_rows_bf16_kernel<..,true>: fetch 25198.3 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.8 x2, write 288
-    "3x3 128->128 @28 wgrad": int(((25198.3 + 18465.8) * 2 + 36864 + 288) * 1024),
-    # relayout_grouped_kernel: fetch 876.3 x2, write 1152; conv_halo_bf16_kernel<3,3,1,2,2,true>: fetch 11585.1 x2, write 12659.1
-    "3x3 256->256 @14 fwd": int(((876.3 + 11585.1) * 2 + 1152 + 12659.1) * 1024),
-    # wgrad_rows_bf16_kernel<..,true>: fetch 12651.4 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.9 x2, write 1152
-    "3x3 256->256 @14 wgrad": int(((12651.4 + 18465.9) * 2 + 36864 + 1152) * 1024),
+    # relayout_grouped_kernel: fetch 84.8 KiB x2, write 72; conv_halo_bf16_kernel<3,3,1,4,3,false,false>: fetch 25758.8 x2, write 50176
+    "3x3 64->64 @56 fwd": int(((84.8 + 25758.8) * 2 + 72 + 50176) * 1024),
+    # relayout_grouped_kernel: fetch 220.0 x2, write 72; conv_halo_bf16_kernel<3,3,1,4,3,false,false>: fetch 25773.0 x2, write 50176
+    "3x3 64->64 @56 dgrad": int(((220.0 + 25773.0) * 2 + 72 + 50176) * 1024),
+    # conv_halo_bf16_kernel<3,3,1,2,2,true,1> (weights read directly): fetch 13891.5 x2, write 25144.5
+    "3x3 128->128 @28 fwd": int((13891.5 * 2 + 25144.5) * 1024),
+    # wgrad_rows_bf16_kernel<..,true>: fetch 25199.3 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.8 x2, write 288
+    "3x3 128->128 @28 wgrad": int(((25199.3 + 18465.8) * 2 + 36864 + 288) * 1024),
+    # conv_halo_bf16_kernel<3,3,1,2,2,true,1> (weights read directly): fetch 11568.8 x2, write 12699.4
+    "3x3 256->256 @14 fwd": int((11568.8 * 2 + 12699.4) * 1024),
+    # wgrad_rows_bf16_kernel<..,true>: fetch 12651.5 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.9 x2, write 1152
+    "3x3 256->256 @14 wgrad": int(((12651.5 + 18465.9) * 2 + 36864 + 1152) * 1024),
 }
 
 # (name, C, O, H, K, stride, pad) at N=128
