@@ -519,6 +519,71 @@ __global__ __launch_bounds__(256) void column_sum_kernel(const typename Elem<T>:
   part[(long)blockIdx.y * N + col] = s;
 }
 
+// Same sums with VE = 16 / sizeof(element) columns per lane (16-byte loads; N %
+// VE == 0, 16-byte aligned rows): the rows of a slice are added in the same
+// order, so the results equal the one-column kernel's.
+template <typename T>
+__global__ __launch_bounds__(256) void column_sum_vec_kernel(const typename Elem<T>::storage* __restrict__ x, int M,
+                                                             int N, float* __restrict__ part, int rows_per) {
+  using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  const int col = (blockIdx.x * 256 + threadIdx.x) * VE;
+  if (col >= N) return;
+  const int r0 = blockIdx.y * rows_per, r1 = min(M, r0 + rows_per);
+  float s[VE] = {};
+#pragma unroll 8
+  for (int r = r0; r < r1; ++r) {
+    const uint4 v = *reinterpret_cast<const uint4*>(x + (long)r * N + col);
+    const S* e = reinterpret_cast<const S*>(&v);
+#pragma unroll
+    for (int k = 0; k < VE; ++k) s[k] += Elem<T>::to_f32(e[k]);
+  }
+  float* o = part + (long)blockIdx.y * N + col;
+#pragma unroll
+  for (int k = 0; k < VE; k += 4) *reinterpret_cast<float4*>(o + k) = make_float4(s[k], s[k + 1], s[k + 2], s[k + 3]);
+}
+
+// Fixed-order sum of partial slabs part[z][i] (z < splits, i < n, n % 4 == 0,
+// 16-byte aligned slabs) read as float4: a block adds QB = 256 >> lg_g quads;
+// its threads form G = 2^lg_g split groups (thread t: quad t % QB, group t / QB),
+// group g adds z = g, g + G, ... in order, then the group sums are added in
+// group order.  Several 16-byte loads in flight per lane.
+template <typename T>
+__global__ __launch_bounds__(256) void sum_partials_vec4_kernel(const float* __restrict__ part, int splits, long n,
+                                                                typename Elem<T>::storage* __restrict__ out,
+                                                                int lg_g) {
+  __shared__ float4 red[256];
+  const int t = threadIdx.x, G = 1 << lg_g, QB = 256 >> lg_g;
+  const int q = t & (QB - 1), g = t >> (8 - lg_g);
+  const long nq = n >> 2;
+  const float4* p4 = reinterpret_cast<const float4*>(part);
+  for (long base = (long)blockIdx.x * QB; base < nq; base += (long)gridDim.x * QB) {
+    const long qi = base + q;
+    float4 a = {0.f, 0.f, 0.f, 0.f};
+    if (qi < nq) {
+#pragma unroll 8
+      for (int z = g; z < splits; z += G) {
+        const float4 v = p4[(size_t)z * nq + qi];
+        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+      }
+    }
+    red[t] = a;
+    __syncthreads();
+    if (g == 0 && qi < nq) {
+      float4 r = red[q];
+      for (int h = 1; h < G; ++h) {
+        const float4 v = red[h * QB + q];
+        r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+      }
+      out[qi * 4 + 0] = Elem<T>::from_f32(r.x);
+      out[qi * 4 + 1] = Elem<T>::from_f32(r.y);
+      out[qi * 4 + 2] = Elem<T>::from_f32(r.z);
+      out[qi * 4 + 3] = Elem<T>::from_f32(r.w);
+    }
+    __syncthreads();
+  }
+}
+
 // ============================================================== pixel shuffle
 // out[b][c][h*r+i][w*r+j] = in[b][c*r*r+i*r+j][h][w]; forward walks the output
 // (coalesced stores), backward walks the input gradient.
@@ -940,8 +1005,10 @@ int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, i
 }
 
 size_t column_sum_ws(int M, int N, int* nslice, int* rows_per) {
-  int cb = (N + 255) / 256;
-  int s = std::max(1, std::min(M / 64, std::max(1, 1024 / cb)));
+  // slices of at least 8 rows, enough of them for ~512 blocks of the
+  // 8-columns-per-lane kernel
+  int cb = (N + 2047) / 2048;
+  int s = std::max(1, std::min(M / 8, std::max(1, 512 / cb)));
   *rows_per = (M + s - 1) / s;
   *nslice = (M + *rows_per - 1) / *rows_per;
   return (size_t)(*nslice) * N * sizeof(float);
@@ -950,6 +1017,18 @@ size_t column_sum_ws(int M, int N, int* nslice, int* rows_per) {
 template <typename T>
 int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st) {
   using S = typename Elem<T>::storage;
+  constexpr int VE = 16 / sizeof(S);
+  if (N % VE == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)ws & 15) == 0) {
+    column_sum_vec_kernel<T><<<dim3((N / VE + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
+    VH_LAUNCH_CHECK();
+    int lg_g = 0;  // split groups: about 8 loads per lane, at most 16 groups
+    while (lg_g < 4 && (nslice >> (lg_g + 1)) >= 8) ++lg_g;
+    const long qb = 256 >> lg_g;
+    const int nb = (int)std::min<long>((N / 4 + qb - 1) / qb, 1L << 20);
+    sum_partials_vec4_kernel<T><<<nb, 256, 0, st>>>(ws, nslice, N, (S*)out, lg_g);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   column_sum_kernel<T><<<dim3((N + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
   VH_LAUNCH_CHECK();
   sum_partials_kernel<T><<<reduce_splits_grid(N), 256, 0, st>>>(ws, nslice, N, (S*)out);
