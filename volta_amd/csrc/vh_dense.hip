@@ -13,8 +13,8 @@
 // Block: 256 threads (2 x 2 waves), tile BM x BN, K in stages of 64; two LDS
 // stages and two register sets: the loads of stage k+2 are issued before the
 // MFMAs of stage k (kept there by sched_barrier), the stores of stage k+1 into
-// LDS follow them.  XCD-aware block order: consecutive logical blocks share
-// the A rows of one m-tile.
+// LDS follow them.  XCD-aware block order: the blocks resident on one XCD
+// cover groups of 8 m-tiles x a few n-tiles, sharing A and B slices in L2.
 #include <type_traits>
 
 #include "vh_kernels.hpp"
@@ -66,8 +66,15 @@ void gemm_nt_bf16_kernel(DenseArgs g) {
   const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (wave >> 1) * (BM / 2), wn = (wave & 1) * (BN / 2);
+  // logical block -> tile in groups of up to 8 m-tiles: consecutive logical
+  // blocks (the ones resident on one XCD at a time) walk 8 m-tiles, then the
+  // next n-tile, so they share both A and B slices in that XCD's L2 (32 of them
+  // cover 8 x 4 tiles instead of 1 x 32)
   const int lb = xcd_block(g.tiles_m * g.tiles_n);
-  const int m0 = (lb / g.tiles_n) * BM, n0 = (lb % g.tiles_n) * BN;
+  const int grp = lb / (8 * g.tiles_n), first_m = grp * 8;
+  const int gm = min(g.tiles_m - first_m, 8);
+  const int in_grp = lb - grp * 8 * g.tiles_n;
+  const int m0 = (first_m + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
 
   // load items: unit u = tid + 256*it -> row u / KU, column unit u % KU (= tid % KU)
   const int cu = tid % Cfg::KU;
