@@ -26,6 +26,10 @@ typedef unsigned int u32x4d __attribute__((ext_vector_type(4)));
 namespace {
 
 constexpr int kOOR = (int)0x80000000u;  // buffer offset past every range: loads 0, stores dropped
+#ifndef VH_GEMM_GROUP_M
+#define VH_GEMM_GROUP_M 8
+#endif
+constexpr int kGroupM = VH_GEMM_GROUP_M;  // m-tiles per group of the block order
 
 struct DenseArgs {
   const uint16_t* a;     // [M][lda]
@@ -71,9 +75,9 @@ void gemm_nt_bf16_kernel(DenseArgs g) {
   // next n-tile, so they share both A and B slices in that XCD's L2 (32 of them
   // cover 8 x 4 tiles instead of 1 x 32)
   const int lb = xcd_block(g.tiles_m * g.tiles_n);
-  const int grp = lb / (8 * g.tiles_n), first_m = grp * 8;
-  const int gm = min(g.tiles_m - first_m, 8);
-  const int in_grp = lb - grp * 8 * g.tiles_n;
+  const int grp = lb / (kGroupM * g.tiles_n), first_m = grp * kGroupM;
+  const int gm = min(g.tiles_m - first_m, kGroupM);
+  const int in_grp = lb - grp * kGroupM * g.tiles_n;
   const int m0 = (first_m + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
 
   // load items: unit u = tid + 256*it -> row u / KU, column unit u % KU (= tid % KU)
