@@ -31,7 +31,7 @@ constexpr int kOutOfRange = (int)0x80000000u;  // buffer offset past every range
 
 struct PwArgs {
   const void* x;      // [B][C][H][W]
-  const void* w;      // forward [O][C]; dgrad [C][O] (transposed copy)
+  const void* w;      // [O][C] (the dgrad kernel transposes it into LDS)
   const void* dy;     // [B][O][P][Q]
   const uint16_t* bias;
   void* out;          // forward y; dgrad dx
