@@ -1014,6 +1014,24 @@ size_t column_sum_ws(int M, int N, int* nslice, int* rows_per) {
   return (size_t)(*nslice) * N * sizeof(float);
 }
 
+// out[i] = sum over z of part[z][i] in split order (i < n): the float4 split-group
+// kernel when n % 4 == 0 and the slabs are 16-byte aligned, else one output per lane.
+template <typename T>
+int run_sum_partials(const float* part, int splits, long n, void* out, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  if (n % 4 == 0 && ((uintptr_t)part & 15) == 0) {
+    int lg_g = 0;  // split groups: about 8 loads per lane, at most 16 groups
+    while (lg_g < 4 && (splits >> (lg_g + 1)) >= 8) ++lg_g;
+    const long qb = 256 >> lg_g;
+    const int nb = (int)std::min<long>((n / 4 + qb - 1) / qb, 1L << 20);
+    sum_partials_vec4_kernel<T><<<nb, 256, 0, st>>>(part, splits, n, (S*)out, lg_g);
+  } else {
+    sum_partials_kernel<T><<<reduce_splits_grid(n), 256, 0, st>>>(part, splits, n, (S*)out);
+  }
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 template <typename T>
 int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st) {
   using S = typename Elem<T>::storage;
@@ -1021,13 +1039,7 @@ int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice
   if (N % VE == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)ws & 15) == 0) {
     column_sum_vec_kernel<T><<<dim3((N / VE + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
     VH_LAUNCH_CHECK();
-    int lg_g = 0;  // split groups: about 8 loads per lane, at most 16 groups
-    while (lg_g < 4 && (nslice >> (lg_g + 1)) >= 8) ++lg_g;
-    const long qb = 256 >> lg_g;
-    const int nb = (int)std::min<long>((N / 4 + qb - 1) / qb, 1L << 20);
-    sum_partials_vec4_kernel<T><<<nb, 256, 0, st>>>(ws, nslice, N, (S*)out, lg_g);
-    VH_LAUNCH_CHECK();
-    return VH_OK;
+    return run_sum_partials<T>(ws, nslice, N, out, st);
   }
   column_sum_kernel<T><<<dim3((N + 255) / 256, nslice), 256, 0, st>>>((const S*)x, M, N, ws, rows_per);
   VH_LAUNCH_CHECK();
@@ -1163,6 +1175,7 @@ int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, floa
                                      hipStream_t);                                                      \
   template int run_channel_sum<T>(const void*, int, int, int, void*, float*, int, hipStream_t);         \
   template int run_column_sum<T>(const void*, int, int, void*, float*, int, int, hipStream_t);          \
+  template int run_sum_partials<T>(const float*, int, long, void*, hipStream_t);                        \
   template int run_pixel_shuffle<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);     \
   template int run_relu<T>(const void*, const void*, void*, long, hipStream_t);                         \
   template int run_sum<T>(const void*, long, float*, float*, hipStream_t);                              \

@@ -79,6 +79,9 @@ int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, i
 size_t column_sum_ws(int M, int N, int* nslice, int* rows_per);
 template <typename T>
 int run_column_sum(const void* x, int M, int N, void* out, float* ws, int nslice, int rows_per, hipStream_t st);
+// out[i] = sum over z < splits of part[z][i] (fixed order), rounded once to T
+template <typename T>
+int run_sum_partials(const float* part, int splits, long n, void* out, hipStream_t st);
 template <typename T>
 int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
 

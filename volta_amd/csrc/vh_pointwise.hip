@@ -349,12 +349,6 @@ __global__ __launch_bounds__(256) void pw_wgrad_s2_bf16_kernel(PwArgs a) {
   }
 }
 
-// dW[o][c] = sum over blocks z of part[z][o][c], fixed order
-__global__ __launch_bounds__(256) void pw_wgrad_reduce_kernel(const float* __restrict__ part, int splits,
-                                                              int total, uint16_t* __restrict__ dw) {
-  reduce_splits_block(part, splits, total, [&](long i, float s) { dw[i] = f32_to_bf16(s); });
-}
-
 bool fits_i32(long v) { return v > 0 && v < (1L << 31) - 16; }
 
 PwArgs base_args(int B, int C, int H, int W, int O, int S) {
@@ -486,10 +480,7 @@ int pw_conv_bf16_wgrad(const void* dy, const void* x, void* dw, int B, int C, in
   else if (it <= 12) r = launch_pw_wgrad<12>(a, grid, st);
   else r = launch_pw_wgrad<16>(a, grid, st);
   if (r != VH_OK) return r;
-  const int total = O * C;
-  pw_wgrad_reduce_kernel<<<reduce_splits_grid(total), 256, 0, st>>>(ws, splits, total, (uint16_t*)dw);
-  VH_LAUNCH_CHECK();
-  return VH_OK;
+  return run_sum_partials<bf16>(ws, splits, (long)O * C, dw, st);
 }
 
 }  // namespace vh
