@@ -122,7 +122,7 @@ __device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, co
 // Load items: thread t serves row owner t/4 (an o of the dY tile, a c of the x
 // tile) and takes that owner's chunks t%4, t%4 + 4, ...; chunk k of a dY owner
 // is row k / cpr, column (k % cpr) * V.  Offsets advance incrementally.
-// PC (whole rows): 512 threads, waves 0-3 multiply (consumers), waves 4-7 only
+// PC: 512 threads, waves 0-3 multiply (consumers), waves 4-7 only
 // load and store into LDS (producers, threads 256-511 serving the item map of
 // threads 0-255).  Neither role holds the other's registers, so two waves fit
 // per SIMD and the loads run beside the MFMAs of the other role.
@@ -133,7 +133,6 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
   constexpr int TO = 64, TC = 64;  // block tile (o, c)
   using VT = typename VecT<V>::t;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  static_assert(!PC || !SEG, "producer / consumer split: whole rows only");
   const bool producer = PC && threadIdx.x >= 256;
   const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
@@ -874,7 +873,8 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
   const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
   // two register sets when they fit (16-byte items: at most 6 + 6; 4- and
   // 8-byte items of whole rows: 16 + 16)
-  // whole rows: producer / consumer blocks (the producers' register sets: two
+  // producer / consumer blocks for whole rows and for the 16-byte-item segment
+  // form (below); whole rows (the producers' register sets: two
   // for 4- and 8-byte items, one closer-fitting set for 16-byte items)
   if (!seg) {
     if constexpr (V == 8) {
@@ -888,7 +888,8 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
   }
   if constexpr (V == 8) {
     if (pl.nd <= 6 && pl.nx <= 6)
-      return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2>(pl, st) : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
+      return seg ? launch_wgrad<3, 3, PW, V, 6, 6, true, 2, true>(pl, st)
+                 : launch_wgrad<3, 3, PW, V, 6, 6, false, 2>(pl, st);
   } else {
     if (!seg && pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 2>(pl, st);
   }
