@@ -116,6 +116,58 @@ __device__ __forceinline__ void reduce_splits_block(const float* __restrict__ pa
 
 inline int reduce_splits_grid(long total) { return (int)std::min<long>((total + 63) / 64, 1L << 20); }
 
+// The same reduction read as float4 quads (total % 4 == 0, 16-byte aligned
+// slabs), for few outputs and many splits: a pass covers QB = 256 >> lg_g
+// quads; the threads form G = 2^lg_g split groups (thread t: quad t % QB,
+// group t / QB), group g adds z = g, g + G, ... in order with several 16-byte
+// loads in flight per lane, and the G group sums are added in group order.
+// store(i, sum) is called for each of the four outputs of a quad.
+template <typename Store>
+__device__ __forceinline__ void reduce_splits_vec4_block(const float* __restrict__ part, int splits, long total,
+                                                         int lg_g, Store store, int blk, int nblk) {
+  __shared__ float4 red4[256];
+  const int t = threadIdx.x, G = 1 << lg_g, QB = 256 >> lg_g;
+  const int q = t & (QB - 1), g = t >> (8 - lg_g);
+  const long nq = total >> 2;
+  const float4* p4 = reinterpret_cast<const float4*>(part);
+  for (long base = (long)blk * QB; base < nq; base += (long)nblk * QB) {
+    const long qi = base + q;
+    float4 a = {0.f, 0.f, 0.f, 0.f};
+    if (qi < nq) {
+#pragma unroll 8
+      for (int z = g; z < splits; z += G) {
+        const float4 v = p4[(size_t)z * nq + qi];
+        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+      }
+    }
+    red4[t] = a;
+    __syncthreads();
+    if (g == 0 && qi < nq) {
+      float4 r = red4[q];
+      for (int h = 1; h < G; ++h) {
+        const float4 v = red4[h * QB + q];
+        r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
+      }
+      store(qi * 4 + 0, r.x);
+      store(qi * 4 + 1, r.y);
+      store(qi * 4 + 2, r.z);
+      store(qi * 4 + 3, r.w);
+    }
+    __syncthreads();
+  }
+}
+
+// Split groups for reduce_splits_vec4_block: about 8 loads per lane, at most 16 groups.
+inline int reduce_vec4_lg_groups(int splits) {
+  int lg_g = 0;
+  while (lg_g < 4 && (splits >> (lg_g + 1)) >= 8) ++lg_g;
+  return lg_g;
+}
+inline int reduce_vec4_grid(long total, int lg_g) {
+  const long qb = 256 >> lg_g;
+  return (int)std::min<long>((total / 4 + qb - 1) / qb, 1L << 20);
+}
+
 // Record an error message for vh_last_error(); returns the status.
 int set_error(int status, const char* fmt, ...);
 

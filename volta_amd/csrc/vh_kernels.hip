@@ -544,44 +544,13 @@ __global__ __launch_bounds__(256) void column_sum_vec_kernel(const typename Elem
 }
 
 // Fixed-order sum of partial slabs part[z][i] (z < splits, i < n, n % 4 == 0,
-// 16-byte aligned slabs) read as float4: a block adds QB = 256 >> lg_g quads;
-// its threads form G = 2^lg_g split groups (thread t: quad t % QB, group t / QB),
-// group g adds z = g, g + G, ... in order, then the group sums are added in
-// group order.  Several 16-byte loads in flight per lane.
+// 16-byte aligned slabs) read as float4 quads (reduce_splits_vec4_block).
 template <typename T>
 __global__ __launch_bounds__(256) void sum_partials_vec4_kernel(const float* __restrict__ part, int splits, long n,
                                                                 typename Elem<T>::storage* __restrict__ out,
                                                                 int lg_g) {
-  __shared__ float4 red[256];
-  const int t = threadIdx.x, G = 1 << lg_g, QB = 256 >> lg_g;
-  const int q = t & (QB - 1), g = t >> (8 - lg_g);
-  const long nq = n >> 2;
-  const float4* p4 = reinterpret_cast<const float4*>(part);
-  for (long base = (long)blockIdx.x * QB; base < nq; base += (long)gridDim.x * QB) {
-    const long qi = base + q;
-    float4 a = {0.f, 0.f, 0.f, 0.f};
-    if (qi < nq) {
-#pragma unroll 8
-      for (int z = g; z < splits; z += G) {
-        const float4 v = p4[(size_t)z * nq + qi];
-        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
-      }
-    }
-    red[t] = a;
-    __syncthreads();
-    if (g == 0 && qi < nq) {
-      float4 r = red[q];
-      for (int h = 1; h < G; ++h) {
-        const float4 v = red[h * QB + q];
-        r.x += v.x; r.y += v.y; r.z += v.z; r.w += v.w;
-      }
-      out[qi * 4 + 0] = Elem<T>::from_f32(r.x);
-      out[qi * 4 + 1] = Elem<T>::from_f32(r.y);
-      out[qi * 4 + 2] = Elem<T>::from_f32(r.z);
-      out[qi * 4 + 3] = Elem<T>::from_f32(r.w);
-    }
-    __syncthreads();
-  }
+  reduce_splits_vec4_block(part, splits, n, lg_g, [&](long i, float v) { out[i] = Elem<T>::from_f32(v); },
+                           (int)blockIdx.x, (int)gridDim.x);
 }
 
 // ============================================================== pixel shuffle
@@ -1020,11 +989,8 @@ template <typename T>
 int run_sum_partials(const float* part, int splits, long n, void* out, hipStream_t st) {
   using S = typename Elem<T>::storage;
   if (n % 4 == 0 && ((uintptr_t)part & 15) == 0) {
-    int lg_g = 0;  // split groups: about 8 loads per lane, at most 16 groups
-    while (lg_g < 4 && (splits >> (lg_g + 1)) >= 8) ++lg_g;
-    const long qb = 256 >> lg_g;
-    const int nb = (int)std::min<long>((n / 4 + qb - 1) / qb, 1L << 20);
-    sum_partials_vec4_kernel<T><<<nb, 256, 0, st>>>(part, splits, n, (S*)out, lg_g);
+    const int lg_g = reduce_vec4_lg_groups(splits);
+    sum_partials_vec4_kernel<T><<<reduce_vec4_grid(n, lg_g), 256, 0, st>>>(part, splits, n, (S*)out, lg_g);
   } else {
     sum_partials_kernel<T><<<reduce_splits_grid(n), 256, 0, st>>>(part, splits, n, (S*)out);
   }
