@@ -96,6 +96,12 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 // blocks per CU.
 constexpr int kFusedStageUnits = 2432;
 
+// The fused form as producer / consumer blocks (512 threads, four waves per SIMD).
+#ifndef VH_HALO_PC
+#define VH_HALO_PC 1
+#endif
+#define VH_HALO_FUSED_WPE (VH_HALO_PC ? 4 : 2)
+
 // Grids of at least this many tiles (3x3, several channel groups) use one LDS
 // stage and three blocks per CU.
 #ifndef VH_HALO_WPE3_MIN_TILES
@@ -117,9 +123,14 @@ constexpr int kFusedStageUnits = 2432;
 // needs no relayout launch.  Thread t stages output channel o0 + t/4, channels
 // 4 (t%4) .. +3 of the group: 36 contiguous bf16 (9 dword-pair loads), repacked
 // per tap into one 8-byte LDS store of 4 channels.
-template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
+// PC (fused form, 512 threads, WPE 4: two blocks per CU): waves 0-3 only
+// multiply (consumers: the accumulators), waves 4-7 only load the next channel
+// groups and store them into the other LDS stage (producers, threads 256-511
+// serving the load map of threads 0-255); one barrier per group on both sides.
+template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false, bool PC = false>
+__global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
+  static_assert(!PC || FUSED, "producer / consumer split: fused form only");
   static_assert(!WD || (R == 3 && S == 3 && WM == 1), "direct weight staging: 3x3, 64-channel tiles");
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int SU = FUSED ? kFusedStageUnits : 1;
@@ -128,7 +139,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   extern __shared__ __attribute__((aligned(16))) u32x4 lds_dyn[];
   u32x4* const lds = FUSED ? lds0 : lds_dyn;
 
-  const int tid = threadIdx.x, lane = tid & 63;
+  const bool producer = PC && threadIdx.x >= 256;
+  const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wm = (wave / Cfg::WN) * FM * 32;  // wave's first output channel in the tile
   const int wn = (wave % Cfg::WN) * FN * 32;  // wave's first position in the tile
@@ -255,8 +267,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // are issued while group kt is multiplied and group kt+1 is written to LDS,
   // so every load has two compute phases to arrive; wide tiles (more than 4 x or 5 weight load
   // items per thread) keep one set to stay within two waves' registers.
-  constexpr int DEPTH = (WPE == 2 && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
-  static_assert(!FUSED || DEPTH == 2, "the fused form keeps two register sets");
+  // (PC: the producers keep one set -- a group's loads have the consumers'
+  // whole multiply phase to arrive -- so that both roles fit 128 registers)
+  constexpr int DEPTH = (WPE == 2 && !PC && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
+  static_assert(!FUSED || PC || DEPTH == 2, "the fused form keeps two register sets");
   u32x4 wreg[DEPTH][WD ? 1 : Cfg::WITER];
   u32x2 wdr[DEPTH][WD ? 9 : 1];
   uint32_t xreg[DEPTH][Cfg::XITER][8];
@@ -367,7 +381,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
   // flight), set 0 is free.  The steady-state loop issues its loads without
   // conditions so that each wait covers only the older register set.
   const int nk = (a.C + 15) / 16;
-  if constexpr (DEPTH == 2) {
+  if constexpr (PC) {
+    // group kt is multiplied from stage kt & 1 while the producers store group
+    // kt+1 into the other stage (read by the consumers before the previous
+    // barrier) and load group kt+2 (fused form: every group is whole, C % 16 == 0)
+    if (producer) {
+      gload(I0{}, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+      if (nk > 1) gload(I0{}, 16);
+      __syncthreads();
+      for (int kt = 0; kt < nk; kt += 2) {
+        if (kt + 1 < nk) sstore(I0{}, 1);
+        if (kt + 2 < nk) gload(I0{}, (kt + 2) * 16);
+        __syncthreads();
+        if (kt + 1 >= nk) break;
+        if (kt + 2 < nk) sstore(I0{}, 0);
+        if (kt + 3 < nk) gload(I0{}, (kt + 3) * 16);
+        __syncthreads();
+      }
+      return;
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      compute(kt & 1);
+      __syncthreads();
+    }
+  } else if constexpr (DEPTH == 2) {
     gload(I0{}, 0);
     gload(I1{}, FUSED && nk < 2 ? 0 : 16);  // all zeros when there is a single group
     __builtin_amdgcn_sched_barrier(0);
@@ -560,7 +600,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
     // positions (16 bytes) per lane.  P*Q % 8 == 0, so a run never crosses an
     // image and its address is 16-byte aligned.
     constexpr int EP = 72;
-    __syncthreads();  // every wave has finished reading the last stage
+    if constexpr (!PC) __syncthreads();  // every wave has finished reading the last stage
+                                         // (PC: the consumers' last loop barrier)
     uint16_t* eb = reinterpret_cast<uint16_t*>(lds) + wave * (64 * EP);
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -691,10 +732,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 // ---------------------------------------------------------------- host side
 namespace {
 
-template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false>
+template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false, bool PC = false>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
-  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD>;
+  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC>;
   static bool attr_set = false;
   if (!attr_set) {
     // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
@@ -706,7 +747,7 @@ int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   HaloArgs g = a;
   g.tiles_m = (a.M + Cfg::BN - 1) / Cfg::BN;
   g.tiles_o = (a.O + Cfg::BM - 1) / Cfg::BM;
-  kern<<<dim3((unsigned)(g.tiles_m * g.tiles_o)), 256, FUSED ? 0 : lds_bytes, st>>>(g);
+  kern<<<dim3((unsigned)(g.tiles_m * g.tiles_o)), PC ? 512 : 256, FUSED ? 0 : lds_bytes, st>>>(g);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -895,9 +936,10 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
   if (fused) {
     if (wd)
-      return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, 2, true, true>(a, lds, st)
-                             : launch_halo<3, 3, 1, 4, 2, true, true>(a, lds, st);
-    return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, 2, true>(a, lds, st) : launch_halo<3, 3, 1, 4, 2, true>(a, lds, st);
+      return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, VH_HALO_FUSED_WPE, true, true, VH_HALO_PC>(a, lds, st)
+                             : launch_halo<3, 3, 1, 4, VH_HALO_FUSED_WPE, true, true, VH_HALO_PC>(a, lds, st);
+    return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, VH_HALO_FUSED_WPE, true, false, VH_HALO_PC>(a, lds, st)
+                           : launch_halo<3, 3, 1, 4, VH_HALO_FUSED_WPE, true, false, VH_HALO_PC>(a, lds, st);
   }
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
