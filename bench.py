@@ -49,12 +49,12 @@ MEASURED_TRAFFIC_BYTES = {
     "3x3 64->64 @56 fwd": int(((84.8 + 25758.8) * 2 + 72 + 50176) * 1024),
     # relayout_grouped_kernel: fetch 220.0 x2, write 72; conv_halo_bf16_kernel<3,3,1,4,3,false,false>: fetch 25773.0 x2, write 50176
     "3x3 64->64 @56 dgrad": int(((220.0 + 25773.0) * 2 + 72 + 50176) * 1024),
-    # conv_halo_bf16_kernel<3,3,1,2,2,true,1> (weights read directly): fetch 13891.5 x2, write 25144.5
-    "3x3 128->128 @28 fwd": int((13891.5 * 2 + 25144.5) * 1024),
+    # conv_halo_bf16_kernel<3,3,1,2,4,true,true,true> (weights read directly): fetch 13903.0 x2, write 25143.1
+    "3x3 128->128 @28 fwd": int((13903.0 * 2 + 25143.1) * 1024),
     # wgrad_rows_bf16_kernel<..,true>: fetch 25199.3 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.8 x2, write 288
     "3x3 128->128 @28 wgrad": int(((25199.3 + 18465.8) * 2 + 36864 + 288) * 1024),
-    # conv_halo_bf16_kernel<3,3,1,2,2,true,1> (weights read directly): fetch 11568.8 x2, write 12699.4
-    "3x3 256->256 @14 fwd": int((11568.8 * 2 + 12699.4) * 1024),
+    # conv_halo_bf16_kernel<3,3,1,2,4,true,true,true> (weights read directly): fetch 11551.3 x2, write 12674.2
+    "3x3 256->256 @14 fwd": int((11551.3 * 2 + 12674.2) * 1024),
     # wgrad_rows_bf16_kernel<..,true>: fetch 12651.5 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18465.9 x2, write 1152
     "3x3 256->256 @14 wgrad": int(((12651.5 + 18465.9) * 2 + 36864 + 1152) * 1024),
 }
