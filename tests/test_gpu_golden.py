@@ -59,8 +59,10 @@ def test_conv_fixture(name, algo):
     y = conv.forward(x)
     dx, dw, db = conv.backward(dev(d["dy"], dt), x)
     sc = _conv_scales(d)
+    HO, WO = oracle.conv_out(H, K, S, P), oracle.conv_out(W, K, S, P)
+    ks = dict(y=C * K * K + 1, dx=O * K * K, dw=B * HO * WO, db=B * HO * WO)
     for k, got in (("y", y), ("dx", dx), ("dw", dw), ("db", db)):
-        assert_parity(host(got), d[k], sc[k], dt, f"{name}/{algo.name}/{k}")
+        assert_parity(host(got), d[k], sc[k], dt, f"{name}/{algo.name}/{k}", k=ks[k])
 
 
 @pytest.mark.parametrize("name", CONVT)
@@ -77,8 +79,10 @@ def test_conv_transpose_fixture(name):
     st, pd = (S, S), (P, P)
     sy = oracle.conv_transpose_forward(a["x"], a["w"], a["b"], st, pd)
     sdx, sdw, sdb = oracle.conv_transpose_backward(a["dy"], a["x"], a["w"], st, pd)
+    HO, WO = d["y"].shape[2:]
+    ks = dict(y=CI * K * K + 1, dx=CO * K * K, dw=B * H * W, db=B * HO * WO)
     for k, got, sc in (("y", y, sy), ("dx", dx, sdx), ("dw", dw, sdw), ("db", db, sdb)):
-        assert_parity(host(got), d[k], sc, dt, f"{name}/{k}")
+        assert_parity(host(got), d[k], sc, dt, f"{name}/{k}", k=ks[k])
 
 
 @pytest.mark.parametrize("name", LINEAR)
@@ -94,8 +98,9 @@ def test_linear_fixture(name):
     a = _abs(d)
     sy = oracle.linear_forward(a["x"], a["w"], a["b"])
     sdx, sdw, sdb = oracle.linear_backward(a["dy"], a["x"], a["w"])
+    ks = dict(y=IN + 1, dx=OUT, dw=M, db=M)
     for k, got, sc in (("y", y, sy), ("dx", dx, sdx), ("dw", dw, sdw), ("db", db, sdb)):
-        assert_parity(host(got), d[k], sc, dt, f"{name}/{k}")
+        assert_parity(host(got), d[k], sc, dt, f"{name}/{k}", k=ks[k])
 
 
 def test_pixel_shuffle_fixture():

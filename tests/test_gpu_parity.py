@@ -12,7 +12,7 @@ import oracle
 import volta_amd
 from volta_amd import nn as vnn
 from volta_amd import ops
-from tests.parity import assert_parity
+from tests.parity import assert_parity, k_conv_dgrad, k_conv_fwd, k_conv_wgrad
 
 pytestmark = pytest.mark.gpu
 
@@ -42,12 +42,13 @@ def ref_and_scale(fn, *args, **kw):
     return fn(*args, **kw), fn(*ab, **kw)
 
 
-def check(got, fn, args, dt, what, kw=None, extra_ref=None, extra_scale=None):
+def check(got, fn, args, dt, what, kw=None, extra_ref=None, extra_scale=None, k=None):
+    """k: products per output element (required by the bf16 gate)."""
     ref, scale = ref_and_scale(fn, *args, **(kw or {}))
     if extra_ref is not None:
         ref = ref + extra_ref
         scale = scale + extra_scale
-    return assert_parity(host(got), ref, scale, dt, what)
+    return assert_parity(host(got), ref, scale, dt, what, k=k)
 
 
 # ------------------------------------------------------------------ known answers
@@ -109,9 +110,9 @@ def test_matmul_family(mkn, dt):
     a, at = prep(g.standard_normal((m, k)), dt)
     b, bt = prep(g.standard_normal((k, n)), dt)
     gr, grt = prep(g.standard_normal((m, n)), dt)
-    check(ops.gpu_matmul(at, bt, m, k, n), oracle.matmul, (a, b), dt, "matmul")
-    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), dt, "dA")
-    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), dt, "dB")
+    check(ops.gpu_matmul(at, bt, m, k, n), oracle.matmul, (a, b), dt, "matmul", k=k)
+    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), dt, "dA", k=n)
+    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), dt, "dB", k=m)
 
 
 @pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (1, 7, 5)])
@@ -125,11 +126,11 @@ def test_linear_fwd_bwd(shape, dt):
     dy, dyt = prep(g.standard_normal((m, o)), dt)
     lin = vnn.Linear(i, o, device=DEV, dtype=DTYPES[dt])
     lin.weight, lin.bias = wt, bt
-    check(lin.forward(xt), oracle.linear_forward, (x, w, b), dt, "y")
+    check(lin.forward(xt), oracle.linear_forward, (x, w, b), dt, "y", k=i + 1)
     dx, dw, db = lin.backward(dyt, xt)
-    check(dx, lambda *a: oracle.linear_backward(*a)[0], (dy, x, w), dt, "dx")
-    check(dw, lambda *a: oracle.linear_backward(*a)[1], (dy, x, w), dt, "dw")
-    check(db, lambda *a: oracle.linear_backward(*a)[2], (dy, x, w), dt, "db")
+    check(dx, lambda *a: oracle.linear_backward(*a)[0], (dy, x, w), dt, "dx", k=o)
+    check(dw, lambda *a: oracle.linear_backward(*a)[1], (dy, x, w), dt, "dw", k=m)
+    check(db, lambda *a: oracle.linear_backward(*a)[2], (dy, x, w), dt, "db", k=m)
 
 
 # ------------------------------------------------------------------ Conv2d
@@ -173,12 +174,15 @@ def test_conv2d_fwd_bwd(case, algo, dt):
     bb = b[None, :, None, None]
     y_shape = (B, O, oracle.conv_out(H, K, S, P), oracle.conv_out(W, K, S, P))
     check(y, oracle.direct_conv, (x, w), dt, "y", dict(stride=(S, S), pad=(P, P)),
-          extra_ref=bb, extra_scale=np.abs(bb))
+          extra_ref=bb, extra_scale=np.abs(bb), k=k_conv_fwd(C, K, K))
     dy, dyt = prep(g.standard_normal(y_shape), dt)
     dx, dw, db = conv.backward(dyt, xt)
-    check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", dict(stride=(S, S), pad=(P, P)))
-    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", dict(stride=(S, S), pad=(P, P)))
-    check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+    kwg = k_conv_wgrad(B, y_shape[2], y_shape[3])
+    check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", dict(stride=(S, S), pad=(P, P)),
+          k=k_conv_dgrad(O, K, K))
+    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", dict(stride=(S, S), pad=(P, P)),
+          k=kwg)
+    check(db, oracle.conv_bias_grad, (dy,), dt, "db", k=kwg)
     if algo == vnn.ConvAlgo.Direct and dt == "f32":
         # the direct kernels keep Volta's CPU summation order and unfused
         # multiply/add (conv.rs:1370-1407, 458-505): bit-identical results
@@ -197,16 +201,17 @@ def test_gpu_ops_boundary_functions(dt):
     dy, dyt = prep(g.standard_normal((B, O, HO, WO)), dt)
     dims = (B, C, O, H, W, K, K, S, S, P, P, HO, WO)
     kw = dict(stride=(S, S), pad=(P, P))
-    check(ops.gpu_direct_conv(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "direct", kw)
-    check(ops.gpu_igemm(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "igemm", kw)
+    kf, kd, kwg = k_conv_fwd(C, K, K, bias=False), k_conv_dgrad(O, K, K), k_conv_wgrad(B, HO, WO)
+    check(ops.gpu_direct_conv(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "direct", kw, k=kf)
+    check(ops.gpu_igemm(xt, wt, *dims), oracle.direct_conv, (x, w), dt, "igemm", kw, k=kf)
     check(ops.gpu_conv_backward_input(dyt, wt, *dims), oracle.direct_conv_backward_input, (dy, w, x.shape), dt,
-          "direct dx", kw)
+          "direct dx", kw, k=kd)
     check(ops.gpu_igemm_backward_input(dyt, wt, *dims), oracle.direct_conv_backward_input, (dy, w, x.shape), dt,
-          "igemm dx", kw)
+          "igemm dx", kw, k=kd)
     check(ops.gpu_conv_backward_weight(dyt, xt, *dims), oracle.direct_conv_backward_weight, (dy, x, w.shape), dt,
-          "direct dw", kw)
+          "direct dw", kw, k=kwg)
     check(ops.gpu_igemm_backward_weight(dyt, xt, *dims), oracle.direct_conv_backward_weight, (dy, x, w.shape), dt,
-          "igemm dw", kw)
+          "igemm dw", kw, k=kwg)
     # im2col / col2im on the padded input, exact copies (sums for col2im)
     xp = oracle.pad(x, P, P)
     xpt = torch.from_numpy(xp).to(DEV, DTYPES[dt])
@@ -215,7 +220,7 @@ def test_gpu_ops_boundary_functions(dt):
     assert np.array_equal(host(col), oracle.im2col(xp, (K, K), (S, S)))
     gcol, gcolt = prep(g.standard_normal(col.shape), dt)
     back = ops.gpu_col2im(gcolt, B, C, HP, WP, K, K, S, S, HO, WO)
-    check(back, oracle.col2im, (gcol, xp.shape, (K, K), (S, S)), dt, "col2im")
+    check(back, oracle.col2im, (gcol, xp.shape, (K, K), (S, S)), dt, "col2im", k=K * K)
 
 
 def test_bad_shape_is_an_error_not_a_crash():
@@ -276,12 +281,14 @@ def test_conv2d_bf16_fast_and_generic_paths(case, policy):
         y = conv.forward(xt)
         bb = b[None, :, None, None]
         kw = dict(stride=(S, S), pad=(P, P))
-        check(y, oracle.direct_conv, (x, w), dt, "y", kw, extra_ref=bb, extra_scale=np.abs(bb))
+        check(y, oracle.direct_conv, (x, w), dt, "y", kw, extra_ref=bb, extra_scale=np.abs(bb),
+              k=k_conv_fwd(C, K, K))
         dy, dyt = prep(g.standard_normal(tuple(y.shape)), dt)
         dx, dw, db = conv.backward(dyt, xt)
-        check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", kw)
-        check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw)
-        check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+        kwg = k_conv_wgrad(B, y.shape[2], y.shape[3])
+        check(dx, oracle.direct_conv_backward_input, (dy, w, x.shape), dt, "dx", kw, k=k_conv_dgrad(O, K, K))
+        check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw, k=kwg)
+        check(db, oracle.conv_bias_grad, (dy,), dt, "db", k=kwg)
     finally:
         volta_amd.check(volta_amd.lib().vh_set_kernel_policy(volta_amd._lib.POLICY_FASTEST))
 
@@ -311,11 +318,13 @@ def test_conv_transpose2d_fwd_bwd(case, dt):
     ct.weight, ct.bias = wt, bt
     y = ct.forward(xt)
     kw = dict(stride=(S, S), pad=(P, P))
-    ref_y = check(y, oracle.conv_transpose_forward, (x, w, b), dt, "y", kw)
+    check(y, oracle.conv_transpose_forward, (x, w, b), dt, "y", kw, k=CI * K * K + 1)
     dy, dyt = prep(g.standard_normal(tuple(y.shape)), dt)
     dx, dw, db = ct.backward(dyt, xt)
+    ks = (CO * K * K, B * H * W, B * y.shape[2] * y.shape[3])
     for i, (name, got) in enumerate((("dx", dx), ("dw", dw), ("db", db))):
-        check(got, lambda *a, i=i, **k: oracle.conv_transpose_backward(*a, **k)[i], (dy, x, w), dt, name, kw)
+        check(got, lambda *a, i=i, **k: oracle.conv_transpose_backward(*a, **k)[i], (dy, x, w), dt, name, kw,
+              k=ks[i])
 
 
 # ------------------------------------------------------------------ PixelShuffle
@@ -449,17 +458,18 @@ def test_conv2d_fused_relu_fwd_and_masked_dgrad(case, algo, dt):
     y = conv.forward(xt, relu=True)
     got = host(y)
     assert (got >= 0).all()
-    assert_parity(got, np.maximum(ref + bb, 0), scale + np.abs(bb), dt, "relu(y)")
+    assert_parity(got, np.maximum(ref + bb, 0), scale + np.abs(bb), dt, "relu(y)", k=k_conv_fwd(C, K, K))
     dy, dyt = prep(g.standard_normal(got.shape), dt)
     dx, dw, db = conv.backward(dyt, xt, relu_input=True)
     dref, dscale = ref_and_scale(oracle.direct_conv_backward_input, dy, w, x.shape, **kw)
     mask = x > 0
     gdx = host(dx)
     assert (gdx[~mask] == 0).all()
-    assert_parity(gdx, np.where(mask, dref, 0), dscale, dt, "masked dx")
+    assert_parity(gdx, np.where(mask, dref, 0), dscale, dt, "masked dx", k=k_conv_dgrad(O, K, K))
     # the weight and bias gradients are those of the plain backward
-    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw)
-    check(db, oracle.conv_bias_grad, (dy,), dt, "db")
+    kwg = k_conv_wgrad(B, got.shape[2], got.shape[3])
+    check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw, k=kwg)
+    check(db, oracle.conv_bias_grad, (dy,), dt, "db", k=kwg)
 
 
 # ------------------------------------------------------------------ the step after dW
