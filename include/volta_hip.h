@@ -28,7 +28,14 @@
  *    last failure of the calling thread.
  *  - Every tensor must hold fewer than 2^31 elements (VH_ERR_UNSUPPORTED otherwise).
  *  - Workspace (split-K partials, re-laid-out weights, im2col matrices) is taken
- *    from a per-stream cache inside the library; calls on one stream may reuse it.
+ *    from one grow-only device buffer per stream inside the library; calls on
+ *    one stream reuse it in stream order.  A buffer that a call outgrows is
+ *    retired, not freed, so a HIP graph captured earlier from library calls
+ *    stays valid; retired and current workspaces are freed only by
+ *    vh_release_cache(), which therefore invalidates every such graph.  While a
+ *    stream is being captured the library never allocates, frees or
+ *    synchronises for it: a call whose workspace would have to grow returns
+ *    VH_ERR_CAPTURE (run the call once eagerly on that stream before capturing).
  */
 #ifndef VOLTA_HIP_H
 #define VOLTA_HIP_H
@@ -47,7 +54,9 @@ typedef enum {
   VH_ERR_OOM = 3,         /* device allocation failed: GpuBuffer::zeros -> None */
   VH_ERR_LAUNCH = 4,      /* HIP runtime / kernel launch error */
   VH_ERR_BAD_ARG = 5,     /* null pointer, bad enum value */
-  VH_ERR_UNSUPPORTED = 6  /* tensor too large for 32-bit indexing */
+  VH_ERR_UNSUPPORTED = 6, /* tensor too large for 32-bit indexing */
+  VH_ERR_CAPTURE = 7      /* the stream's workspace would have to grow while the stream is
+                             being captured into a HIP graph (see Workspace below) */
 } vh_status;
 
 typedef enum { VH_F32 = 0, VH_BF16 = 1 } vh_dtype;
@@ -60,14 +69,20 @@ typedef enum { VH_ALGO_DIRECT = 0, VH_ALGO_IM2COL = 1, VH_ALGO_IGEMM = 2, VH_ALG
 int vh_init(void);
 const char* vh_last_error(void);
 /* GpuBuffer::zeros / from_slice / to_vec (src/gpu/buffer.rs:40-220) and the
- * size-bucketed pool (src/gpu/pool.rs:28-35, 123-190). */
+ * size-bucketed pool (src/gpu/pool.rs:28-35, 123-190).  Like the reference's
+ * pool, which serves one in-order wgpu queue, the pool is single-stream: vh_free
+ * makes the buffer available to the next vh_alloc at once, so free a buffer only
+ * when every later use of the reallocated memory is ordered after its last use
+ * (one stream, or a synchronisation in between). */
 int vh_alloc(size_t bytes, void** dptr);
 int vh_free(void* dptr);
 int vh_upload(void* dst_dev, const void* src_host, size_t bytes, void* stream);
 int vh_download(void* dst_host, const void* src_dev, size_t bytes, void* stream);
 /* GpuContext::sync (src/gpu/context.rs:342-382). */
 int vh_stream_sync(void* stream);
-/* Releases cached workspace and pooled buffers (pool.rs clear). */
+/* Releases cached workspace and pooled buffers (pool.rs clear) after a device
+ * synchronisation.  Invalidates every HIP graph captured from library calls;
+ * must not be called while a stream is being captured. */
 int vh_release_cache(void);
 /* Kernel choice inside an algorithm (no reference counterpart: Volta has one
  * shader per op).  VH_POLICY_FASTEST (default) uses specialised kernels where

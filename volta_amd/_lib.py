@@ -21,6 +21,7 @@ VH_ERR_OOM = 3
 VH_ERR_LAUNCH = 4
 VH_ERR_BAD_ARG = 5
 VH_ERR_UNSUPPORTED = 6
+VH_ERR_CAPTURE = 7
 
 F32 = 0
 BF16 = 1

@@ -68,32 +68,51 @@ static constexpr size_t kPoolMaxCount = 64;
 static size_t round_bytes(size_t b) { return (b + 255) & ~size_t(255); }
 
 // ------------------------------------------------------------------ per-stream workspace
+// One grow-only device buffer per HIP stream; stream order makes its reuse by
+// consecutive calls on that stream safe.  A buffer that a later call outgrows
+// is retired, never freed on the spot: a HIP graph captured earlier on the
+// stream still holds its address (and kernels queued on the stream may still
+// use it).  Retired buffers are freed only by vh_release_cache(), which is why
+// a release invalidates every graph captured from library calls.  While the
+// stream is being captured the workspace never grows (that would allocate, and
+// synchronise nothing, in the middle of a capture): the call fails with
+// VH_ERR_CAPTURE and the caller runs it once eagerly before capturing.
 struct Ws {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 static std::mutex g_ws_mu;
 static std::unordered_map<hipStream_t, Ws> g_ws;
+static std::vector<void*> g_ws_retired;
 
-// Returns a device buffer of >= bytes private to `st` (stream order makes reuse safe).
+// Growth rule of ws_get: the new size to allocate, or 0 when `have` suffices.
+static size_t ws_grow_to(size_t have, size_t need) {
+  if (need <= have) return 0;
+  return round_bytes(std::max(need, have * 5 / 4));
+}
+
+// Returns a device buffer of >= bytes private to `st`.
 static int ws_get(hipStream_t st, size_t bytes, void** out) {
   *out = nullptr;
   if (bytes == 0) return VH_OK;
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Ws& w = g_ws[st];
-  if (w.bytes < bytes) {
-    if (w.ptr) {
-      VH_HIP_CHECK(hipStreamSynchronize(st));
-      VH_HIP_CHECK(hipFree(w.ptr));
-      w.ptr = nullptr;
-      w.bytes = 0;
-    }
-    size_t nb = round_bytes(std::max(bytes, w.bytes * 5 / 4));
-    hipError_t e = hipMalloc(&w.ptr, nb);
-    if (e != hipSuccess) {
-      w.ptr = nullptr;
+  const size_t nb = ws_grow_to(w.bytes, bytes);
+  if (nb) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VH_HIP_CHECK(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone)
+      return set_error(VH_ERR_CAPTURE,
+                       "workspace of this stream (%zu bytes) must grow to %zu while the stream is captured: "
+                       "run the call once eagerly on the stream before capturing",
+                       w.bytes, bytes);
+    void* p = nullptr;
+    if (hipMalloc(&p, nb) != hipSuccess) {
+      (void)hipGetLastError();
       return set_error(VH_ERR_OOM, "workspace allocation of %zu bytes failed", nb);
     }
+    if (w.ptr) g_ws_retired.push_back(w.ptr);  // may still be referenced: freed by vh_release_cache only
+    w.ptr = p;
     w.bytes = nb;
   }
   *out = w.ptr;
@@ -673,9 +692,18 @@ int vh_alloc(size_t bytes, void** dptr) {
   }
   void* p = nullptr;
   if (hipMalloc(&p, nb) != hipSuccess) {
-    // drop the cache and retry once
-    vh_release_cache();
-    if (hipMalloc(&p, nb) != hipSuccess) return set_error(VH_ERR_OOM, "hipMalloc(%zu) failed", nb);
+    // drop the pooled free buffers (not the workspaces: captured graphs may use them) and retry once
+    (void)hipGetLastError();
+    {
+      std::lock_guard<std::mutex> lk(g_pool.mu);
+      for (auto& kv : g_pool.free_list) (void)hipFree(kv.second);
+      g_pool.free_list.clear();
+      g_pool.cached = 0;
+    }
+    if (hipMalloc(&p, nb) != hipSuccess) {
+      (void)hipGetLastError();
+      return set_error(VH_ERR_OOM, "hipMalloc(%zu) failed", nb);
+    }
   }
   std::lock_guard<std::mutex> lk(g_pool.mu);
   g_pool.live[p] = nb;
@@ -700,6 +728,9 @@ int vh_free(void* dptr) {
 }
 
 int vh_release_cache(void) {
+  VH_ENTRY();
+  // The device, not each stream: a stream seen earlier may have been destroyed.
+  VH_HIP_CHECK(hipDeviceSynchronize());
   {
     std::lock_guard<std::mutex> lk(g_pool.mu);
     for (auto& kv : g_pool.free_list) (void)hipFree(kv.second);
@@ -707,13 +738,11 @@ int vh_release_cache(void) {
     g_pool.cached = 0;
   }
   std::lock_guard<std::mutex> lk(g_ws_mu);
-  for (auto& kv : g_ws) {
-    if (kv.second.ptr) {
-      (void)hipStreamSynchronize(kv.first);
-      (void)hipFree(kv.second.ptr);
-    }
-  }
+  for (auto& kv : g_ws)
+    if (kv.second.ptr) (void)hipFree(kv.second.ptr);
   g_ws.clear();
+  for (void* p : g_ws_retired) (void)hipFree(p);
+  g_ws_retired.clear();
   return VH_OK;
 }
 

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "../../include/volta_hip.h"
 
@@ -167,6 +168,18 @@ inline int reduce_vec4_grid(long total, int lg_g) {
   const long qb = 256 >> lg_g;
   return (int)std::min<long>((total / 4 + qb - 1) / qb, 1L << 20);
 }
+
+// Raises a kernel's dynamic-LDS limit to the CU's 160 KB.  Each call site is
+// one template instantiation, so the flag is per kernel; std::call_once makes
+// concurrent first launches from several host threads safe.
+#define VH_LDS_LIMIT_ONCE(kern)                                                                        \
+  do {                                                                                                 \
+    static std::once_flag _vh_lds_once;                                                                \
+    std::call_once(_vh_lds_once, [&] {                                                                 \
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern),                                   \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);               \
+    });                                                                                                \
+  } while (0)
 
 // Record an error message for vh_last_error(); returns the status.
 int set_error(int status, const char* fmt, ...);

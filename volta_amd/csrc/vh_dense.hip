@@ -272,13 +272,8 @@ template <int BM, int BN, bool BIAS, bool PC = false>
 int launch_nt(const DenseArgs& a0, hipStream_t st) {
   using Cfg = DenseCfg<BM, BN>;
   auto kern = gemm_nt_bf16_kernel<BM, BN, BIAS, PC>;
-  static bool attr = false;
   const size_t lds = (size_t)2 * Cfg::STAGE * 16;
-  if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    attr = true;
-  }
+  VH_LDS_LIMIT_ONCE(kern);
   DenseArgs a = a0;
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;

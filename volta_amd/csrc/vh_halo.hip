@@ -736,14 +736,8 @@ template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
   auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
-    if (!FUSED)
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
-    attr_set = true;
-  }
+  // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
+  if (!FUSED) VH_LDS_LIMIT_ONCE(kern);
   HaloArgs g = a;
   g.tiles_m = (a.M + Cfg::BN - 1) / Cfg::BN;
   g.tiles_o = (a.O + Cfg::BM - 1) / Cfg::BM;

@@ -449,12 +449,7 @@ size_t pw_conv_bf16_wgrad_ws(int B, int C, int H, int W, int O, int S) {
 template <int IT>
 static int launch_pw_wgrad(const PwArgs& a, dim3 grid, hipStream_t st) {
   auto kern = pw_wgrad_s2_bf16_kernel<IT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    attr_set = true;
-  }
+  VH_LDS_LIMIT_ONCE(kern);
   kern<<<grid, 256, pw_wgrad_lds(a.Q), st>>>(a);
   VH_LAUNCH_CHECK();
   return VH_OK;

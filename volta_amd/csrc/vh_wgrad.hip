@@ -855,12 +855,7 @@ int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
 template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1, bool PC = false>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
   auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH, PC>;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              160 * 1024);
-    attr = true;
-  }
+  VH_LDS_LIMIT_ONCE(kern);
   dim3 grid((unsigned)(pl.tiles_o * pl.tiles_c * pl.splits));
   kern<<<grid, PC ? 512 : 256, pl.lds, st>>>(pl.a);
   VH_LAUNCH_CHECK();
