@@ -54,7 +54,7 @@ typedef enum {
   VH_ERR_OOM = 3,         /* device allocation failed: GpuBuffer::zeros -> None */
   VH_ERR_LAUNCH = 4,      /* HIP runtime / kernel launch error */
   VH_ERR_BAD_ARG = 5,     /* null pointer, bad enum value */
-  VH_ERR_UNSUPPORTED = 6, /* tensor too large for 32-bit indexing */
+  VH_ERR_UNSUPPORTED = 6, /* tensor too large for 32-bit indexing; scratch maximum exceeded */
   VH_ERR_CAPTURE = 7      /* the stream's workspace would have to grow while the stream is
                              being captured into a HIP graph (see Workspace below) */
 } vh_status;
@@ -259,6 +259,24 @@ int vh_conv2d_backward_relu(int dtype, int algo, const void* out_grad, const voi
                             int64_t batch, int64_t in_channels, int64_t out_channels, int64_t height,
                             int64_t width, int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
                             int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream);
+
+/* Allocation-free variant of vh_conv2d_backward (no counterpart in the reference):
+ * for callers that cannot allocate device memory -- code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc.  Same arguments, algorithms,
+ * kernels and results as vh_conv2d_backward; its workspace (re-laid-out weights,
+ * split-K partial sums, im2col matrices) is a static device array of
+ * VH_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first use on that GPU
+ * until the process ends.  The call never allocates or frees: a call that would
+ * need more workspace returns VH_ERR_UNSUPPORTED before anything is queued.  Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams, two threads, without ordering between them) race; order them. */
+#define VH_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int vh_conv2d_backward_noalloc(int dtype, int algo, const void* out_grad, const void* input,
+                               const void* weight, void* grad_input, void* grad_weight,
+                               void* grad_bias, int64_t batch, int64_t in_channels,
+                               int64_t out_channels, int64_t height, int64_t width,
+                               int64_t kernel_h, int64_t kernel_w, int64_t stride_h,
+                               int64_t stride_w, int64_t pad_h, int64_t pad_w, void* stream);
 
 /* ---- Glue of the config graphs (ReLU between layers, the sum loss, its seed) ---- */
 #define VH_UNARY_RELU 0

@@ -80,6 +80,7 @@ SIGNATURES = {
     "vh_pixel_shuffle_backward": [_INT, _P, _P] + [_I64] * 5 + [_P],
     "vh_conv2d_forward_relu": [_INT, _INT, _P, _P, _P, _P] + _LAYER11 + [ctypes.POINTER(_INT), _P],
     "vh_conv2d_backward_relu": [_INT, _INT, _P, _P, _P, _P, _P, _P] + _LAYER11 + [_P],
+    "vh_conv2d_backward_noalloc": [_INT, _INT, _P, _P, _P, _P, _P, _P] + _LAYER11 + [_P],
     "vh_unary": [_INT, _INT, _P, _P, _I64, _P],
     "vh_unary_backward": [_INT, _INT, _P, _P, _P, _I64, _P],
     "vh_sum_reduce": [_INT, _P, _I64, _P, _P],

@@ -38,6 +38,7 @@ static bool g_fast_paths = [] {
 // ------------------------------------------------------------------ device init
 static std::once_flag g_init_once;
 static int g_init_status = VH_ERR_NO_DEVICE;
+static int scratch_ptr(void** out);
 
 static int ensure_init() {
   std::call_once(g_init_once, [] {
@@ -48,6 +49,14 @@ static int ensure_init() {
     }
     g_init_status = VH_OK;
   });
+  if (g_init_status == VH_OK) {
+    // the static scratch of the current device (other devices: on their first no-alloc call)
+    static std::once_flag scratch_once;
+    std::call_once(scratch_once, [] {
+      void* p;
+      (void)scratch_ptr(&p);
+    });
+  }
   if (g_init_status != VH_OK) return set_error(g_init_status, "no HIP device available");
   return VH_OK;
 }
@@ -85,6 +94,11 @@ static std::mutex g_ws_mu;
 static std::unordered_map<hipStream_t, Ws> g_ws;
 static std::vector<void*> g_ws_retired;
 
+// Set by the allocation-free entry point for the duration of one call on the
+// calling thread: ws_get then serves every request from this fixed buffer.
+static thread_local void* t_ws_fixed = nullptr;
+static thread_local size_t t_ws_fixed_bytes = 0;
+
 // Growth rule of ws_get: the new size to allocate, or 0 when `have` suffices.
 static size_t ws_grow_to(size_t have, size_t need) {
   if (need <= have) return 0;
@@ -95,6 +109,13 @@ static size_t ws_grow_to(size_t have, size_t need) {
 static int ws_get(hipStream_t st, size_t bytes, void** out) {
   *out = nullptr;
   if (bytes == 0) return VH_OK;
+  if (t_ws_fixed) {
+    if (bytes > t_ws_fixed_bytes)
+      return set_error(VH_ERR_UNSUPPORTED, "call needs %zu bytes of scratch; the static scratch holds %zu", bytes,
+                       t_ws_fixed_bytes);
+    *out = t_ws_fixed;
+    return VH_OK;
+  }
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Ws& w = g_ws[st];
   const size_t nb = ws_grow_to(w.bytes, bytes);
@@ -130,6 +151,50 @@ struct Carve {
 };
 
 static inline char* at(void* base, size_t off) { return static_cast<char*>(base) + off; }
+
+// ------------------------------------------------------------------ static scratch
+// Device memory of the allocation-free entry point vh_conv2d_backward_noalloc:
+// a fixed array in the code object's zero-initialised data, one copy per GPU.
+// In host code `scratch` names a host-side stand-in, not device memory: its
+// device address comes from hipGetSymbolAddress, once per device with that
+// device current, and only that address is ever passed to kernels.
+static constexpr size_t kScratchBytes = VH_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static constexpr int kMaxDevices = 64;
+static std::once_flag g_scratch_once[kMaxDevices];
+static void* g_scratch_ptr[kMaxDevices];
+static hipError_t g_scratch_err[kMaxDevices];
+
+// Device address of the current device's scratch (set-up on first use per device).
+static int scratch_ptr(void** out) {
+  *out = nullptr;
+  int dev = 0;
+  VH_HIP_CHECK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(VH_ERR_UNSUPPORTED, "device %d beyond the scratch table", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev])
+    return set_error(VH_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(g_scratch_err[dev]));
+  *out = g_scratch_ptr[dev];
+  return VH_OK;
+}
+
+// Routes every workspace request of the calling thread to a fixed buffer for the
+// lifetime of the guard (ws_get never allocates while it is active).
+struct FixedWs {
+  FixedWs(void* p, size_t bytes) {
+    t_ws_fixed = p;
+    t_ws_fixed_bytes = bytes;
+  }
+  ~FixedWs() {
+    t_ws_fixed = nullptr;
+    t_ws_fixed_bytes = 0;
+  }
+};
 
 // ------------------------------------------------------------------ validation
 static constexpr long kMaxElems = (1L << 31) - 1;
@@ -263,8 +328,10 @@ struct DgradPhase {
   int a, b, Hc, Wc, kh0, kw0, Rc, Sc, offa, offb;
 };
 
+// need != nullptr: sizing mode -- stores the workspace bytes the call would
+// request and returns without launching anything (same for the passes below).
 static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias, void* dx, const ConvDims& d,
-                        hipStream_t st, const void* mask = nullptr) {
+                        hipStream_t st, const void* mask = nullptr, size_t* need = nullptr) {
   const int SH = (int)d.SH, SW = (int)d.SW;
   std::vector<DgradPhase> ph;
   PhaseTable tab{};
@@ -302,6 +369,10 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
     }
   Carve cv;
   const size_t o_w = cv.take(std::max<size_t>(wtot, 16)), o_g = cv.take(gmax);
+  if (need) {
+    *need = cv.off;
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   VH_TRY(VH_DISPATCH(dt, run_relayout_phase, w, at(ws, o_w), (int)d.O, (int)d.C, (int)d.KH, (int)d.KW, SH, SW, tab,
@@ -349,7 +420,7 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
 // mask: the layer input, when it came from a ReLU: dx is zeroed where it is not
 // positive (the ReLU backward of the layer below, fused where the kernel has it).
 static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const ConvDims& d, hipStream_t st,
-                       const void* mask = nullptr) {
+                       const void* mask = nullptr, size_t* need = nullptr) {
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
   const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
@@ -370,6 +441,14 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   size_t ws_gemm = igemm_prepare(p);
   Carve cv;
   size_t o_w = cv.take(wbytes), o_g = cv.take(ws_gemm);
+  if (need) {
+    // the larger of this pass's request and the stride-phase path's
+    size_t n = cv.off, np = 0;
+    if ((d.SH > 1 || d.SW > 1) && g_fast_paths && dgrad_phases(dt, dy, w, nullptr, dx, d, st, mask, &np) == VH_OK)
+      n = std::max(n, np);
+    *need = n;
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wd = at(ws, o_w);
@@ -403,16 +482,18 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
 // split-K over output positions: rows = O (A = dY), columns = (kh, kw, c)
 // (B = gather of x), stored OIHW.
 static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db, bool* db_done,
-                       const ConvDims& d, hipStream_t st) {
+                       const ConvDims& d, hipStream_t st, size_t* need = nullptr) {
   if (db_done) *db_done = false;
+  size_t most = 0;  // sizing mode: the largest request of every path that may run
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
-    size_t need = wgrad_rows_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH, (int)d.KW,
-                                (int)d.PH, (int)d.PW, db != nullptr);
-    if (need) {
+    size_t nb = wgrad_rows_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH, (int)d.KW,
+                              (int)d.PH, (int)d.PW, db != nullptr);
+    most = std::max(most, nb);
+    if (nb && !need) {
       void* ws;
-      VH_TRY(ws_get(st, need, &ws));
+      VH_TRY(ws_get(st, nb, &ws));
       int r = wgrad_rows_bf16(dy, x, dw, db, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
-                              (int)d.KW, (int)d.PH, (int)d.PW, (float*)ws, need, st);
+                              (int)d.KW, (int)d.PH, (int)d.PW, (float*)ws, nb, st);
       if (r != VH_ERR_UNSUPPORTED) {
         if (r == VH_OK && db_done) *db_done = db != nullptr;
         return r;
@@ -420,12 +501,13 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
     }
   }
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths) {
-    size_t need = pw_conv_bf16_wgrad_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH);
-    if (need) {
+    size_t nb = pw_conv_bf16_wgrad_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH);
+    most = std::max(most, nb);
+    if (nb && !need) {
       void* ws;
-      VH_TRY(ws_get(st, need, &ws));
+      VH_TRY(ws_get(st, nb, &ws));
       int r = pw_conv_bf16_wgrad(dy, x, dw, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH,
-                                 (float*)ws, need, st);
+                                 (float*)ws, nb, st);
       if (r != VH_ERR_UNSUPPORTED) return r;
     }
   }
@@ -448,14 +530,23 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   p.args.b = Operand{x, 0, p.args.N, 0};
   p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
   size_t ws_gemm = igemm_prepare(p);
+  if (need) {
+    *need = std::max(most, ws_gemm);
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, ws_gemm, &ws));
   return run_igemm(p, (float*)ws, st);
 }
 
-static int bias_grad_nchw(int dt, const void* dy, void* db, long B, long C, long HW, hipStream_t st) {
+static int bias_grad_nchw(int dt, const void* dy, void* db, long B, long C, long HW, hipStream_t st,
+                          size_t* need = nullptr) {
   int ns;
   size_t bytes = channel_sum_ws((int)B, (int)C, (int)HW, &ns);
+  if (need) {
+    *need = bytes;
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, bytes, &ws));
   return VH_DISPATCH(dt, run_channel_sum, dy, (int)B, (int)C, (int)HW, db, (float*)ws, ns, st);
@@ -511,7 +602,7 @@ static int im2col_fwd(int dt, const void* x, const void* w, const void* bias, vo
 // (conv.rs:1242-1298) and the pad crop in one gather kernel; dW = dY_2d^T . col
 // (matmul.rs:563-574) over a re-materialised col.
 static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void* dx, void* dw,
-                      const ConvDims& d, hipStream_t st) {
+                      const ConvDims& d, hipStream_t st, size_t* need = nullptr) {
   const long HP = d.H + 2 * d.PH, WP = d.W + 2 * d.PW, CKK = d.C * d.KH * d.KW;
   const long M = d.B * d.HO * d.WO;
   VH_TRY(check_sizes({M * CKK, d.B * d.C * HP * WP}));
@@ -555,6 +646,10 @@ static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void
   size_t o_col = dw ? cv.take((size_t)M * CKK * es) : 0;
   size_t o_xp = (dw && padded) ? cv.take((size_t)d.B * d.C * HP * WP * es) : 0;
   size_t o_g = cv.take(ws_w);
+  if (need) {
+    *need = cv.off;
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   if (dx) {
@@ -580,10 +675,15 @@ static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void
   return VH_OK;
 }
 
-static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const ConvDims& d, hipStream_t st) {
+static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const ConvDims& d, hipStream_t st,
+                        size_t* need = nullptr) {
   ConvGeom g = geom_of(d);
   int slices, len;
   size_t bytes = VH_DISPATCH(dt, direct_wgrad_ws, g, &slices, &len);
+  if (need) {
+    *need = bytes;
+    return VH_OK;
+  }
   void* ws;
   VH_TRY(ws_get(st, bytes, &ws));
   return VH_DISPATCH(dt, run_direct_wgrad, dy, x, dw, g, (float*)ws, slices, len, st);
@@ -954,9 +1054,11 @@ int vh_conv2d_forward_relu(int dtype, int algo, const void* input, const void* w
                              width, kernel_h, kernel_w, stride_h, stride_w, pad_h, pad_w, algo_used, stream, 1);
 }
 
+// need != nullptr: sizing mode -- stores the largest workspace request of the
+// passes the call would run and launches nothing.
 static int conv2d_backward_impl(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
                                 void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS, void* stream,
-                                bool relu_input) {
+                                bool relu_input, size_t* need = nullptr) {
   VH_TRY(check_dtype(dtype));
   ConvDims d{batch, in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
              pad_h, pad_w, 0, 0};
@@ -967,6 +1069,26 @@ static int conv2d_backward_impl(int dtype, int algo, const void* out_grad, const
   if (!out_grad || (grad_input && !weight) || (grad_weight && !input) || (relu_input && grad_input && !input))
     return set_error(VH_ERR_BAD_ARG, "null pointer");
   const void* mask = relu_input && grad_input ? input : nullptr;
+  if (need) {
+    size_t most = 0, n = 0;
+    auto take = [&](int r) {
+      if (r == VH_OK) most = std::max(most, n);
+      n = 0;
+      return r;
+    };
+    if (algo == VH_ALGO_IM2COL) {
+      if (grad_input || grad_weight)
+        VH_TRY(take(im2col_bwd(dtype, out_grad, input, weight, grad_input, grad_weight, d, st, &n)));
+    } else if (algo == VH_ALGO_IGEMM) {
+      if (grad_input) VH_TRY(take(igemm_dgrad(dtype, out_grad, weight, grad_input, d, st, mask, &n)));
+      if (grad_weight) VH_TRY(take(igemm_wgrad(dtype, out_grad, input, grad_weight, grad_bias, nullptr, d, st, &n)));
+    } else if (grad_weight) {
+      VH_TRY(take(direct_wgrad(dtype, out_grad, input, grad_weight, d, st, &n)));
+    }
+    if (grad_bias) VH_TRY(take(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.O, d.HO * d.WO, st, &n)));
+    *need = most;
+    return VH_OK;
+  }
   if (algo == VH_ALGO_IM2COL) {
     if (grad_input || grad_weight) VH_TRY(im2col_bwd(dtype, out_grad, input, weight, grad_input, grad_weight, d, st));
     if (mask) VH_TRY(mask_after(dtype, mask, grad_input, d.B * d.C * d.H * d.W, st));
@@ -1001,6 +1123,27 @@ int vh_conv2d_backward_relu(int dtype, int algo, const void* out_grad, const voi
   return conv2d_backward_impl(dtype, algo, out_grad, input, weight, grad_input, grad_weight, grad_bias, batch,
                               in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
                               pad_h, pad_w, stream, true);
+}
+
+int vh_conv2d_backward_noalloc(int dtype, int algo, const void* out_grad, const void* input, const void* weight,
+                               void* grad_input, void* grad_weight, void* grad_bias, VH_LAYER_ARGS,
+                               void* stream) {
+  VH_ENTRY();
+  void* sp;
+  VH_TRY(scratch_ptr(&sp));
+  size_t need = 0;
+  VH_TRY(conv2d_backward_impl(dtype, algo, out_grad, input, weight, grad_input, grad_weight, grad_bias, batch,
+                              in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+                              pad_h, pad_w, stream, false, &need));
+  if (need > kScratchBytes)
+    return set_error(VH_ERR_UNSUPPORTED,
+                     "vh_conv2d_backward_noalloc: this call needs %zu bytes of scratch, above the static "
+                     "maximum of %zu bytes; use vh_conv2d_backward",
+                     need, kScratchBytes);
+  FixedWs guard(sp, kScratchBytes);
+  return conv2d_backward_impl(dtype, algo, out_grad, input, weight, grad_input, grad_weight, grad_bias, batch,
+                              in_channels, out_channels, height, width, kernel_h, kernel_w, stride_h, stride_w,
+                              pad_h, pad_w, stream, false);
 }
 
 static int convt_dims(ConvDims& d, long B, long CI, long CO, long H, long W, long KH, long KW, long SH, long SW,
