@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the Volta conv / matmul hot path on one MI355X.
 
-Default workload (the Conv2d fwd+bwd metric's
+Headline workload (the Conv2d fwd+bwd metric's
 config): ResNet-style 3x3 conv block, bf16 storage with fp32 accumulation,
 N=128, layers 64->64 @56x56, 128->128 @28x28, 256->256 @14x14 (3x3, stride 1,
 pad 1) and the 1x1 stride-2 projection 64->128 @56x56.  One step = forward,
@@ -12,12 +12,17 @@ Prints ONE JSON line (driver contract).  `value` is whole-job TFLOP/s of the
 step (algorithmic FLOPs 2*N*K*C*R*S*P*Q per pass) over K steps: forward of
 every layer, then input and weight gradients in reverse layer order (the order
 of a training step), each weight gradient on a second stream next to the
-input-gradient chain (--one-stream: all on one stream).  The same step captured in a HIP
-graph gives `graph_ms_per_step`; each pass alone gives `per_op_ms`.  `roofline` is for the
-dominant pass, timed with HIP events on the stream it runs on (graph of 10
-calls of that pass alone).
-`cpu_baseline` times the CPU oracle (a C restatement of Volta's
-single-threaded CPU loops) on a bounded sample and extrapolates.
+input-gradient chain (--one-stream: all on one stream).  The same step captured
+in a HIP graph gives `graph_ms_per_step`; each pass alone gives `per_op_ms`.
+`roofline` is for the dominant pass, timed with HIP events on the stream it
+runs on (graph of 10 calls of that pass alone).
+
+`configs` holds every BASELINE config at full size: its fwd+bwd step time,
+TFLOP/s, each pass alone (ms, TFLOP/s, GB/s of algorithmic bytes), the
+dominant pass's roofline and a CPU baseline.  `cpu_baseline` (and each
+config's) times the CPU oracle (a C restatement of Volta's single-threaded CPU
+loops) on one pinned core, on a bounded sample of each loop nest,
+extrapolated; `host` states the host's cores and CPU model.
 """
 from __future__ import annotations
 
@@ -83,11 +88,6 @@ def parse():
     ap.add_argument("--one-stream", action="store_true",
                     help="issue the whole step on one stream (default: each layer's weight gradient on a "
                          "second stream next to the input-gradient chain)")
-    ap.add_argument("--configs", action="store_true",
-                    help="instead of the headline line, time a fwd+bwd step of every BASELINE config "
-                         "(one JSON line each)")
-    ap.add_argument("--config-only", default=None,
-                    help="with --configs: only the config whose name starts with this (e.g. 'configs[4]')")
     ap.add_argument("--profile-op", default=None,
                     help="run only this pass (e.g. '3x3 256->256 @14 wgrad') --steps times, then a "
                          "256 MiB device copy, for rocprofv3 counter runs; prints nothing else")
@@ -206,12 +206,19 @@ def pass_fns(L):
     }
 
 
-def profile_op(torch, layers, name, reps):
+def profile_op(torch, vnn, dev, layers, name, reps):
     """Counter runs: the named pass `reps` times, then a plain copy of 256 MiB
-    (the calibration kernel: it reads and writes exactly 256 MiB)."""
-    layer, op = name.rsplit(" ", 1)
-    L = next(L for L in layers if L["name"] == layer)
-    fn = pass_fns(L)[op]
+    (the calibration kernel: it reads and writes exactly 256 MiB).  `name` is a
+    headline pass ('3x3 256->256 @14 wgrad') or 'configs[i]:<pass>' for a pass of
+    another config ('configs[4]:L1 64->64 k3 fwd')."""
+    if ":" in name:
+        cfg, pname = name.split(":", 1)
+        w = next(w for w in build_workloads(torch, vnn, dev, layers) if w.name.startswith(cfg))
+        fn = w.passes[pname][0]
+    else:
+        layer, op = name.rsplit(" ", 1)
+        L = next(L for L in layers if L["name"] == layer)
+        fn = pass_fns(L)[op]
     for _ in range(reps):
         fn()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
@@ -221,154 +228,363 @@ def profile_op(torch, layers, name, reps):
     torch.cuda.synchronize()
 
 
-def config_steps(torch, vnn, dev, steps, warmup, only=None):
-    """Fwd+bwd step of each BASELINE config (synthetic inputs of the config's
-    shapes, the library's MI355X algorithm choice), one JSON line per config.
-    configs[0] and configs[4] run their whole graphs: convolutions with ReLU
-    between them, the sum loss, its seeded gradient (dY = 1) and the backward
-    chain; configs[3] runs each ConvTranspose2d layer's forward and backward."""
-    g = torch.Generator().manual_seed(3)
-    dts = {"f32": torch.float32, "bf16": torch.bfloat16}
-
-    def chain(dt, N, H, specs, tail=None):
-        """conv -> ReLU -> ... -> conv layers in sequence; specs = (C, O, K, S, P) per
-        layer.  Each ReLU is fused into the producing conv's epilogue
-        (vh_conv2d_forward_relu) and its backward into the next layer's input
-        gradient (vh_conv2d_backward_relu).  Returns run() and the step's
-        algorithmic FLOPs (the first layer has no dX)."""
-        convs, acts = [], []
-        if dt == "bf16" and H == 256:  # configs[4] input ~U[0,1)
-            x = torch.rand((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
-        else:
-            x = torch.randn((N, specs[0][0], H, H), generator=g).to(dev, dts[dt])
-        acts.append(x)
-        fl = 0.0
-        h = H
-        for li, (C, O, K, S, P) in enumerate(specs):
-            conv = vnn.Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dts[dt], generator=g)
-            ho = conv_out(h, K, S, P)
-            convs.append(conv)
-            acts.append(torch.empty((N, O, ho, ho), device=dev, dtype=dts[dt]))  # relu(y), or y for the last
-            fl += (2 if li == 0 else 3) * 2.0 * N * O * C * K * K * ho * ho
-            h = ho
-        grads = [torch.empty_like(a) for a in acts]  # grads[i]: gradient w.r.t. acts[i] (pre-ReLU for i > 0)
-        wouts = [(torch.empty_like(c.weight), torch.empty_like(c.bias)) for c in convs]
-        loss = torch.empty((1,), device=dev, dtype=torch.float32)
-        tail_out = tail_dout = None
-        if tail is not None:
-            tail_out = torch.empty(tail[1], device=dev, dtype=dts[dt])
-            tail_dout = torch.empty_like(tail_out)
-        L = len(convs)
-
-        def run():
-            for li, conv in enumerate(convs):
-                conv.forward(acts[li], out=acts[li + 1], relu=li + 1 < L)
-            last = acts[L]
-            if tail is not None:
-                tail[0].forward(last, out=tail_out)
-                vnn.sum_loss(tail_out, out=loss)
-                vnn.sum_loss_backward(tail_out, 1.0, out=tail_dout)
-                tail[0].backward(tail_dout, out=grads[L])
-            else:
-                vnn.sum_loss(last, out=loss)
-                vnn.sum_loss_backward(last, 1.0, out=grads[L])
-            for li in range(L - 1, -1, -1):
-                dw, db = wouts[li]
-                # grads[li] for li > 0 is the gradient before the ReLU that produced acts[li]
-                convs[li].backward(grads[li + 1], acts[li], input_grad=li > 0, weight_grad=True,
-                                   outs=(grads[li] if li > 0 else None, dw, db), relu_input=li > 0)
-        return run, fl
-
-    def convt_layer(dt, N, CI, CO, H, K, S, P):
-        ct = vnn.ConvTranspose2d(CI, CO, K, S, P, device=dev, dtype=dts[dt], generator=g)
-        x = torch.randn((N, CI, H, H), generator=g).to(dev, dts[dt])
-        HO = (H - 1) * S + K - 2 * P
-        dy = torch.randn((N, CO, HO, HO), generator=g).to(dev, dts[dt])
-        y = torch.empty((N, CO, HO, HO), device=dev, dtype=dts[dt])
-        outs = (torch.empty_like(x), torch.empty_like(ct.weight), torch.empty_like(ct.bias))
-        fl = 3 * 2.0 * N * H * H * CI * CO * K * K
-
-        def run():
-            ct.forward(x, out=y)
-            ct.backward(dy, x, outs=outs)
-        return run, fl
-
-    ps = vnn.PixelShuffle(3)
-    cfgs = {
-        "configs[0] MNIST-CNN f32 N=64 (conv-ReLU-conv, sum loss)":
-            ("f32", [chain("f32", 64, 28, [(1, 32, 3, 1, 1), (32, 64, 3, 1, 1)])]),
-        "configs[3] DCGAN ConvTranspose2d f32 N=128": ("f32", [convt_layer("f32", 128, 100, 512, 1, 4, 1, 0),
-                                                               convt_layer("f32", 128, 512, 256, 4, 4, 2, 1),
-                                                               convt_layer("f32", 128, 256, 128, 8, 4, 2, 1),
-                                                               convt_layer("f32", 128, 128, 64, 16, 4, 2, 1),
-                                                               convt_layer("f32", 128, 64, 3, 32, 4, 2, 1)]),
-        "configs[4] super-resolution bf16 N=16 256x256 (conv/ReLU chain, PixelShuffle, sum loss)":
-            ("bf16", [chain("bf16", 16, 256, [(3, 64, 5, 1, 2), (64, 64, 3, 1, 1), (64, 32, 3, 1, 1),
-                                              (32, 27, 3, 1, 1)], tail=(ps, (16, 3, 768, 768)))]),
-    }
-    for name, (dt, layers) in cfgs.items():
-        if only and not name.startswith(only):
-            continue
-
-        def step(layers=layers):
-            for run, _ in layers:
-                run()
-        ms = time_eager_fn(torch, step, steps, warmup)
-        fl = sum(f for _, f in layers)
-        tf = fl / (ms * 1e-3) / 1e12
-        print(json.dumps({"config": name, "dtype": dt, "ms_per_step": round(ms, 4), "gflop_per_step": round(fl / 1e9, 3),
-                          "tflops": round(tf, 2), "pct_peak": round(100 * tf / PEAK_TFLOPS[dt], 2)}), flush=True)
-    if not only or "configs[1]".startswith(only):
-        print(json.dumps({"config": "configs[1] Linear / square products", **gemm_secondary(torch, vnn, dev)}),
-              flush=True)
+def conv_pass_work(N, C, O, H, W, K, S, P, es):
+    """Algorithmic FLOPs and bytes (|in| + |W| + |out| at storage size es) of
+    one conv pass (forward, input or weight gradient: the same three tensors)."""
+    HO, WO = conv_out(H, K, S, P), conv_out(W, K, S, P)
+    flops = 2.0 * N * O * C * K * K * HO * WO
+    byts = es * (N * C * H * W + O * C * K * K + N * O * HO * WO)
+    return flops, byts
 
 
-def gemm_secondary(torch, vnn, dev, reps=5):
-    """Linear 4096x1024 -> 4096 fwd + dX + dW (+ bias) in f32 and bf16, and the
-    8192^3 bf16 product; reported beside the headline (same HIP-event timing)."""
+def roofline_of(flops, byts, ms, dt):
+    """Roofline entry of one pass: MFMA-bound when its intensity is at or above
+    the dtype's ridge (peak FLOP/s / 8 TB/s), else HBM-bound."""
+    peak = PEAK_TFLOPS[dt]
+    ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
+    if byts and flops / byts < ridge:
+        ach = byts / (ms * 1e-3) / 1e9
+        return dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM_GBS, unit="GB/s", frac=round(ach / PEAK_HBM_GBS, 4))
+    ach = flops / (ms * 1e-3) / 1e12
+    return dict(bound="mfma", achieved=round(ach, 2), peak=peak, unit="TFLOP/s", frac=round(ach / peak, 4))
+
+
+class Workload:
+    """One BASELINE config at its full size: `step` (one fwd+bwd step), the
+    passes it is made of (name -> (fn, flops, bytes)), its dtype and the CPU
+    baseline function (seconds per step of Volta's CPU path, extrapolated)."""
+
+    def __init__(self, name, dt, step, passes, cpu, note=""):
+        self.name, self.dt, self.step, self.passes, self.cpu, self.note = name, dt, step, passes, cpu, note
+
+
+def chain_passes(chain, es):
+    """(fn, flops, bytes) of every pass of a ConvChain (convs, tail, loss, seed)."""
+    fns = chain.passes()
     out = {}
-    g = torch.Generator().manual_seed(1)
-    for dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
-        lin = vnn.Linear(1024, 4096, device=dev, dtype=dt, generator=g)
-        x = torch.randn((4096, 1024), generator=g).to(dev, dt)
-        dy = torch.randn((4096, 4096), generator=g).to(dev, dt)
-        y = torch.empty((4096, 4096), device=dev, dtype=dt)
-        outs = (torch.empty_like(x), torch.empty_like(lin.weight), torch.empty_like(lin.bias))
-
-        def step():
-            lin.forward(x, out=y)
-            lin.backward(dy, x, outs=outs)
-        for _ in range(2):
-            step()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            step()
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / reps
-        fl = 3 * 2.0 * 4096 * 1024 * 4096
-        out[f"linear_4096x1024x4096_fwd_bwd_{name}_tflops"] = round(fl / ms / 1e9, 2)
-    import volta_amd
-    from volta_amd import ops
-    a = torch.randn((8192, 8192), generator=g).to(dev, torch.bfloat16)
-    b = torch.randn((8192, 8192), generator=g).to(dev, torch.bfloat16)
-    c = torch.empty_like(a)
-    st = torch.cuda.current_stream().cuda_stream
-    lib = volta_amd.lib()
-    for _ in range(2):
-        volta_amd.check(lib.vh_matmul(volta_amd.BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), 8192, 8192, 8192, st))
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
-        volta_amd.check(lib.vh_matmul(volta_amd.BF16, a.data_ptr(), b.data_ptr(), c.data_ptr(), 8192, 8192, 8192, st))
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / reps
-    out["matmul_8192cubed_bf16_tflops"] = round(2.0 * 8192 ** 3 / ms / 1e9, 2)
+    for i, conv in enumerate(chain.convs):
+        N, C, H, W = chain.acts[i].shape
+        O, _, K, _ = conv.weight.shape
+        fl, by = conv_pass_work(N, C, O, H, W, K, conv.stride[0], conv.padding[0], es)
+        for op in ("fwd", "dgrad", "wgrad"):
+            if f"L{i} {op}" in fns:
+                out[f"L{i} {C}->{O} k{K} {op}"] = (fns[f"L{i} {op}"], fl, by)
+    n_out = chain.output.numel()
+    if chain.tail is not None:
+        n_in = chain.acts[-1].numel()
+        out["PixelShuffle fwd"] = (fns["tail fwd"], 0.0, es * (n_in + n_out))
+        out["PixelShuffle bwd"] = (fns["tail bwd"], 0.0, es * (n_in + n_out))
+    out["sum loss"] = (fns["loss"], float(n_out), es * n_out)
+    out["loss seed"] = (fns["seed"], 0.0, es * n_out)
     return out
+
+
+def build_workloads(torch, vnn, dev, c3_layers):
+    """configs[0..4] (BASELINE.json order) as Workloads."""
+    g = torch.Generator().manual_seed(3)
+    wl = []
+    # configs[0]: MNIST-CNN f32, N=64: conv 1->32 3x3, ReLU, conv 32->64 3x3, sum loss
+    x0 = torch.randn((64, 1, 28, 28), generator=g).to(dev, torch.float32)
+    c0 = vnn.ConvChain([(1, 32, 3, 1, 1), (32, 64, 3, 1, 1)], x0, generator=g)
+    wl.append(Workload("configs[0] MNIST-CNN f32 N=64 (conv-ReLU-conv, sum loss)", "f32", c0.step,
+                       chain_passes(c0, 4), cpu_config0))
+    # configs[1]: Linear 4096x1024 -> 4096 (f32, bf16) and the 8192^3 bf16 product
+    for dt, tdt in (("f32", torch.float32), ("bf16", torch.bfloat16)):
+        es = 4 if dt == "f32" else 2
+        lin = vnn.Linear(1024, 4096, device=dev, dtype=tdt, generator=g)
+        x = torch.randn((4096, 1024), generator=g).to(dev, tdt)
+        dy = torch.randn((4096, 4096), generator=g).to(dev, tdt)
+        y = torch.empty((4096, 4096), device=dev, dtype=tdt)
+        outs = (torch.empty_like(x), torch.empty_like(lin.weight), torch.empty_like(lin.bias))
+        fl = 2.0 * 4096 * 1024 * 4096
+        by = es * (4096 * 1024 + 1024 * 4096 + 4096 * 4096)
+        passes = {
+            "fwd (+bias)": (lambda lin=lin, x=x, y=y: lin.forward(x, out=y), fl, by),
+            "dX": (lambda lin=lin, x=x, dy=dy, o=outs: lin.backward(dy, x, weight_grad=False,
+                                                                   outs=(o[0], None, None)), fl, by),
+            "dW (+db)": (lambda lin=lin, x=x, dy=dy, o=outs: lin.backward(dy, x, input_grad=False,
+                                                                         outs=(None, o[1], o[2])), fl, by),
+        }
+
+        def step(lin=lin, x=x, y=y, dy=dy, o=outs):
+            lin.forward(x, out=y)
+            lin.backward(dy, x, outs=o)
+        wl.append(Workload(f"configs[1] Linear 4096x1024->4096 fwd+bwd {dt}", dt, step, passes, cpu_config1_linear))
+    import volta_amd
+    lib = volta_amd.lib()
+    n = 8192
+    a = torch.randn((n, n), generator=g).to(dev, torch.bfloat16)
+    b = torch.randn((n, n), generator=g).to(dev, torch.bfloat16)
+    gr = torch.randn((n, n), generator=g).to(dev, torch.bfloat16)
+    c, da, db_ = torch.empty_like(a), torch.empty_like(a), torch.empty_like(a)
+    fl, by = 2.0 * n ** 3, 2.0 * 3 * n ** 2
+    cs = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    sq = {"C = A.B": (lambda: volta_amd.check(lib.vh_matmul(volta_amd.BF16, a.data_ptr(), b.data_ptr(),
+                                                             c.data_ptr(), n, n, n, cs())), fl, by),
+          "dA = G.B^T": (lambda: volta_amd.check(lib.vh_matmul_backward_a(volta_amd.BF16, gr.data_ptr(), b.data_ptr(),
+                                                                           da.data_ptr(), n, n, n, cs())), fl, by),
+          "dB = A^T.G": (lambda: volta_amd.check(lib.vh_matmul_backward_b(volta_amd.BF16, a.data_ptr(), gr.data_ptr(),
+                                                                           db_.data_ptr(), n, n, n, cs())), fl, by)}
+
+    def sq_step():
+        for fn, _, _ in sq.values():
+            fn()
+    wl.append(Workload("configs[1] square 8192^3 bf16 fwd+bwd (C, dA, dB)", "bf16", sq_step, sq, cpu_config1_square))
+    # configs[2]: the headline block (timed above; its passes are the headline's per_op_ms)
+    passes2 = {}
+    for L in c3_layers:
+        for op, fn in pass_fns(L).items():
+            passes2[f"{L['name']} {op}"] = (fn, L["flops"], L["bytes"])
+    wl.append(Workload("configs[2] ResNet-style 3x3 block bf16 N=128 (the headline)", "bf16", None, passes2,
+                       cpu_config2))
+    # configs[3]: DCGAN generator ConvTranspose2d f32, N=128
+    passes3 = {}
+    steps3 = []
+    for CI, CO, H, K, S, P in C4_LAYERS:
+        ct = vnn.ConvTranspose2d(CI, CO, K, S, P, device=dev, dtype=torch.float32, generator=g)
+        ct.weight = (torch.randn(ct.weight.shape, generator=g) * 0.02).to(dev)
+        x = torch.randn((C4_BATCH, CI, H, H), generator=g).to(dev)
+        HO = (H - 1) * S + K - 2 * P
+        dy = torch.randn((C4_BATCH, CO, HO, HO), generator=g).to(dev)
+        y = torch.empty((C4_BATCH, CO, HO, HO), device=dev)
+        outs = (torch.empty_like(x), torch.empty_like(ct.weight), torch.empty_like(ct.bias))
+        fl = 2.0 * C4_BATCH * H * H * CI * CO * K * K
+        by = 4.0 * (x.numel() + ct.weight.numel() + y.numel())
+        nm = f"{CI}->{CO} @{HO}"
+        passes3[f"{nm} fwd"] = (lambda ct=ct, x=x, y=y: ct.forward(x, out=y), fl, by)
+        passes3[f"{nm} dX"] = (lambda ct=ct, x=x, dy=dy, o=outs: ct.backward(dy, x, weight_grad=False,
+                                                                           outs=(o[0], None, None)), fl, by)
+        passes3[f"{nm} dW (+db)"] = (lambda ct=ct, x=x, dy=dy, o=outs: ct.backward(dy, x, input_grad=False,
+                                                                                 outs=(None, o[1], o[2])), fl, by)
+        steps3.append((ct, x, y, dy, outs))
+
+    def step3():
+        for ct, x, y, dy, o in steps3:
+            ct.forward(x, out=y)
+            ct.backward(dy, x, outs=o)
+    wl.append(Workload("configs[3] DCGAN ConvTranspose2d f32 N=128 (each layer fwd+bwd)", "f32", step3, passes3,
+                       cpu_config3))
+    # configs[4]: super-resolution bf16, N=16, 3x256x256 ~U[0,1): conv/ReLU chain, PixelShuffle r=3, sum loss
+    x4 = torch.rand((16, 3, 256, 256), generator=g).to(dev, torch.bfloat16)
+    c4 = vnn.ConvChain([(3, 64, 5, 1, 2), (64, 64, 3, 1, 1), (64, 32, 3, 1, 1), (32, 27, 3, 1, 1)], x4,
+                       tail=vnn.PixelShuffle(3), generator=g)
+    wl.append(Workload("configs[4] super-resolution bf16 N=16 256x256 (conv/ReLU chain, PixelShuffle, sum loss)",
+                       "bf16", c4.step, chain_passes(c4, 2), cpu_config4))
+    return wl
+
+
+def measure_workload(torch, w, steps, warmup, step_ms=None, pass_ms=None):
+    """Step time (HIP events around `steps` eager steps), per-pass times (each
+    pass alone, 10 calls in a HIP graph) and the dominant pass's roofline."""
+    if step_ms is None:
+        step_ms = time_eager_fn(torch, w.step, steps, warmup)
+    passes = {}
+    for name, (fn, fl, by) in w.passes.items():
+        ms = pass_ms[name] if pass_ms and name in pass_ms else time_op_graph(torch, fn, reps=10, replays=3)
+        passes[name] = dict(ms=round(ms, 4), tflops=round(fl / (ms * 1e-3) / 1e12, 2) if fl else 0.0,
+                            gbs=round(by / (ms * 1e-3) / 1e9, 1))
+    fl = sum(f for _, f, _ in w.passes.values() if f > 1e6)  # conv / GEMM FLOPs (not the loss adds)
+    dom = max(w.passes, key=lambda n: passes[n]["ms"])
+    _, dfl, dby = w.passes[dom]
+    roof = roofline_of(dfl, dby, passes[dom]["ms"], w.dt)
+    roof.update(kernel=dom, launch_ms=passes[dom]["ms"], algorithmic_bytes=dby)
+    tf = fl / (step_ms * 1e-3) / 1e12
+    return dict(dtype=w.dt, ms_per_step=round(step_ms, 4), gflop_per_step=round(fl / 1e9, 3), tflops=round(tf, 2),
+                pct_peak=round(100 * tf / PEAK_TFLOPS[w.dt], 2), roofline=roof,
+                sum_of_passes_ms=round(sum(p["ms"] for p in passes.values()), 4), passes=passes)
+
+
+C4_BATCH = 128
+# configs[3] layers: (CI, CO, H, K, stride, pad)
+C4_LAYERS = [(100, 512, 1, 4, 1, 0), (512, 256, 4, 4, 2, 1), (256, 128, 8, 4, 2, 1), (128, 64, 16, 4, 2, 1),
+             (64, 3, 32, 4, 2, 1)]
+CPU_NOTE = ("oracle/volta_oracle.c: a C restatement of Volta's single-threaded CPU loops (f32, -O2, FMA "
+            "contraction off; its GEMM is a plain-loop stand-in for matrixmultiply 0.3.10), 1 thread pinned to "
+            "one core")
+
+
+def _t(fn, *a, **k):
+    t0 = time.perf_counter()
+    fn(*a, **k)
+    return time.perf_counter() - t0
+
+
+def _dx_literal_per_iter(O, K, S, P, W, rows=8):
+    """Seconds per (input element x output position) iteration of Volta's literal
+    Direct input-gradient scan (conv.rs:450-515), timed on a `rows`-row strip of
+    one input channel of one image."""
+    import ctypes
+
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(1)
+    HO_s, WO = conv_out(rows, K, S, P), conv_out(W, K, S, P)
+    w = rng.standard_normal((O, 1, K, K)).astype(np.float32)
+    dy = rng.standard_normal((1, O, HO_s, WO)).astype(np.float32)
+    dx = np.empty((1, 1, rows, W), np.float32)
+    fp = ctypes.POINTER(ctypes.c_float)
+    t = _t(oracle.lib().or_direct_conv_backward_input_literal, dy.ctypes.data_as(fp), w.ctypes.data_as(fp),
+           dx.ctypes.data_as(fp), *map(ctypes.c_size_t, (1, 1, O, rows, W, K, K, S, S, P, P)))
+    return t / (rows * W * O * HO_s * WO), t
+
+
+def cpu_config0():
+    """configs[0] on Volta's CPU path (auto-select: conv1 Im2col, conv2 Direct,
+    conv.rs:55-68): everything in full except the Direct input-gradient scan of
+    conv2 (8.0e10 iterations), timed on a strip and extrapolated."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0)
+    N = 64
+    x = rng.standard_normal((N, 1, 28, 28)).astype(np.float32)
+    w1 = rng.uniform(-0.8165, 0.8165, (32, 1, 3, 3)).astype(np.float32)
+    w2 = rng.uniform(-0.1443, 0.1443, (64, 32, 3, 3)).astype(np.float32)
+    kw = dict(stride=(1, 1), pad=(1, 1))
+    t = 0.0
+    t0 = time.perf_counter()
+    h = oracle.relu(oracle.im2col_conv_forward(x, w1, **kw))
+    y = oracle.direct_conv(h, w2, **kw)
+    oracle.sum_all(y)
+    dy = oracle.sum_backward(1.0, y.shape)
+    oracle.direct_conv_backward_weight(dy, h, w2.shape, **kw)
+    dh = oracle.relu_backward(np.ones_like(h), h)
+    oracle.im2col_conv_backward(dh, x, w1, **kw)
+    t = time.perf_counter() - t0
+    per, ts = _dx_literal_per_iter(64, 3, 1, 1, 28)
+    tdx = per * N * 32 * 28 * 28 * 64 * 28 * 28
+    return t + tdx, t + ts, ("full graph except conv2's literal Direct dX scan, which is timed on an 8-row strip "
+                             "of 1 input channel of 1 image and extrapolated")
+
+
+_LINEAR_CPU = {}
+
+
+def cpu_config1_linear():
+    """configs[1] Linear 4096x1024 -> 4096 fwd + dX + dW + db (MatMulGradFn,
+    matmul.rs:450-460, 563-574; bias grad binary.rs:533-598) on 256 of the 4096
+    rows (every pass is linear in the rows), x16.  bf16 has no CPU arithmetic in
+    the reference (f32 math on bf16-rounded values): the same loops."""
+    if "v" not in _LINEAR_CPU:
+        import numpy as np
+
+        import oracle
+        rng = np.random.default_rng(0)
+        ms = 256
+        x = rng.standard_normal((ms, 1024)).astype(np.float32)
+        w = rng.uniform(-0.0765, 0.0765, (1024, 4096)).astype(np.float32)
+        b = np.zeros(4096, np.float32)
+        dy = rng.standard_normal((ms, 4096)).astype(np.float32)
+        t = _t(oracle.linear_forward, x, w, b) + _t(oracle.linear_backward, dy, x, w)
+        _LINEAR_CPU["v"] = (t * 4096 / ms, t)
+    tot, meas = _LINEAR_CPU["v"]
+    return tot, meas, "256 of 4096 rows of fwd, dX, dW and db, x16"
+
+
+def cpu_config1_square():
+    """configs[1] 8192^3: C = A.B, dA = G.B^T, dB = A^T.G (matmul.rs:450-460,
+    563-574, transposes materialised as the reference does) on 16 of the 8192
+    rows of A and G (each product is linear in them), x512."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0)
+    ms, n = 16, 8192
+    a = rng.standard_normal((ms, n)).astype(np.float32)
+    b = rng.standard_normal((n, n)).astype(np.float32)
+    g = rng.standard_normal((ms, n)).astype(np.float32)
+    t = _t(oracle.matmul, a, b) + _t(oracle.matmul_backward_a, g, b) + _t(oracle.matmul_backward_b, a, g)
+    return t * n / ms, t, "16 of 8192 rows of A and G for C, dA and dB, x512"
+
+
+def cpu_config3():
+    """configs[3] ConvTranspose2d layers (conv_transpose.rs:356-435 forward,
+    161-341 backward) on 4 of the 128 images (every loop is linear in the batch), x32."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0)
+    ns = 4
+    t = 0.0
+    for CI, CO, H, K, S, P in C4_LAYERS:
+        x = rng.standard_normal((ns, CI, H, H)).astype(np.float32)
+        w = rng.normal(0, 0.02, (CI, CO, K, K)).astype(np.float32)
+        b = np.zeros(CO, np.float32)
+        kw = dict(stride=(S, S), pad=(P, P))
+        t0 = time.perf_counter()
+        y = oracle.conv_transpose_forward(x, w, b, **kw)
+        oracle.conv_transpose_backward(np.ones_like(y), x, w, **kw)
+        t += time.perf_counter() - t0
+    return t * C4_BATCH / ns, t, f"{ns} of {C4_BATCH} images of every layer's forward and backward, x{C4_BATCH // ns}"
+
+
+def cpu_config4(rows=8):
+    """configs[4] on Volta's CPU path (auto-select: Direct for every layer,
+    conv.rs:55-57): each Direct forward and weight gradient on a `rows`-row strip
+    of one image, scaled per output position; the literal input-gradient scans on
+    a strip of one input channel (per-iteration cost x iteration count);
+    PixelShuffle, ReLU and the sum on one image, x16."""
+    import numpy as np
+
+    import oracle
+    rng = np.random.default_rng(0)
+    N, H = 16, 256
+    specs = [(3, 64, 5, 2), (64, 64, 3, 1), (64, 32, 3, 1), (32, 27, 3, 1)]
+    tot = meas = 0.0
+    for li, (C, O, K, P) in enumerate(specs):
+        kw = dict(stride=(1, 1), pad=(P, P))
+        x = rng.standard_normal((1, C, rows, H)).astype(np.float32)
+        w = rng.standard_normal((O, C, K, K)).astype(np.float32)
+        tf = _t(oracle.direct_conv, x, w, **kw)
+        dy = np.ones((1, O, conv_out(rows, K, 1, P), H), np.float32)
+        tw = _t(oracle.direct_conv_backward_weight, dy, x, w.shape, **kw)
+        per_pos = conv_out(rows, K, 1, P) * H
+        tot += (tf + tw) * N * H * H / per_pos
+        meas += tf + tw
+        if li > 0:
+            per, ts = _dx_literal_per_iter(O, K, 1, P, H)
+            tot += per * N * C * H * H * O * H * H
+            meas += ts
+    y = rng.standard_normal((1, 27, H, H)).astype(np.float32)
+    te = (_t(oracle.pixel_shuffle, y, 3) + _t(oracle.pixel_shuffle_backward, np.ones((1, 3, 3 * H, 3 * H),
+                                                                                          np.float32), 3)
+          + _t(oracle.sum_all, y) + 3 * (_t(oracle.relu, y) + _t(oracle.relu_backward, y, y)) * 64 / 27)
+    tot += te * N
+    meas += te
+    return tot, meas, (f"Direct fwd and dW of each layer on a {rows}-row strip of 1 image (per output position), "
+                       "literal dX scans on an 8-row strip of 1 input channel (per iteration), PixelShuffle / ReLU / "
+                       "sum on 1 image; extrapolated linearly")
+
+
+def cpu_config2():
+    r = cpu_baseline()
+    return r["seconds_per_step_extrapolated"], r["measured_s"], r["sample"]
+
+
+class pinned_one_core:
+    """Runs the CPU leg on one core of this process's affinity set (restored after)."""
+
+    def __enter__(self):
+        self.prev = os.sched_getaffinity(0)
+        self.core = min(self.prev)
+        os.sched_setaffinity(0, {self.core})
+        return self
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.prev)
+
+
+def host_info():
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(nproc=os.cpu_count(), affinity_cpus=len(os.sched_getaffinity(0)), cpu_model=model)
 
 
 def cpu_baseline(images=32, strip_rows=8):
@@ -424,7 +640,7 @@ def cpu_baseline(images=32, strip_rows=8):
                 sample=("oracle/volta_oracle.c (restated Volta CPU Direct loops, f32, 1 thread): fwd and dW on "
                         f"{images} of 128 images, literal dX scan on a {strip_rows}-row strip of 1 input channel of "
                         f"1 image; extrapolated linearly to the full step ({total_s:.3g} s estimated, {used:.1f} s measured)"),
-                seconds_per_step_extrapolated=total_s)
+                seconds_per_step_extrapolated=total_s, measured_s=used)
 
 
 def main():
@@ -444,15 +660,12 @@ def main():
     step_flops = 3.0 * sum(L["flops"] for L in layers)
 
     if args.profile_op:
-        profile_op(torch, layers, args.profile_op, args.steps)
-        return
-    if args.configs:
-        config_steps(torch, vnn, dev, args.steps, args.warmup, args.config_only)
+        profile_op(torch, vnn, dev, layers, args.profile_op, args.steps)
         return
 
     # headline: the training step (forward, then dX and dW in reverse layer
-    # order) issued eagerly on one stream, K steps between HIP events; the same
-    # step captured in one HIP graph is timed too (graph_ms_per_step)
+    # order) issued eagerly, K steps between HIP events; the same step captured
+    # in one HIP graph is timed too (graph_ms_per_step)
     train_step = make_train_step(torch, layers, None if args.one_stream else torch.cuda.Stream())
     graph_ms = time_graph_step(torch, train_step, args.steps, args.warmup)
     ms_per_step = time_eager_fn(torch, train_step, args.steps, args.warmup)
@@ -466,26 +679,47 @@ def main():
             ms = time_op_graph(torch, fn, reps=10, replays=max(2, args.steps // 4))
             ops.append(dict(layer=L["name"], op=k, ms=ms, flops=L["flops"], bytes=L["bytes"]))
     dom = max(ops, key=lambda o: o["ms"])
-    ai = dom["flops"] / dom["bytes"]
-    ridge = PEAK_TFLOPS["bf16"] * 1e12 / (PEAK_HBM_GBS * 1e9)
-    if ai >= ridge:
-        ach = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-        roof = dict(bound="mfma", achieved=round(ach, 2), peak=PEAK_TFLOPS["bf16"], unit="TFLOP/s",
-                    frac=round(ach / PEAK_TFLOPS["bf16"], 4), traffic=None)
-    else:
-        ach = dom["bytes"] / (dom["ms"] * 1e-3) / 1e9
-        roof = dict(bound="hbm", achieved=round(ach, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                    frac=round(ach / PEAK_HBM_GBS, 4), traffic=None)
+    roof = roofline_of(dom["flops"], dom["bytes"], dom["ms"], "bf16")
     roof["kernel"] = f"{dom['layer']} {dom['op']}"
     roof["traffic"] = MEASURED_TRAFFIC_BYTES.get(roof["kernel"])
     roof["algorithmic_bytes"] = dom["bytes"]
     roof["launch_ms"] = round(dom["ms"], 4)
 
-    secondary = gemm_secondary(torch, vnn, dev)
+    # every BASELINE config: step, per-pass times and rooflines (configs[2] = the headline's numbers)
+    configs = {}
+    works = build_workloads(torch, vnn, dev, layers)
+    for w in works:
+        if w.step is None:
+            r = measure_workload(torch, w, args.steps, args.warmup, step_ms=ms_per_step,
+                                 pass_ms={f"{o['layer']} {o['op']}": o["ms"] for o in ops})
+        else:
+            r = measure_workload(torch, w, args.steps, args.warmup)
+        configs[w.name] = r
+    torch.cuda.synchronize()
 
+    host = host_info()
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline()
+        # Volta's CPU path per config, one thread pinned to one core of this process
+        with pinned_one_core() as pin:
+            host["cpu_leg_core"] = pin.core
+            for w in works:
+                r = configs[w.name]
+                tot, meas, sample = w.cpu()
+                r["cpu_baseline"] = dict(value=round(r["gflop_per_step"] / tot / 1e3, 6), unit="TFLOP/s", cores=1,
+                                         kind="port", seconds_per_step=round(tot, 4),
+                                         measured_s=round(meas, 2), sample=sample)
+                r["speedup_vs_cpu"] = round(tot * 1e3 / r["ms_per_step"], 1)
+        c2 = next(configs[w.name]["cpu_baseline"] for w in works if w.name.startswith("configs[2]"))
+        cpu = dict(c2, sample=c2["sample"] + "; " + CPU_NOTE)
+
+    lin = {w.name: configs[w.name] for w in works if w.name.startswith("configs[1]")}
+    secondary = {
+        "linear_4096x1024x4096_fwd_bwd_f32_tflops": next(v["tflops"] for k, v in lin.items() if k.endswith("f32")),
+        "linear_4096x1024x4096_fwd_bwd_bf16_tflops": next(v["tflops"] for k, v in lin.items() if k.endswith("bf16")),
+        "matmul_8192cubed_bf16_tflops": next(v["passes"]["C = A.B"]["tflops"] for k, v in lin.items()
+                                             if "square" in k),
+    }
 
     out = {
         "metric": METRIC,
@@ -511,6 +745,8 @@ def main():
         "graph_ms_per_step": round(graph_ms, 4),
         "per_op_ms": {f"{o['layer']} {o['op']}": round(o["ms"], 4) for o in ops},
         "secondary": secondary,
+        "host": host,
+        "configs": configs,
     }
     print(json.dumps(out), flush=True)
 

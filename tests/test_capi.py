@@ -57,3 +57,16 @@ def test_pixel_shuffle_rejects_bad_channels():
         ps.forward(torch.empty(1, 10, 2, 2))
     with pytest.raises(ValueError):
         volta_amd.PixelShuffle(0)
+
+
+def test_size_mismatch_raises_before_any_launch():
+    # The C ABI carries no tensor sizes; the wrappers compare each tensor with its
+    # dimensions and raise VH_ERR_BAD_SHAPE first (checked here on host tensors).
+    with pytest.raises(volta_amd.VoltaHipError) as e:
+        ops.expect_numel(torch.empty(5), 6, "x")
+    assert e.value.status == _lib.VH_ERR_BAD_SHAPE
+    ops.expect_numel(torch.empty(2, 3), 6, "x")
+    ops.expect_numel(None, 6, "absent output")
+    sizes = ops._CONV_OPERANDS
+    assert set(sizes) == {"vh_direct_conv", "vh_igemm", "vh_conv_backward_input", "vh_igemm_backward_input",
+                          "vh_conv_backward_weight", "vh_igemm_backward_weight"}

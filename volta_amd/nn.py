@@ -18,8 +18,8 @@ from typing import Optional, Tuple
 import torch
 
 from . import _lib
-from ._lib import ALGO_AUTO, ALGO_DIRECT, ALGO_IGEMM, ALGO_IM2COL, check, lib
-from .ops import _same_dtype, ptr, stream_ptr
+from ._lib import ALGO_AUTO, ALGO_DIRECT, ALGO_IGEMM, ALGO_IM2COL, VoltaHipError, check, lib
+from .ops import _same_dtype, expect_numel, ptr, stream_ptr
 
 
 class ConvAlgo(enum.IntEnum):
@@ -79,6 +79,7 @@ class Conv2d:
         """relu=True: the layer followed by ReLU, fused (vh_conv2d_forward_relu)."""
         dt = _same_dtype(x, self.weight, self.bias)
         y = out if out is not None else torch.empty(self.output_shape(x), dtype=x.dtype, device=x.device)
+        expect_numel(y, math.prod(self.output_shape(x)), "Conv2d.forward out")
         used = ctypes.c_int(-1)
         fn = lib().vh_conv2d_forward_relu if relu else lib().vh_conv2d_forward
         check(fn(dt, int(self.algo), ptr(x), ptr(self.weight), ptr(self.bias), ptr(y), *self._dims(x),
@@ -105,6 +106,10 @@ class Conv2d:
             dx = torch.empty_like(x) if input_grad else None
             dw = torch.empty_like(self.weight) if weight_grad else None
             db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        expect_numel(out_grad, math.prod(self.output_shape(x)), "Conv2d.backward out_grad")
+        expect_numel(dx, x.numel(), "Conv2d.backward grad_input")
+        expect_numel(dw, self.weight.numel(), "Conv2d.backward grad_weight")
+        expect_numel(db, self.weight.shape[0], "Conv2d.backward grad_bias")
         fn = lib().vh_conv2d_backward_relu if relu_input else lib().vh_conv2d_backward
         check(fn(dt, int(algo), ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw), ptr(db), *self._dims(x),
                  stream_ptr(x.device)))
@@ -137,6 +142,7 @@ class ConvTranspose2d:
     def forward(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         dt = _same_dtype(x, self.weight, self.bias)
         y = out if out is not None else torch.empty(self.output_shape(x), dtype=x.dtype, device=x.device)
+        expect_numel(y, math.prod(self.output_shape(x)), "ConvTranspose2d.forward out")
         check(lib().vh_conv_transpose2d_forward(dt, ptr(x), ptr(self.weight), ptr(self.bias), ptr(y),
                                                 *self._dims(x), stream_ptr(x.device)))
         return y
@@ -151,6 +157,10 @@ class ConvTranspose2d:
             dx = torch.empty_like(x) if input_grad else None
             dw = torch.empty_like(self.weight) if weight_grad else None
             db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        expect_numel(out_grad, math.prod(self.output_shape(x)), "ConvTranspose2d.backward out_grad")
+        expect_numel(dx, x.numel(), "ConvTranspose2d.backward grad_input")
+        expect_numel(dw, self.weight.numel(), "ConvTranspose2d.backward grad_weight")
+        expect_numel(db, self.weight.shape[1], "ConvTranspose2d.backward grad_bias")
         check(lib().vh_conv_transpose2d_backward(dt, ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw),
                                                  ptr(db), *self._dims(x), stream_ptr(x.device)))
         return dx, dw, db
@@ -170,7 +180,11 @@ class Linear:
         dt = _same_dtype(x, self.weight, self.bias)
         m, i = x.shape
         o = self.weight.shape[1]
+        if i != self.weight.shape[0]:
+            raise VoltaHipError(_lib.VH_ERR_BAD_SHAPE, f"Linear: input has {i} features, weight expects "
+                                                       f"{self.weight.shape[0]}")
         y = out if out is not None else torch.empty((m, o), dtype=x.dtype, device=x.device)
+        expect_numel(y, m * o, "Linear.forward out")
         check(lib().vh_linear_forward(dt, ptr(x), ptr(self.weight), ptr(self.bias), ptr(y), m, i, o,
                                       stream_ptr(x.device)))
         return y
@@ -187,6 +201,13 @@ class Linear:
             dx = torch.empty_like(x) if input_grad else None
             dw = torch.empty_like(self.weight) if weight_grad else None
             db = torch.empty_like(self.bias) if (self.bias is not None and weight_grad) else None
+        if i != self.weight.shape[0]:
+            raise VoltaHipError(_lib.VH_ERR_BAD_SHAPE, f"Linear: input has {i} features, weight expects "
+                                                       f"{self.weight.shape[0]}")
+        expect_numel(out_grad, m * o, "Linear.backward out_grad")
+        expect_numel(dx, m * i, "Linear.backward grad_x")
+        expect_numel(dw, i * o, "Linear.backward grad_weight")
+        expect_numel(db, o, "Linear.backward grad_bias")
         check(lib().vh_linear_backward(dt, ptr(out_grad), ptr(x), ptr(self.weight), ptr(dx), ptr(dw), ptr(db),
                                        m, i, o, stream_ptr(x.device)))
         return dx, dw, db
@@ -256,3 +277,101 @@ def sum_loss_backward(y: torch.Tensor, grad: float = 1.0, out: Optional[torch.Te
     dy = out if out is not None else torch.empty_like(y)
     check(lib().vh_sum_backward(_same_dtype(y), float(grad), ptr(dy), y.numel(), stream_ptr(y.device)))
     return dy
+
+
+class ConvChain:
+    """The configs[0] / configs[4] graphs: a Sequential (sequential.rs) of
+    Conv2d -> ReLU -> ... -> Conv2d, an optional tail layer (PixelShuffle) and the
+    sum loss, with every activation and gradient buffer allocated once.
+
+    Each ReLU is fused into the convolution that produces its input
+    (vh_conv2d_forward_relu) and its backward into the next layer's input
+    gradient (vh_conv2d_backward_relu).  ``acts[i]`` is layer i's input
+    (``acts[0]`` the graph input, ``acts[i]`` = ReLU(conv_{i-1}) for 0 < i < L,
+    ``acts[L]`` the last conv's output); ``grads[i]`` is the gradient with
+    respect to conv_{i-1}'s output before its ReLU (``grads[L]`` w.r.t. the last
+    output).  The first layer computes no input gradient (the graph input needs
+    none)."""
+
+    def __init__(self, specs, x: torch.Tensor, tail=None, generator=None, algo: ConvAlgo = ConvAlgo.Auto):
+        """specs: (C, O, K, stride, pad) per conv layer; x: the graph input
+        [N, C0, H, W] (kept); tail: a layer with forward(x, out=) / backward(g, out=)."""
+        dev, dt = x.device, x.dtype
+        self.convs = []
+        self.acts = [x]
+        shape = tuple(x.shape)
+        for C, O, K, S, P in specs:
+            if shape[1] != C:
+                raise ValueError(f"ConvChain: layer expects {C} channels, gets {shape[1]}")
+            conv = Conv2d(C, O, K, S, P, use_bias=True, device=dev, dtype=dt, generator=generator)
+            conv.set_algo(algo)
+            shape = (shape[0], O, conv_out(shape[2], K, S, P), conv_out(shape[3], K, S, P))
+            self.convs.append(conv)
+            self.acts.append(torch.empty(shape, device=dev, dtype=dt))
+        self.grads = [None] + [torch.empty_like(a) for a in self.acts[1:]]
+        self.wgrads = [(torch.empty_like(c.weight), torch.empty_like(c.bias)) for c in self.convs]
+        self.tail = tail
+        self.tail_out = self.tail_grad = None
+        if tail is not None:
+            self.tail_out = tail.forward(self.acts[-1])
+            self.tail_grad = torch.empty_like(self.tail_out)
+        self.loss = torch.empty((1,), device=dev, dtype=torch.float32)
+
+    @property
+    def output(self) -> torch.Tensor:
+        return self.tail_out if self.tail is not None else self.acts[-1]
+
+    def forward(self) -> torch.Tensor:
+        """Forward of every layer and the loss; returns the one-element fp32 loss."""
+        L = len(self.convs)
+        for i, conv in enumerate(self.convs):
+            conv.forward(self.acts[i], out=self.acts[i + 1], relu=i + 1 < L)
+        if self.tail is not None:
+            self.tail.forward(self.acts[-1], out=self.tail_out)
+        return sum_loss(self.output, out=self.loss)
+
+    def backward(self, grad: float = 1.0) -> None:
+        """Seeds dLoss/dOutput = grad (the autograd seed for grad = 1) and runs the
+        backward chain: gradients land in ``grads`` and ``wgrads``."""
+        L = len(self.convs)
+        if self.tail is not None:
+            sum_loss_backward(self.tail_out, grad, out=self.tail_grad)
+            self.tail.backward(self.tail_grad, out=self.grads[L])
+        else:
+            sum_loss_backward(self.acts[-1], grad, out=self.grads[L])
+        for i in range(L - 1, -1, -1):
+            dw, db = self.wgrads[i]
+            self.convs[i].backward(self.grads[i + 1], self.acts[i], input_grad=i > 0, weight_grad=True,
+                                   outs=(self.grads[i] if i > 0 else None, dw, db), relu_input=i > 0)
+
+    def step(self) -> None:
+        """One fwd+bwd training step of the graph."""
+        self.forward()
+        self.backward()
+
+    def passes(self):
+        """name -> callable of each pass alone (forward, input gradient, weight
+        gradient of every layer, the tail, the loss and its seed), for timing."""
+        L = len(self.convs)
+        out = {}
+        for i, conv in enumerate(self.convs):
+            def fwd(i=i, conv=conv):
+                conv.forward(self.acts[i], out=self.acts[i + 1], relu=i + 1 < L)
+
+            def wgrad(i=i, conv=conv):
+                conv.backward(self.grads[i + 1], self.acts[i], input_grad=False, weight_grad=True,
+                              outs=(None,) + self.wgrads[i])
+            out[f"L{i} fwd"] = fwd
+            if i > 0:
+                def dgrad(i=i, conv=conv):
+                    conv.backward(self.grads[i + 1], self.acts[i], input_grad=True, weight_grad=False,
+                                  outs=(self.grads[i], None, None), relu_input=True)
+                out[f"L{i} dgrad"] = dgrad
+            out[f"L{i} wgrad"] = wgrad
+        if self.tail is not None:
+            out["tail fwd"] = lambda: self.tail.forward(self.acts[-1], out=self.tail_out)
+            out["tail bwd"] = lambda: self.tail.backward(self.tail_grad, out=self.grads[L])
+        out["loss"] = lambda: sum_loss(self.output, out=self.loss)
+        out["seed"] = lambda: sum_loss_backward(self.output, 1.0,
+                                                out=self.tail_grad if self.tail is not None else self.grads[L])
+        return out

@@ -57,6 +57,16 @@ def _call(name: str, *args) -> None:
     check(getattr(lib(), name)(*args))
 
 
+def expect_numel(t: Optional[torch.Tensor], n: int, what: str) -> None:
+    """The C ABI carries no tensor sizes: a tensor smaller than its dimensions
+    say would be read or written out of bounds.  Raises VH_ERR_BAD_SHAPE (the
+    reference's assert_eq! panic, kernels.rs:1129-1130) before any launch.  An
+    empty problem (n == 0, e.g. batch 0) touches no memory and is not checked."""
+    if t is not None and n > 0 and t.numel() != n:
+        raise VoltaHipError(_lib.VH_ERR_BAD_SHAPE,
+                            f"{what}: tensor holds {t.numel()} elements, the dimensions give {n}")
+
+
 def _optional(fn):
     """Reference semantics: Option::None when the device path is unavailable."""
 
@@ -81,6 +91,8 @@ def _optional(fn):
 def gpu_matmul(a: torch.Tensor, b: torch.Tensor, m: int, k: int, n: int):
     """gpu_ops.rs:151 -- c[m,n] = a[m,k] . b[k,n]."""
     dt = _same_dtype(a, b)
+    expect_numel(a, m * k, "gpu_matmul a")
+    expect_numel(b, k * n, "gpu_matmul b")
     c = torch.empty((m, n), dtype=a.dtype, device=a.device)
     _call("vh_matmul", dt, ptr(a), ptr(b), ptr(c), m, k, n, stream_ptr(a.device))
     return c
@@ -90,6 +102,8 @@ def gpu_matmul(a: torch.Tensor, b: torch.Tensor, m: int, k: int, n: int):
 def gpu_matmul_backward_a(grad: torch.Tensor, b: torch.Tensor, m: int, k: int, n: int):
     """gpu_ops.rs:408 -- grad_a[m,k] = grad[m,n] . b[k,n]^T."""
     dt = _same_dtype(grad, b)
+    expect_numel(grad, m * n, "gpu_matmul_backward_a grad")
+    expect_numel(b, k * n, "gpu_matmul_backward_a b")
     out = torch.empty((m, k), dtype=grad.dtype, device=grad.device)
     _call("vh_matmul_backward_a", dt, ptr(grad), ptr(b), ptr(out), m, k, n, stream_ptr(grad.device))
     return out
@@ -99,6 +113,8 @@ def gpu_matmul_backward_a(grad: torch.Tensor, b: torch.Tensor, m: int, k: int, n
 def gpu_matmul_backward_b(a: torch.Tensor, grad: torch.Tensor, m: int, k: int, n: int):
     """gpu_ops.rs:430 -- grad_b[k,n] = a[m,k]^T . grad[m,n]."""
     dt = _same_dtype(a, grad)
+    expect_numel(a, m * k, "gpu_matmul_backward_b a")
+    expect_numel(grad, m * n, "gpu_matmul_backward_b grad")
     out = torch.empty((k, n), dtype=a.dtype, device=a.device)
     _call("vh_matmul_backward_b", dt, ptr(a), ptr(grad), ptr(out), m, k, n, stream_ptr(a.device))
     return out
@@ -109,6 +125,7 @@ def gpu_matmul_backward_b(a: torch.Tensor, grad: torch.Tensor, m: int, k: int, n
 def gpu_im2col(input, batch_size, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out, w_out):
     """gpu_ops.rs:515 -- (B,C,H,W) (already padded) -> (B*h_out*w_out, C*kh*kw)."""
     dt = dtype_code(input)
+    expect_numel(input, batch_size * channels * height * width, "gpu_im2col input")
     col = torch.empty((batch_size * h_out * w_out, channels * kernel_h * kernel_w), dtype=input.dtype,
                       device=input.device)
     _call("vh_im2col", dt, ptr(input), ptr(col), batch_size, channels, height, width, kernel_h, kernel_w,
@@ -120,6 +137,7 @@ def gpu_im2col(input, batch_size, channels, height, width, kernel_h, kernel_w, s
 def gpu_col2im(col, batch_size, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out, w_out):
     """gpu_ops.rs:546 -- adjoint of gpu_im2col."""
     dt = dtype_code(col)
+    expect_numel(col, batch_size * h_out * w_out * channels * kernel_h * kernel_w, "gpu_col2im col")
     out = torch.empty((batch_size, channels, height, width), dtype=col.dtype, device=col.device)
     _call("vh_col2im", dt, ptr(col), ptr(out), batch_size, channels, height, width, kernel_h, kernel_w,
           stride_h, stride_w, h_out, w_out, stream_ptr(col.device))
@@ -127,8 +145,18 @@ def gpu_col2im(col, batch_size, channels, height, width, kernel_h, kernel_w, str
 
 
 # ---------------------------------------------------------------- conv kernels
+_CONV_OPERANDS = {  # which tensors each conv entry takes: x (input), w (weight), y (out_grad)
+    "vh_direct_conv": "xw", "vh_igemm": "xw", "vh_conv_backward_input": "yw", "vh_igemm_backward_input": "yw",
+    "vh_conv_backward_weight": "yx", "vh_igemm_backward_weight": "yx"}
+
+
 def _conv_call(name, t0, t1, out_shape, dims):
     dt = _same_dtype(t0, t1)
+    B, C, O, H, W, KH, KW = dims[:7]
+    HO, WO = dims[11:13]
+    sizes = {"x": B * C * H * W, "w": O * C * KH * KW, "y": B * O * HO * WO}
+    for t, role in zip((t0, t1), _CONV_OPERANDS[name]):
+        expect_numel(t, sizes[role], f"{name} {dict(x='input', w='weight', y='out_grad')[role]}")
     out = torch.empty(out_shape, dtype=t0.dtype, device=t0.device)
     _call(name, dt, ptr(t0), ptr(t1), ptr(out), *dims, stream_ptr(t0.device))
     return out
