@@ -46,7 +46,8 @@ struct HaloArgs {
   // past Q are computed and dropped).  One strip (TW = Q) means whole rows.
   int TW, nstrips;
   int Hp;                // padded input rows: H + 2*ph
-  int Wp;                // LDS cells per ext row (even): >= TW + S - 1 + cs
+  int Wp;                // LDS cells per ext row (even): >= TW + S - 1 + cs, = TW mod 16 (or 8)
+                         // where the LDS budget allows (bank-conflict-free fragment reads)
   int cs;                // cell of input column strip*TW - pw (0, or 1 for strips
                          // with pw odd: cell 0 then sits on an even input column)
   int lcol0, lcell0;     // first loaded column pair: input column strip*TW + lcol0
@@ -326,6 +327,12 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int it = 0; it < Cfg::WITER; ++it) WSM(st)[w_loff[it]] = wreg[sI][it];
     }
+    // Each item is two adjacent cells (a column pair).  Consecutive lanes hold
+    // consecutive pairs, so storing every lane's first cell together would hit
+    // every other 16-byte cell (two-way bank conflicts); lanes whose bit 2
+    // differs from bit 3 store their second cell first, which makes each group
+    // of 8 (and of 16) lanes cover distinct banks.
+    const bool xsw = ((lane >> 2) ^ (lane >> 3)) & 1;
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       {
@@ -336,8 +343,8 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
         c1v.x = pack_hi(xr[0], xr[1]); c1v.y = pack_hi(xr[2], xr[3]);
         c1v.z = pack_hi(xr[4], xr[5]); c1v.w = pack_hi(xr[6], xr[7]);
         u32x4* base = XSM(st) + x_loff[it];
-        base[0] = c0v;
-        base[1] = c1v;
+        base[xsw ? 1 : 0] = xsw ? c1v : c0v;
+        base[xsw ? 0 : 1] = xsw ? c0v : c1v;
       }
     }
   };
@@ -877,6 +884,27 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     if (O > 64 && (!have || best.lds > 80 * 1024) && eval(TW, 2, c) && better(c)) { best = c; have = true; }
   }
   if (!have) return VH_ERR_UNSUPPORTED;
+  // Row pitch: the 32 lanes of a fragment read consecutive positions, i.e.
+  // consecutive 16-byte cells except at a row end, where the cell index jumps
+  // by Wp - TW.  With Wp = TW (mod 16) the jump keeps every group of 16 lanes
+  // on distinct banks (mod 8: groups of 8).  Take the widest alignment whose
+  // larger stage keeps every decision the base pitch led to (blocks per CU,
+  // fused form's static stage size).
+  {
+    const int WMb = best.WM, BMb = WMb * 64;
+    auto units = [&](int wp) { return BMb * (2 * R * S + 1) + 2 * best.rows_max * wp + 2; };
+    const bool two = best.lds <= 80 * 1024;
+    const bool fused_base = units(best.Wp) <= kFusedStageUnits;
+    for (int al : {16, 8}) {
+      const int wp = best.Wp + ((best.TW - best.Wp) % al + al) % al;
+      const size_t lds_wp = (size_t)a.stages * units(wp) * 16;
+      if (lds_wp > (two ? 80 * 1024 : 160 * 1024)) continue;
+      if (fused_base && units(wp) > kFusedStageUnits) continue;
+      best.Wp = wp;
+      best.lds = lds_wp;
+      break;
+    }
+  }
   const int WM = best.WM, rows_max = best.rows_max;
   a.TW = best.TW;
   a.nstrips = (Q + a.TW - 1) / a.TW;
@@ -889,7 +917,8 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.cs = whole ? 0 : (pw & 1);
   a.lcol0 = whole ? 0 : -pw - a.cs;
   a.lcell0 = whole ? pw : 0;
-  a.npairs = whole ? W / 2 : a.Wp / 2;
+  // strips load the cells their taps read (the pitch may leave unused cells past them)
+  a.npairs = whole ? W / 2 : ((a.TW + S - 1 + a.cs + 1) & ~1) / 2;
   a.fW2 = FastDiv((uint32_t)a.npairs);
   a.rows_max = rows_max;
   a.fRowsMax = FastDiv((uint32_t)rows_max);

@@ -61,7 +61,7 @@ struct WgradArgs {
   int steps_per_split;
   int V;               // elements per global load (8, 4 or 2): divides Q and W
   int cpr_dy, cpr_x;   // chunks of V elements per dY row / per x row
-  int dadv, cadv;      // 4V elements of a dY owner's run as (rows, columns), columns < RL
+  int dadv, cadv;      // TPO*V elements (an item's stride) of a dY owner's run as (rows, columns), < RL
   int xadv, xcadv;     // the same for x rows (columns < XL)
   int dy_bytes, x_bytes;  // buffer ranges (< 2^31)
   int tiles_o, tiles_c, splits;       // grid = tiles_o * tiles_c * splits blocks
@@ -126,17 +126,25 @@ __device__ __forceinline__ u32x4w window8(const u32x4w& c0, const u32x4w& c1, co
 // load and store into LDS (producers, threads 256-511 serving the item map of
 // threads 0-255).  Neither role holds the other's registers, so two waves fit
 // per SIMD and the loads run beside the MFMAs of the other role.
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH, bool PC = false>
+// KQ (K quarters; whole rows, producer / consumer form): the block tile is
+// 32 o x 32 c, and the four consumer waves share it, each taking every fourth
+// 16-position MFMA step of each K step; at the end the four accumulator sets
+// are summed in LDS in wave order and one partial tile is stored.  Against the
+// 64 x 64 tile that is a quarter of the split-K partial bytes for the same
+// number of blocks, for twice the operand rows staged per MFMA.
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH, bool PC = false, bool KQ = false>
 __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradArgs a) {
   static_assert(R == 3 && S == 3, "3x3 windows");
+  static_assert(!KQ || (PC && !SEG), "K quarters: whole rows, producer / consumer blocks");
   constexpr int RS = R * S;
-  constexpr int TO = 64, TC = 64;  // block tile (o, c)
+  constexpr int TO = KQ ? 32 : 64, TC = KQ ? 32 : 64;  // block tile (o, c)
+  constexpr int TPO = 256 / TO;                        // load threads per row owner
   using VT = typename VecT<V>::t;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   const bool producer = PC && threadIdx.x >= 256;
   const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
-  const int wo = (wave >> 1) * 32, wc = (wave & 1) * 32;
+  const int wo = KQ ? 0 : (wave >> 1) * 32, wc = KQ ? 0 : (wave & 1) * 32;
   // logical block -> (o tile, c tile, split): the tiles of one split (which
   // read the same dY / x rows) are consecutive, hence on one XCD's L2
   const int lb = xcd_block(a.tiles_o * a.tiles_c * a.splits);
@@ -160,14 +168,14 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     reinterpret_cast<u32x4w*>(smem)[i] = u32x4w{0u, 0u, 0u, 0u};
 
   const int PQ = a.P * a.Q, HW = a.H * a.W;
-  const int own = tid >> 2, sub = tid & 3;
+  const int own = tid / TPO, sub = tid % TPO;
   // dY owner o = own: chunk k = sub + 4*it -> (row g, column) ; x owner c = own likewise
   const bool dy_own_ok = o0 + own < a.O, x_own_ok = c0 + own < a.C;
   const int dy_base_g = dy_own_ok ? (o0 + own) * PQ * 2 : 0;  // bytes, plane of o at image 0
   const int x_base_g = x_own_ok ? (c0 + own) * HW * 2 : 0;
   const int dy_chunks = G * a.cpr_dy, x_chunks = XR * a.cpr_x;
-  // item it of this thread is chunk sub + 4*it of its owner: (row, column) start
-  // at (g0, col0) and advance by 4V elements per item (a.dadv rows + a.cadv
+  // item it of this thread is chunk sub + TPO*it of its owner: (row, column) start
+  // at (g0, col0) and advance by TPO*V elements per item (a.dadv rows + a.cadv
   // columns, with one carry); recomputed per step instead of kept in registers
   int dg0 = 0, dc0 = sub * V;
   while (dc0 >= a.RL) { dc0 -= a.RL; ++dg0; }
@@ -188,7 +196,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      d_lds[it] = sub + 4 * it < dy_chunks ? own * OS + 8 + g * DP + col : sink_el;
+      d_lds[it] = sub + TPO * it < dy_chunks ? own * OS + 8 + g * DP + col : sink_el;
       col += a.cadv;
       const int wrap = col >= a.RL;
       col -= wrap ? a.RL : 0;
@@ -198,7 +206,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      const bool ok = sub + 4 * it < x_chunks;
+      const bool ok = sub + TPO * it < x_chunks;
       x_lds[it] = ok ? dy_elems + own * CS + j * XP + col : sink_el;
       x_row[it] = ok && x_own_ok ? j : kSinkRow;
       col += a.xcadv;
@@ -225,14 +233,14 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
       const int dstep = (n * a.O * PQ + p0 * a.Q) * 2;  // scalar byte offset of the dY run
 #pragma unroll
       for (int it = 0; it < ND; ++it)
-        rdy[sI][it] = BufLoad<V>::ld(dyr, d_voff + it * 8 * V, dstep);
+        rdy[sI][it] = BufLoad<V>::ld(dyr, d_voff + it * 2 * TPO * V, dstep);
       // x run row j is input row p0 - ph + j; t = byte offset of the thread's first item
       const int rbase = p0 - a.ph;
       const int t = x_voff + (n * a.C * HW + rbase * a.W) * 2;
 #pragma unroll
       for (int it = 0; it < NX; ++it) {
         const bool ok = (unsigned)(x_row[it] + rbase) < (unsigned)a.H;
-        rx[sI][it] = BufLoad<V>::ld(xrr, ok ? t + it * 8 * V : (int)0x80000000u, 0);
+        rx[sI][it] = BufLoad<V>::ld(xrr, ok ? t + it * 2 * TPO * V : (int)0x80000000u, 0);
       }
       return;
     }
@@ -250,7 +258,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
       const int cg = SEG ? dc_org + col : col;  // a V-chunk is all inside [0, Q) or all outside
-      const bool ok = dy_own_ok && sub + 4 * it < dy_chunks && (!SEG || (cg >= 0 && cg < a.Q));
+      const bool ok = dy_own_ok && sub + TPO * it < dy_chunks && (!SEG || (cg >= 0 && cg < a.Q));
       rdy[sI][it] = BufLoad<V>::ld(dyr, ok ? dys + (g * a.Q + cg) * 2 : (int)0x80000000u, 0);
       col += a.cadv;
       const int wrap = col >= a.RL;
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
       const int cg = SEG ? v0s + col : col;
-      const bool ok = x_own_ok && sub + 4 * it < x_chunks && j >= jmin && j < jmax && (!SEG || cg < a.W);
+      const bool ok = x_own_ok && sub + TPO * it < x_chunks && j >= jmin && j < jmax && (!SEG || cg < a.W);
       rx[sI][it] = BufLoad<V>::ld(xrr, ok ? xso + (j * a.W + cg) * 2 : (int)0x80000000u, 0);
       col += a.xcadv;
       const int wrap = col >= a.XL;
@@ -288,7 +296,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     int g = dg0, col = dc0;
 #pragma unroll
     for (int it = 0; it < ND; ++it) {
-      uint16_t* dst = sub + 4 * it < dy_chunks ? d + g * DP + col : sink;
+      uint16_t* dst = sub + TPO * it < dy_chunks ? d + g * DP + col : sink;
       *reinterpret_cast<VT*>(dst) = rdy[sI][it];
       col += a.cadv;
       const int wrap = col >= a.RL;
@@ -299,7 +307,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     col = xc0;
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
-      uint16_t* dst = sub + 4 * it < x_chunks ? xs + j * XP + col : sink;
+      uint16_t* dst = sub + TPO * it < x_chunks ? xs + j * XP + col : sink;
       *reinterpret_cast<VT*>(dst) = rx[sI][it];
       col += a.xcadv;
       const int wrap = col >= a.XL;
@@ -370,6 +378,37 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
     // of step kk (the last prefetch re-reads the final step: harmless)
     const int nkk = nchunk >> 1;  // even number of chunks: nkk >= 1
     Frag fa, fb;
+    if constexpr (KQ) {
+      // this wave's MFMA steps kk = wave, wave + 4, ... < nkk: 64 positions
+      // apart, i.e. dg rows + dv columns with at most one carry
+      const int dg = 64 / XV, dv = 64 - dg * XV;
+      auto step4 = [&]() {
+        v0 += dv;
+        g += dg;
+        const int w1 = v0 >= XV;
+        v0 -= w1 ? XV : 0;
+        g += w1;
+      };
+      v0 += wave * 16;
+      while (v0 >= XV) {  // at most 48 / 8 iterations, once per stage
+        v0 -= XV;
+        ++g;
+      }
+      const int nmy = (nkk - wave + 3) >> 2;  // wave-uniform, >= 0
+      if (nmy > 0) {
+        load(fa);
+        int kk = 0;
+        for (; kk + 2 <= nmy; kk += 2) {
+          step4();
+          load(fb);
+          mma(fa);
+          if (kk + 2 < nmy) step4();
+          load(fa);
+          mma(fb);
+        }
+        if (kk < nmy) mma(fa);
+      }
+    } else {
     load(fa);
     int kk = 0;
     for (; kk + 2 <= nkk; kk += 2) {
@@ -385,12 +424,13 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
       mma(fb);
     }
     if (kk < nkk) mma(fa);
+    }
     if (do_bias) {
       // thread t sums quarter (t % 4) of the columns [8, 8 + BW) of every dY row
       // slot of o = t / 4: the step's own dY columns (past Q they hold zeros;
       // the halo columns of a segment belong to its neighbours)
       const uint16_t* drow = DYS(st) + own * OS + 8;
-      const int q4 = a.BW >> 2, beg = sub * q4;
+      const int q4 = a.BW / TPO, beg = sub * q4;
       for (int gg = 0; gg < G; ++gg)
         for (int k = beg; k < beg + q4; ++k) dbias += bf16_to_f32(drow[gg * DP + k]);
     }
@@ -424,13 +464,14 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
         if (DEPTH == 1 && ks + 3 < nsteps) gload(I0{}, step_b + ks + 3);
         __syncthreads();
       }
-      return;
-    }
-    zero_acc();
-    __syncthreads();
-    for (int ks = 0; ks < nsteps; ++ks) {
-      compute(ks & 1);
+      if constexpr (!KQ) return;  // KQ: the producers take part in the epilogue's barriers
+    } else {
+      zero_acc();
       __syncthreads();
+      for (int ks = 0; ks < nsteps; ++ks) {
+        compute(ks & 1);
+        __syncthreads();
+      }
     }
   } else if constexpr (DEPTH == 2) {
     // invariant at an even ks: LDS buffer 0 holds step ks, register set 1
@@ -494,10 +535,31 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
 #undef DYS
 #undef XS
 
-  // partial tile store in the accumulator layout (rows past O / columns past C
-  // included: the reduction skips them): lane l's elements 4j .. 4j+3 of tap t
-  // form one 16-byte unit; the 64 lanes of one (tap, j) write 1 KB contiguously.
-  {
+  if constexpr (KQ) {
+    // The four consumer waves hold partial sums of the same 32 x 32 x 9 tile.
+    // Each writes its accumulators to LDS ([wave][tap][j][lane][4] floats,
+    // 36 KB per wave; every stage has been read by now), then all 512 threads
+    // add the four copies in wave order, 16 bytes at a time, and store the
+    // block's partial tile in that same [tap][j][lane][4] layout.
+    float4* red = reinterpret_cast<float4*>(smem);
+    constexpr int Q4 = RS * 4 * 64;  // float4 units per wave copy
+    if (!producer) {
+#pragma unroll
+      for (int t = 0; t < RS; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          red[(wave * RS + t) * 256 + j * 64 + lane] =
+              float4{acc[t][4 * j], acc[t][4 * j + 1], acc[t][4 * j + 2], acc[t][4 * j + 3]};
+    }
+    __syncthreads();
+    float4* pb = reinterpret_cast<float4*>(a.part) + ((long)split * a.tiles_o * a.tiles_c + tile) * Q4;
+    for (int q = threadIdx.x; q < Q4; q += 512) {
+      const float4 u0 = red[q], u1 = red[Q4 + q], u2 = red[2 * Q4 + q], u3 = red[3 * Q4 + q];
+      pb[q] = float4{((u0.x + u1.x) + u2.x) + u3.x, ((u0.y + u1.y) + u2.y) + u3.y,
+                     ((u0.z + u1.z) + u2.z) + u3.z, ((u0.w + u1.w) + u2.w) + u3.w};
+    }
+    if (producer) return;
+  } else {
     float* pb = a.part + ((((long)split * a.tiles_o * a.tiles_c + tile) * 4 + wave) * RS) * 1024 + lane * 4;
 #pragma unroll
     for (int t = 0; t < RS; ++t)
@@ -511,10 +573,11 @@ __global__ __launch_bounds__(PC ? 512 : 256) void wgrad_rows_bf16_kernel(WgradAr
         *reinterpret_cast<float4*>(pb + (t * 4 + j) * 256) = u;
       }
   }
-  if (do_bias) {
+  if (do_bias && !producer) {
     // combine the 4 quarter sums of each o (adjacent lanes)
     dbias += __shfl_xor(dbias, 1, 64);
     dbias += __shfl_xor(dbias, 2, 64);
+    if constexpr (TPO == 8) dbias += __shfl_xor(dbias, 4, 64);
     const int o = o0 + own;
     if (sub == 0 && o < a.O) a.dbias_part[(long)split * a.O + o] = dbias;
   }
@@ -546,22 +609,31 @@ __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __r
 // this file): element i of a split is ((((tile * 4 + wave) * RS + tap) * 4 + j)
 // * 64 + lane) * 4 + k, i.e. dW[o][c][tap] with
 //   o = o-tile * 64 + (wave / 2) * 32 + 8 j + 4 (lane / 32) + k,
-//   c = c-tile * 64 + (wave % 2) * 32 + lane % 32   (tile = c-tile * tiles_o + o-tile).
+//   c = c-tile * 64 + (wave % 2) * 32 + lane % 32   (tile = c-tile * tiles_o + o-tile);
+// in the K-quarter form (kq) one 32 x 32 tile per block, no wave index:
+//   o = o-tile * 32 + 8 j + 4 (lane / 32) + k,  c = c-tile * 32 + lane % 32.
 __global__ __launch_bounds__(256) void wgrad_reduce_frag_bf16_kernel(const float* __restrict__ part, int splits,
                                                                      int RS, int tiles_o, int O, int C,
                                                                      uint16_t* __restrict__ dw,
                                                                      const float* __restrict__ bpart,
-                                                                     uint16_t* __restrict__ db, int nbw, long total) {
+                                                                     uint16_t* __restrict__ db, int nbw, long total,
+                                                                     int kq) {
   if ((int)blockIdx.x < nbw) {
     reduce_splits_block(part, splits, total, [&](long i, float s) {
       const int k = (int)(i & 3), lane = (int)((i >> 2) & 63), j = (int)((i >> 8) & 3);
       const long rest = i >> 10;
       const int tap = (int)(rest % RS);
       const long tw = rest / RS;
-      const int wave = (int)(tw & 3);
-      const long tile = tw >> 2;
-      const int o = (int)(tile % tiles_o) * 64 + (wave >> 1) * 32 + 8 * j + 4 * (lane >> 5) + k;
-      const int c = (int)(tile / tiles_o) * 64 + (wave & 1) * 32 + (lane & 31);
+      int o, c;
+      if (kq) {  // one 32 x 32 wave tile per block tile
+        o = (int)(tw % tiles_o) * 32 + 8 * j + 4 * (lane >> 5) + k;
+        c = (int)(tw / tiles_o) * 32 + (lane & 31);
+      } else {
+        const int wave = (int)(tw & 3);
+        const long tile = tw >> 2;
+        o = (int)(tile % tiles_o) * 64 + (wave >> 1) * 32 + 8 * j + 4 * (lane >> 5) + k;
+        c = (int)(tile / tiles_o) * 64 + (wave & 1) * 32 + (lane & 31);
+      }
       if (o < O && c < C) dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
     }, (int)blockIdx.x, nbw);
   } else {
@@ -730,10 +802,14 @@ struct WgradPlan {
   int splits, nd, nx;
   size_t lds;
   int tiles_o, tiles_c;
+  bool kq;  // 32 x 32 tiles, K quarters (partials: one wave tile per block)
 };
 
-bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, int ph, int pw) {
+// kq: whole rows only, 32 x 32 block tiles with the K quarters of the KQ form
+// (false when the rows need column segments).
+bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, int ph, int pw, bool kq = false) {
   WgradArgs& a = pl.a;
+  const int TT = kq ? 32 : 64, TPO = 256 / TT;
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0 || R != 3 || S != 3 || ph > 2 || pw > 2) return false;
   a.N = N; a.C = C; a.H = H; a.W = W; a.O = O; a.P = P; a.Q = Q; a.ph = ph; a.pw = pw;
@@ -770,8 +846,8 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
       if (((os / 8) & 1) == 0) os += 8;  // odd number of 16-byte units: conflict-free
       int cs = (g + R - 1) * xv;
       if (((cs / 8) & 1) == 0) cs += 8;
-      const size_t lds = 2 * ((size_t)(64 * os + 64 * cs) + 8) * 2;  // + a 16-byte sink per stage
-      const int nd = (g * (rl / a.V) + 3) / 4, nx = ((g + R - 1) * (xl / a.V) + 3) / 4;
+      const size_t lds = 2 * ((size_t)(TT * os + TT * cs) + 8) * 2;  // + a 16-byte sink per stage
+      const int nd = (g * (rl / a.V) + TPO - 1) / TPO, nx = ((g + R - 1) * (xl / a.V) + TPO - 1) / TPO;
       if (lds > 160 * 1024 || nd > 16 || nx > 16) continue;
       const double cost = double(g * rl + (g + R - 1) * xl) / double(g * xv);
       if (!whole && cost >= best) continue;
@@ -794,16 +870,22 @@ bool plan_wgrad(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, 
     }
   }
   if (a.G == 0) return false;
+  // K quarters: whole rows, and the MFMA steps of a K step (16 positions each)
+  // dealt evenly over the four waves (measured: 14 steps -> 4,4,3,3 was slower
+  // than the 64 x 64 form)
+  if (kq && (a.nseg != 1 || a.HL != 0 || (a.G * a.XV / 16) % 4 != 0)) return false;
+  if (kq) pl.lds = std::max<size_t>(pl.lds, (size_t)4 * R * S * 1024 * sizeof(float));  // the epilogue's sum
   a.cpr_dy = a.RL / a.V;
   a.cpr_x = a.XL / a.V;
-  a.dadv = 4 * a.V / a.RL;
-  a.cadv = 4 * a.V % a.RL;
-  a.xadv = 4 * a.V / a.XL;
-  a.xcadv = 4 * a.V % a.XL;
+  a.dadv = TPO * a.V / a.RL;
+  a.cadv = TPO * a.V % a.RL;
+  a.xadv = TPO * a.V / a.XL;
+  a.xcadv = TPO * a.V % a.XL;
   a.steps_per_img = P / a.G * a.nseg;
   a.total_steps = N * a.steps_per_img;
-  pl.tiles_o = (O + 63) / 64;
-  pl.tiles_c = (C + 63) / 64;
+  pl.kq = kq;
+  pl.tiles_o = (O + TT - 1) / TT;
+  pl.tiles_c = (C + TT - 1) / TT;
   const int tiles = pl.tiles_o * pl.tiles_c;
   // one wave of blocks over the 256 CUs (one block per CU: LDS-limited)
   int splits = std::max(1, std::min(a.total_steps, (256 + tiles - 1) / tiles));
@@ -852,9 +934,9 @@ int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
   return VH_OK;
 }
 
-template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1, bool PC = false>
+template <int R, int S, int PW, int V, int ND, int NX, bool SEG, int DEPTH = 1, bool PC = false, bool KQ = false>
 int launch_wgrad(const WgradPlan& pl, hipStream_t st) {
-  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH, PC>;
+  auto kern = wgrad_rows_bf16_kernel<R, S, PW, V, ND, NX, SEG, DEPTH, PC, KQ>;
   VH_LDS_LIMIT_ONCE(kern);
   dim3 grid((unsigned)(pl.tiles_o * pl.tiles_c * pl.splits));
   kern<<<grid, PC ? 512 : 256, pl.lds, st>>>(pl.a);
@@ -866,6 +948,16 @@ template <int PW, int V>
 int launch_v(const WgradPlan& pl, hipStream_t st) {
   const int n = std::max(pl.nd, pl.nx);
   const bool seg = pl.a.nseg > 1 || pl.a.HL != 0;
+  if (pl.kq) {  // whole rows, producer / consumer, K quarters
+    if constexpr (V == 8) {
+      if (pl.nd <= 8 && pl.nx <= 8) return launch_wgrad<3, 3, PW, V, 8, 8, false, 1, true, true>(pl, st);
+      if (pl.nd <= 12 && pl.nx <= 12) return launch_wgrad<3, 3, PW, V, 12, 12, false, 1, true, true>(pl, st);
+      if (pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 1, true, true>(pl, st);
+    } else {
+      if (pl.nd <= 16 && pl.nx <= 16) return launch_wgrad<3, 3, PW, V, 16, 16, false, 2, true, true>(pl, st);
+    }
+    return VH_ERR_UNSUPPORTED;
+  }
   // two register sets when they fit (16-byte items: at most 6 + 6; 4- and
   // 8-byte items of whole rows: 16 + 16)
   // producer / consumer blocks for whole rows and for the 16-byte-item segment
@@ -899,7 +991,7 @@ int launch_v(const WgradPlan& pl, hipStream_t st) {
 
 // partials of the row kernel: [split][tile][4 waves][tap][1024]
 size_t frag_part_bytes(const WgradPlan& pl, int RS) {
-  return (size_t)pl.splits * pl.tiles_o * pl.tiles_c * 4 * RS * 1024 * sizeof(float);
+  return (size_t)pl.splits * pl.tiles_o * pl.tiles_c * (pl.kq ? 1 : 4) * RS * 1024 * sizeof(float);
 }
 
 template <int PW>
@@ -908,6 +1000,24 @@ int launch_pw(const WgradPlan& pl, hipStream_t st) {
 }
 
 }  // namespace
+
+// The K-quarter form (a quarter of the partial bytes) where it computes fewer
+// padded rows / columns than 64 x 64 tiles (O or C not a multiple of 64), or
+// where a K step spans at least 4 output rows; else the 64 x 64 form.
+// Measured: with one output row per K step (256-wide rows) the K-quarter form
+// stages 3 input rows per output row and was slower than 64 x 64 segments.
+static bool plan_rows(WgradPlan& pl, int N, int C, int H, int W, int O, int R, int S, int ph, int pw) {
+  WgradPlan kq;
+  if (plan_wgrad(kq, N, C, H, W, O, R, S, ph, pw, true)) {
+    const long pad64 = (long)((O + 63) / 64 * 64) * ((C + 63) / 64 * 64);
+    const long pad32 = (long)((O + 31) / 32 * 32) * ((C + 31) / 32 * 32);
+    if (pad32 < pad64 || kq.a.G >= 4) {
+      pl = kq;
+      return true;
+    }
+  }
+  return plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw, false);
+}
 
 size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, int pw, bool bias) {
   SmallcArgs sa;
@@ -918,7 +1028,7 @@ size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, in
     return b;
   }
   WgradPlan pl;
-  if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return 0;
+  if (!plan_rows(pl, N, C, H, W, O, R, S, ph, pw)) return 0;
   size_t b = frag_part_bytes(pl, R * S);
   if (bias) b += (size_t)pl.splits * O * sizeof(float) + 256;
   return b;
@@ -946,7 +1056,7 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
     return VH_OK;
   }
   WgradPlan pl;
-  if (!plan_wgrad(pl, N, C, H, W, O, R, S, ph, pw)) return VH_ERR_UNSUPPORTED;
+  if (!plan_rows(pl, N, C, H, W, O, R, S, ph, pw)) return VH_ERR_UNSUPPORTED;
   {
     const long dyb = (long)N * O * pl.a.P * pl.a.Q * 2, xb = (long)N * C * H * W * 2;
     if (dyb >= (1L << 31) - 16 || xb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
@@ -963,7 +1073,7 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
   const long total = (long)(pbytes / sizeof(float) / pl.splits);
   const int nbw = reduce_splits_grid(total), nbb = db ? reduce_splits_grid(O) : 0;
   wgrad_reduce_frag_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, pl.splits, R * S, pl.tiles_o, O, C, (uint16_t*)dw,
-                                                           pl.a.dbias_part, (uint16_t*)db, nbw, total);
+                                                           pl.a.dbias_part, (uint16_t*)db, nbw, total, pl.kq ? 1 : 0);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
