@@ -170,6 +170,59 @@ int vh_igemm_backward_weight(int dtype, const void* out_grad, const void* input,
                              int64_t stride_w, int64_t pad_h, int64_t pad_w, int64_t h_out,
                              int64_t w_out, void* stream);
 
+/* ------------------------------------------------------------------ allocating forms */
+/* The reference's gpu_* functions return a newly allocated result buffer
+ * (GpuBuffer::zeros, src/gpu/kernels.rs:1133,1233,1333; wrapped as Storage::Gpu,
+ * src/ops/gpu_ops.rs:160-168).  Each *_alloc takes the output from the
+ * library's pool (release it with vh_free), runs the entry point above into it
+ * and returns it in *out (NULL on failure); same arguments otherwise. */
+int vh_matmul_alloc(int dtype, const void* a, const void* b, void** c, int64_t m, int64_t k,
+                    int64_t n, void* stream);                        /* gpu_ops.rs:151 */
+int vh_matmul_backward_a_alloc(int dtype, const void* grad, const void* b, void** grad_a,
+                               int64_t m, int64_t k, int64_t n, void* stream); /* gpu_ops.rs:408 */
+int vh_matmul_backward_b_alloc(int dtype, const void* a, const void* grad, void** grad_b,
+                               int64_t m, int64_t k, int64_t n, void* stream); /* gpu_ops.rs:430 */
+int vh_im2col_alloc(int dtype, const void* input, void** col, int64_t batch, int64_t channels,
+                    int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                    int64_t stride_h, int64_t stride_w, int64_t h_out, int64_t w_out,
+                    void* stream);                                    /* gpu_ops.rs:515 */
+int vh_col2im_alloc(int dtype, const void* col, void** output, int64_t batch, int64_t channels,
+                    int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                    int64_t stride_h, int64_t stride_w, int64_t h_out, int64_t w_out,
+                    void* stream);                                    /* gpu_ops.rs:546 */
+/* Conv forms: (t0, t1) are the two inputs of the out-parameter entry point in its
+ * order -- (input, weight), (out_grad, weight) or (out_grad, input). */
+int vh_direct_conv_alloc(int dtype, const void* t0, const void* t1, void** out, int64_t batch,
+                         int64_t in_channels, int64_t out_channels, int64_t height, int64_t width,
+                         int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                         int64_t pad_h, int64_t pad_w, int64_t h_out, int64_t w_out,
+                         void* stream);                               /* gpu_ops.rs:574 */
+int vh_igemm_alloc(int dtype, const void* t0, const void* t1, void** out, int64_t batch,
+                   int64_t in_channels, int64_t out_channels, int64_t height, int64_t width,
+                   int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                   int64_t pad_h, int64_t pad_w, int64_t h_out, int64_t w_out,
+                   void* stream);                                     /* gpu_ops.rs:622 */
+int vh_conv_backward_input_alloc(int dtype, const void* t0, const void* t1, void** out,
+                                 int64_t batch, int64_t in_channels, int64_t out_channels,
+                                 int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                                 int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                 int64_t h_out, int64_t w_out, void* stream); /* gpu_ops.rs:670 */
+int vh_igemm_backward_input_alloc(int dtype, const void* t0, const void* t1, void** out,
+                                  int64_t batch, int64_t in_channels, int64_t out_channels,
+                                  int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                  int64_t h_out, int64_t w_out, void* stream); /* gpu_ops.rs:766 */
+int vh_conv_backward_weight_alloc(int dtype, const void* t0, const void* t1, void** out,
+                                  int64_t batch, int64_t in_channels, int64_t out_channels,
+                                  int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                                  int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                  int64_t h_out, int64_t w_out, void* stream); /* gpu_ops.rs:718 */
+int vh_igemm_backward_weight_alloc(int dtype, const void* t0, const void* t1, void** out,
+                                   int64_t batch, int64_t in_channels, int64_t out_channels,
+                                   int64_t height, int64_t width, int64_t kernel_h, int64_t kernel_w,
+                                   int64_t stride_h, int64_t stride_w, int64_t pad_h, int64_t pad_w,
+                                   int64_t h_out, int64_t w_out, void* stream); /* gpu_ops.rs:814 */
+
 /* ------------------------------------------------------------------ layers */
 /* ConvAlgo::auto_select, conv.rs:29-69, verbatim rule (both branches); returns
  * the vh_conv_algo value, or -1 if height/width < kernel_size. */

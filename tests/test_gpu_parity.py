@@ -547,3 +547,66 @@ def test_size_mismatch_is_an_error_before_launch():
     conv = vnn.Conv2d(2, 3, 3, 1, 1, device=DEV)
     with pytest.raises(volta_amd.VoltaHipError):
         conv.backward(torch.zeros(1, 3, 4, 4, device=DEV), x)  # out_grad of the wrong size
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_allocating_forms_match_out_parameter_entries(dt):
+    """The *_alloc entries (the reference's gpu_* return a new buffer,
+    gpu_ops.rs:160-168) give the same bits as the out-parameter entries, in a
+    pool buffer the caller releases with vh_free."""
+    import ctypes
+    lib = volta_amd.lib()
+    code = volta_amd.F32 if dt == "f32" else volta_amd.BF16
+    st = torch.cuda.current_stream().cuda_stream
+    g = rng(17)
+
+    def alloc_call(name, shape, *args):
+        p = ctypes.c_void_p()
+        volta_amd.check(getattr(lib, name)(code, *args[:2], ctypes.byref(p), *args[2:], st))
+        torch.cuda.synchronize()
+        host_buf = np.empty(int(np.prod(shape)), np.uint16 if dt == "bf16" else np.float32)
+        volta_amd.check(lib.vh_download(host_buf.ctypes.data, p.value, host_buf.nbytes, st))
+        volta_amd.check(lib.vh_free(p.value))
+        t = torch.from_numpy(host_buf.view(np.int16) if dt == "bf16" else host_buf)
+        return (t.view(torch.bfloat16) if dt == "bf16" else t).reshape(shape)
+
+    m, k, n = 37, 24, 40
+    _, at = prep(g.standard_normal((m, k)), dt)
+    _, bt = prep(g.standard_normal((k, n)), dt)
+    _, grt = prep(g.standard_normal((m, n)), dt)
+    cases = [("vh_matmul_alloc", ops.gpu_matmul(at, bt, m, k, n), (at.data_ptr(), bt.data_ptr(), m, k, n)),
+             ("vh_matmul_backward_a_alloc", ops.gpu_matmul_backward_a(grt, bt, m, k, n),
+              (grt.data_ptr(), bt.data_ptr(), m, k, n)),
+             ("vh_matmul_backward_b_alloc", ops.gpu_matmul_backward_b(at, grt, m, k, n),
+              (at.data_ptr(), grt.data_ptr(), m, k, n))]
+    B, C, O, H, W, K, S, P = 2, 8, 16, 11, 9, 3, 2, 1
+    HO, WO = oracle.conv_out(H, K, S, P), oracle.conv_out(W, K, S, P)
+    _, xt = prep(g.standard_normal((B, C, H, W)), dt)
+    _, wt = prep(g.standard_normal((O, C, K, K)) * 0.2, dt)
+    _, dyt = prep(g.standard_normal((B, O, HO, WO)), dt)
+    dims = (B, C, O, H, W, K, K, S, S, P, P, HO, WO)
+    for name, fn, t0, t1 in (("vh_direct_conv", ops.gpu_direct_conv, xt, wt), ("vh_igemm", ops.gpu_igemm, xt, wt),
+                             ("vh_conv_backward_input", ops.gpu_conv_backward_input, dyt, wt),
+                             ("vh_igemm_backward_input", ops.gpu_igemm_backward_input, dyt, wt),
+                             ("vh_conv_backward_weight", ops.gpu_conv_backward_weight, dyt, xt),
+                             ("vh_igemm_backward_weight", ops.gpu_igemm_backward_weight, dyt, xt)):
+        cases.append((name + "_alloc", fn(t0, t1, *dims), (t0.data_ptr(), t1.data_ptr()) + dims))
+    xp = torch.from_numpy(oracle.pad(host(xt), P, P)).to(DEV, DTYPES[dt])
+    HP, WP = xp.shape[2:]
+    col = ops.gpu_im2col(xp, B, C, HP, WP, K, K, S, S, HO, WO)
+    cases.append(("vh_im2col_alloc", col, (xp.data_ptr(), None, B, C, HP, WP, K, K, S, S, HO, WO)))
+    back = ops.gpu_col2im(col, B, C, HP, WP, K, K, S, S, HO, WO)
+    cases.append(("vh_col2im_alloc", back, (col.data_ptr(), None, B, C, HP, WP, K, K, S, S, HO, WO)))
+    for name, ref, args in cases:
+        if args[1] is None:  # one input: (input, out, dims...)
+            p = ctypes.c_void_p()
+            volta_amd.check(getattr(lib, name)(code, args[0], ctypes.byref(p), *args[2:], st))
+            torch.cuda.synchronize()
+            host_buf = np.empty(ref.numel(), np.uint16 if dt == "bf16" else np.float32)
+            volta_amd.check(lib.vh_download(host_buf.ctypes.data, p.value, host_buf.nbytes, st))
+            volta_amd.check(lib.vh_free(p.value))
+            t = torch.from_numpy(host_buf.view(np.int16) if dt == "bf16" else host_buf)
+            got = (t.view(torch.bfloat16) if dt == "bf16" else t).reshape(ref.shape)
+        else:
+            got = alloc_call(name, tuple(ref.shape), *args)
+        assert torch.equal(got, ref.cpu()), f"{name} differs from the out-parameter entry"

@@ -42,6 +42,7 @@ _I64 = ctypes.c_int64
 _P = ctypes.c_void_p
 _INT = ctypes.c_int
 _SZ = ctypes.c_size_t
+_PP = ctypes.POINTER(ctypes.c_void_p)
 
 _CONV13 = [_I64] * 13
 _LAYER11 = [_I64] * 11
@@ -68,6 +69,17 @@ SIGNATURES = {
     "vh_conv_backward_weight": [_INT, _P, _P, _P] + _CONV13 + [_P],
     "vh_igemm_backward_input": [_INT, _P, _P, _P] + _CONV13 + [_P],
     "vh_igemm_backward_weight": [_INT, _P, _P, _P] + _CONV13 + [_P],
+    "vh_matmul_alloc": [_INT, _P, _P, _PP, _I64, _I64, _I64, _P],
+    "vh_matmul_backward_a_alloc": [_INT, _P, _P, _PP, _I64, _I64, _I64, _P],
+    "vh_matmul_backward_b_alloc": [_INT, _P, _P, _PP, _I64, _I64, _I64, _P],
+    "vh_im2col_alloc": [_INT, _P, _PP] + [_I64] * 10 + [_P],
+    "vh_col2im_alloc": [_INT, _P, _PP] + [_I64] * 10 + [_P],
+    "vh_direct_conv_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
+    "vh_igemm_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
+    "vh_conv_backward_input_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
+    "vh_igemm_backward_input_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
+    "vh_conv_backward_weight_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
+    "vh_igemm_backward_weight_alloc": [_INT, _P, _P, _PP] + _CONV13 + [_P],
     "vh_conv_algo_auto_select": [_I64] * 5 + [_INT],
     "vh_conv_algo_select_mi355x": [_I64] * 11,
     "vh_conv2d_forward": [_INT, _INT, _P, _P, _P, _P] + _LAYER11 + [ctypes.POINTER(_INT), _P],

@@ -1002,6 +1002,81 @@ int vh_conv_algo_select_mi355x(int64_t batch, int64_t in_channels, int64_t out_c
   return VH_ALGO_IGEMM;
 }
 
+// ------------------------------------------------------------------ allocating forms
+// The reference's gpu_* functions allocate their result (GpuBuffer::zeros,
+// kernels.rs:1133, 1233, 1333) and return it (gpu_ops.rs:160-168).  These take
+// the output buffer from the pool (vh_alloc: the caller releases it with
+// vh_free), run the out-parameter entry point into it, and return it in *out;
+// on failure nothing is returned and the buffer goes back to the pool.
+}  // extern "C"
+template <typename F>
+static int with_alloc(void** out, long elems, int dtype, F&& fn) {
+  if (!out) return set_error(VH_ERR_BAD_ARG, "null output pointer");
+  *out = nullptr;
+  VH_TRY(check_dtype(dtype));
+  if (elems < 0) return set_error(VH_ERR_BAD_SHAPE, "negative output size");
+  void* p = nullptr;
+  VH_TRY(vh_alloc((size_t)elems * elem_size(dtype), &p));
+  const int st = fn(p);
+  if (st != VH_OK) {
+    (void)vh_free(p);
+    return st;
+  }
+  *out = p;
+  return VH_OK;
+}
+extern "C" {
+
+int vh_matmul_alloc(int dtype, const void* a, const void* b, void** c, int64_t m, int64_t k, int64_t n,
+                    void* stream) {
+  return with_alloc(c, (long)m * n, dtype, [&](void* o) { return vh_matmul(dtype, a, b, o, m, k, n, stream); });
+}
+
+int vh_matmul_backward_a_alloc(int dtype, const void* grad, const void* b, void** grad_a, int64_t m, int64_t k,
+                               int64_t n, void* stream) {
+  return with_alloc(grad_a, (long)m * k, dtype,
+                    [&](void* o) { return vh_matmul_backward_a(dtype, grad, b, o, m, k, n, stream); });
+}
+
+int vh_matmul_backward_b_alloc(int dtype, const void* a, const void* grad, void** grad_b, int64_t m, int64_t k,
+                               int64_t n, void* stream) {
+  return with_alloc(grad_b, (long)k * n, dtype,
+                    [&](void* o) { return vh_matmul_backward_b(dtype, a, grad, o, m, k, n, stream); });
+}
+
+int vh_im2col_alloc(int dtype, const void* input, void** col, int64_t batch, int64_t channels, int64_t height,
+                    int64_t width, int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                    int64_t h_out, int64_t w_out, void* stream) {
+  return with_alloc(col, (long)batch * h_out * w_out * channels * kernel_h * kernel_w, dtype, [&](void* o) {
+    return vh_im2col(dtype, input, o, batch, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out,
+                     w_out, stream);
+  });
+}
+
+int vh_col2im_alloc(int dtype, const void* col, void** output, int64_t batch, int64_t channels, int64_t height,
+                    int64_t width, int64_t kernel_h, int64_t kernel_w, int64_t stride_h, int64_t stride_w,
+                    int64_t h_out, int64_t w_out, void* stream) {
+  return with_alloc(output, (long)batch * channels * height * width, dtype, [&](void* o) {
+    return vh_col2im(dtype, col, o, batch, channels, height, width, kernel_h, kernel_w, stride_h, stride_w, h_out,
+                     w_out, stream);
+  });
+}
+
+#define VH_CONV_ALLOC(NAME, ELEMS)                                                                             \
+  int NAME##_alloc(int dtype, const void* t0, const void* t1, void** out, VH_CONV_ARGS) {                      \
+    return with_alloc(out, (long)(ELEMS), dtype, [&](void* o) {                                                \
+      return NAME(dtype, t0, t1, o, batch, in_channels, out_channels, height, width, kernel_h, kernel_w,        \
+                  stride_h, stride_w, pad_h, pad_w, h_out, w_out, stream);                                      \
+    });                                                                                                        \
+  }
+VH_CONV_ALLOC(vh_direct_conv, batch * out_channels * h_out * w_out)
+VH_CONV_ALLOC(vh_igemm, batch * out_channels * h_out * w_out)
+VH_CONV_ALLOC(vh_conv_backward_input, batch * in_channels * height * width)
+VH_CONV_ALLOC(vh_igemm_backward_input, batch * in_channels * height * width)
+VH_CONV_ALLOC(vh_conv_backward_weight, out_channels * in_channels * kernel_h * kernel_w)
+VH_CONV_ALLOC(vh_igemm_backward_weight, out_channels * in_channels * kernel_h * kernel_w)
+#undef VH_CONV_ALLOC
+
 // ------------------------------------------------------------------ layers
 #define VH_LAYER_ARGS                                                                                      \
   int64_t batch, int64_t in_channels, int64_t out_channels, int64_t height, int64_t width, int64_t kernel_h, \
