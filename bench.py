@@ -89,8 +89,9 @@ def parse():
                     help="issue the whole step on one stream (default: each layer's weight gradient on a "
                          "second stream next to the input-gradient chain)")
     ap.add_argument("--profile-op", default=None,
-                    help="run only this pass (e.g. '3x3 256->256 @14 wgrad') --steps times, then a "
-                         "256 MiB device copy, for rocprofv3 counter runs; prints nothing else")
+                    help="run only these passes (e.g. '3x3 256->256 @14 wgrad', several separated by ';', "
+                         "or 'headline' for all twelve) --steps times each, then a 256 MiB device copy, for "
+                         "rocprofv3 counter runs; prints only the pass names")
     return ap.parse_args()
 
 
@@ -206,21 +207,37 @@ def pass_fns(L):
     }
 
 
-def profile_op(torch, vnn, dev, layers, name, reps):
-    """Counter runs: the named pass `reps` times, then a plain copy of 256 MiB
-    (the calibration kernel: it reads and writes exactly 256 MiB).  `name` is a
-    headline pass ('3x3 256->256 @14 wgrad') or 'configs[i]:<pass>' for a pass of
-    another config ('configs[4]:L1 64->64 k3 fwd')."""
-    if ":" in name:
-        cfg, pname = name.split(":", 1)
-        w = next(w for w in build_workloads(torch, vnn, dev, layers) if w.name.startswith(cfg))
-        fn = w.passes[pname][0]
-    else:
-        layer, op = name.rsplit(" ", 1)
-        L = next(L for L in layers if L["name"] == layer)
-        fn = pass_fns(L)[op]
-    for _ in range(reps):
-        fn()
+def profile_op(torch, vnn, dev, layers, names, reps):
+    """Counter runs: each named pass `reps` times, then a plain copy of 256 MiB
+    (the calibration kernel: it reads and writes exactly 256 MiB).  `names` is
+    one pass or several separated by ';': a headline pass ('3x3 256->256 @14
+    wgrad'), 'configs[i]:<pass>' for a pass of another config ('configs[4]:L1
+    64->64 k3 fwd'), or 'headline' for all twelve headline passes.  Before each
+    pass one `fill_` of a 4 KiB marker tensor is dispatched, so the dispatches
+    of a trace split into the passes in the order given (printed, one per line)."""
+    works = None
+    todo = []
+    for name in names.split(";"):
+        name = name.strip()
+        if name == "headline":
+            todo += [(f"{L['name']} {op}", fn) for L in layers for op, fn in pass_fns(L).items()]
+        elif ":" in name:
+            cfg, pname = name.split(":", 1)
+            works = works or build_workloads(torch, vnn, dev, layers)
+            w = next(w for w in works if w.name.startswith(cfg) and pname in w.passes)
+            todo.append((name, w.passes[pname][0]))
+        else:
+            layer, op = name.rsplit(" ", 1)
+            L = next(L for L in layers if L["name"] == layer)
+            todo.append((name, pass_fns(L)[op]))
+    marker = torch.empty(1024, dtype=torch.float32, device=dev)
+    for name, fn in todo:
+        torch.cuda.synchronize()
+        marker.fill_(1.0)
+        print("pass:", name, flush=True)
+        for _ in range(reps):
+            fn()
+    torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0").fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()

@@ -103,6 +103,11 @@ constexpr int kFusedStageUnits = 2432;
 #endif
 #define VH_HALO_FUSED_WPE (VH_HALO_PC ? 4 : 2)
 
+// Fragment-read lookahead (in taps) of the producer / consumer form's consumers.
+#ifndef VH_HALO_PC_LA
+#define VH_HALO_PC_LA 1
+#endif
+
 // Grids of at least this many tiles (3x3, several channel groups) use one LDS
 // stage and three blocks per CU.
 #ifndef VH_HALO_WPE3_MIN_TILES
@@ -128,7 +133,10 @@ constexpr int kFusedStageUnits = 2432;
 // multiply (consumers: the accumulators), waves 4-7 only load the next channel
 // groups and store them into the other LDS stage (producers, threads 256-511
 // serving the load map of threads 0-255); one barrier per group on both sides.
-template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false, bool PC = false>
+// EPI selects the epilogue at compile time (0 per-element stores, 1 vector
+// stores through LDS, 2 lane pairs), so each instance carries the registers of
+// one epilogue only.
+template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false, bool PC = false, int EPI = 0>
 __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
   using Cfg = HaloCfg<R, S, WM, XI>;
   static_assert(!PC || FUSED, "producer / consumer split: fused form only");
@@ -268,9 +276,10 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   // are issued while group kt is multiplied and group kt+1 is written to LDS,
   // so every load has two compute phases to arrive; wide tiles (more than 4 x or 5 weight load
   // items per thread) keep one set to stay within two waves' registers.
-  // (PC: the producers keep one set -- a group's loads have the consumers'
-  // whole multiply phase to arrive -- so that both roles fit 128 registers)
-  constexpr int DEPTH = (WPE == 2 && !PC && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
+  // (PC: the producers keep two sets for narrow loads -- the loads of group k are
+  // issued two multiply phases before the group is stored -- and both roles fit
+  // 128 registers; with 4 x items per thread one set, which fits without spills)
+  constexpr int DEPTH = PC ? (Cfg::XITER <= 2 ? 2 : 1) : (WPE == 2 && Cfg::XITER <= 4 && Cfg::WITER <= 5) ? 2 : 1;
   static_assert(!FUSED || PC || DEPTH == 2, "the fused form keeps two register sets");
   u32x4 wreg[DEPTH][WD ? 1 : Cfg::WITER];
   u32x2 wdr[DEPTH][WD ? 9 : 1];
@@ -281,24 +290,25 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   auto gload = [&](auto SET, int c0) {
     constexpr int sI = decltype(SET)::value;
     const int crem = a.C - c0;  // channels left from c0 (<= 0 past the last group)
-    // the fused form loads only whole groups inside C (C % 16 == 0, c0 < C)
+    // groups past the last one (c0 >= C) read zeros through the zero-length
+    // buffer: the channel offset is a scalar offset, which is not range-checked
     if constexpr (WD) {
 #pragma unroll
       for (int j = 0; j < 9; ++j)
         wdr[sI][j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                   FUSED || crem > 0 ? wrsrc : zrsrc, wd_goff + 8 * j, c0 * 18, 0));
+                                                   crem > 0 ? wrsrc : zrsrc, wd_goff + 8 * j, c0 * 18, 0));
     } else {
 #pragma unroll
       for (int it = 0; it < Cfg::WITER; ++it)
         wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     FUSED || crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
+                                                     crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
     }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
       const int half = it < XH ? 0 : 1;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(FUSED || j + 8 * half < crem ? xrsrc : zrsrc,
+        xreg[sI][it][j] = __builtin_amdgcn_raw_buffer_load_b32(j + 8 * half < crem ? xrsrc : zrsrc,
                                                                x_voff[it], (c0 + j) * HW2, 0);
     }
   };
@@ -392,7 +402,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
     // group kt is multiplied from stage kt & 1 while the producers store group
     // kt+1 into the other stage (read by the consumers before the previous
     // barrier) and load group kt+2 (fused form: every group is whole, C % 16 == 0)
-    if (producer) {
+    if (producer && DEPTH == 1) {
       gload(I0{}, 0);
       __builtin_amdgcn_sched_barrier(0);
       sstore(I0{}, 0);
@@ -409,9 +419,44 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       }
       return;
     }
+    if constexpr (DEPTH == 2) if (producer) {
+      // two register sets: at an even kt set 1 holds group kt+1 and set 0
+      // group kt+2 (in flight).  Every load is issued (groups past the last
+      // read zeros), so each wait covers only the set about to be stored.
+      gload(I0{}, 0);
+      gload(I1{}, 16);
+      __builtin_amdgcn_sched_barrier(0);
+      sstore(I0{}, 0);
+      gload(I0{}, 32);
+      __syncthreads();
+      for (int kt = 0; kt < nk; kt += 2) {
+        if (kt + 1 < nk) sstore(I1{}, 1);
+        gload(I1{}, (kt + 3) * 16);
+        __syncthreads();
+        if (kt + 1 >= nk) break;
+        if (kt + 2 < nk) sstore(I0{}, 0);
+        gload(I0{}, (kt + 4) * 16);
+        __syncthreads();
+      }
+      return;
+    }
     __syncthreads();
     for (int kt = 0; kt < nk; ++kt) {
+      // fragment reads of tap t+LA placed between the MFMAs of tap t, so each
+      // read has LA taps of MFMAs to arrive (LA = VH_HALO_PC_LA)
       compute(kt & 1);
+      constexpr int LA = VH_HALO_PC_LA;
+      if constexpr (LA > 0) {
+        __builtin_amdgcn_sched_group_barrier(0x100, LA * (FM + FN), 0);  // reads of taps 0 .. LA-1
+#pragma unroll
+        for (int t = 0; t < RS; ++t) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (t + LA < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (t + LA < RS) __builtin_amdgcn_sched_group_barrier(0x100, (FM + FN) / 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, FM * FN - 2, 0);
+        }
+      }
       __syncthreads();
     }
   } else if constexpr (DEPTH == 2) {
@@ -522,7 +567,23 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 #undef WSM
 #undef XSM
   const int PQ = a.P * a.Q;
-  if (a.pair_epi) {
+  // fp32 bias of the 16 accumulator rows of fragment row i of this lane (output
+  // channel o0 + wm + i*32 + (v>>2)*8 + (lane>>5)*4 + (v&3)), loaded per i: one
+  // uniform branch, buffer loads that return 0 past O (the whole offset in the
+  // per-lane operand: the scalar offset is not range-checked).
+  const __amdgpu_buffer_rsrc_t brsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.bias, (short)0, a.bias ? a.O * 2 : 0, 0x00020000);
+  auto load_bias = [&](int i, float (&bi)[16]) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) bi[v] = 0.f;
+    if (a.bias) {
+      const int ob = (o0 + wm + i * 32 + (lane >> 5) * 4) * 2;
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        bi[v] = bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(brsrc, ob + ((v >> 2) * 8 + (v & 3)) * 2, 0, 0));
+    }
+  };
+  if constexpr (EPI == 2) {
     // Pair epilogue.  Accumulator v of a lane is output row (v>>2)*8 + (v&3)
     // (+4 in the upper half-wave) at the lane's position.  Lanes 2m and 2m+1
     // hold consecutive positions (the same image row: Q and every tile start
@@ -549,14 +610,6 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
                           ((lane >> 5) * 4 + (lane & 1)) * PQ2
                     : (int)0x80000000u;
     }
-    float bv[FM][16];
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        bv[i][v] = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
-      }
     // the ReLU-backward mask of the dwords this lane stores, all loaded before the first store
     uint32_t mk[FM][FN][8];
     if (a.act == 2) {
@@ -566,11 +619,16 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
         for (int vp = 0; vp < 8; ++vp) {
           const int orow = o0 + wm + i * 32 + (vp >> 1) * 8 + (vp & 1) * 2;
 #pragma unroll
-          for (int j = 0; j < FN; ++j) mk[i][j][vp] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, yoff[j], orow * PQ2, 0);
+          // the row offset goes into the range-checked per-lane offset: rows past O
+          // (last o tile) and positions past the end read zeros
+          for (int j = 0; j < FN; ++j)
+            mk[i][j][vp] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, (int)((uint32_t)yoff[j] + (uint32_t)(orow * PQ2)), 0, 0);
         }
     }
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+      float bv[16];
+      load_bias(i, bv);
 #pragma unroll
       for (int vp = 0; vp < 8; ++vp) {
         const int v = 2 * vp;  // rows v, v+1 = orow, orow+1
@@ -578,7 +636,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
         const bool ok = full_o || orow + (lane >> 5) * 4 + (lane & 1) < a.O;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          float a0 = acc[i][j][v] + bv[i][v], a1 = acc[i][j][v + 1] + bv[i][v + 1];
+          float a0 = acc[i][j][v] + bv[v], a1 = acc[i][j][v + 1] + bv[v + 1];
           if (a.act == 1) {
             a0 = fmaxf(a0, 0.f);
             a1 = fmaxf(a1, 0.f);
@@ -597,9 +655,10 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
           if (ok) __builtin_amdgcn_raw_buffer_store_b32(d, yrsrc, yoff[j], orow * PQ2, 0);
         }
       }
+    }
     return;
   }
-  if (a.vec_epi) {
+  if constexpr (EPI == 1) {
     // Vector epilogue.  Each wave writes its 64 o x 64 position tile, bias added
     // and rounded once to bf16 (ReLU applied in fp32 first), into its own LDS
     // region [o][position] (pitch 72 elements: the two half-waves, 4 rows
@@ -611,31 +670,38 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
                                          // (PC: the consumers' last loop barrier)
     uint16_t* eb = reinterpret_cast<uint16_t*>(lds) + wave * (64 * EP);
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+    for (int i = 0; i < FM; ++i) {
+      float bv[16];
+      load_bias(i, bv);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        const int o = o0 + wm + row;
-        const float bias = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-          float val = acc[i][j][v] + bias;
+          float val = acc[i][j][v] + bv[v];
           if (a.act == 1) val = fmaxf(val, 0.f);
           eb[row * EP + j * 32 + (lane & 31)] = __builtin_bit_cast(uint16_t, (__bf16)val);
         }
       }
+    }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
     __builtin_amdgcn_wave_barrier();
+    // lane -> 8 positions m .. m+7 (the same for every pass) and rows it*8 + lane/8:
+    // all eight LDS reads first, then the stores
+    const int k8 = lane & 7, m = m0 + wn + k8 * 8;
+    uint32_t n_e, pq_e;
+    a.fPQ.divmod((uint32_t)min(m, a.M - 1), n_e, pq_e);
+    const long ybase = (long)n_e * a.O * PQ + pq_e;
+    uint4 ev[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) ev[it] = *reinterpret_cast<const uint4*>(eb + (it * 8 + (lane >> 3)) * EP + k8 * 8);
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
-      const int c = it * 64 + lane, row = c >> 3, k = c & 7;
+      const int row = it * 8 + (lane >> 3);
       const int o = o0 + wm + row;
-      const int m = m0 + wn + k * 8;
       if (o < a.O && m < a.M) {
-        uint32_t n, pq;
-        a.fPQ.divmod((uint32_t)m, n, pq);
-        const long off = ((long)n * a.O + o) * PQ + pq;
-        uint4 val = *reinterpret_cast<const uint4*>(eb + row * EP + k * 8);
+        const long off = ybase + (long)o * PQ;
+        uint4 val = ev[it];
         if (a.act == 2) {
           // zero where the layer's forward output (the mask) is not positive
           const uint4 mk = *reinterpret_cast<const uint4*>(a.mask + off);
@@ -688,7 +754,8 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       for (int v = 0; v < 16; ++v) {
         const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) mv[i][j][v] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, yoff[j], orow * PQ2, 0);
+        for (int j = 0; j < FN; ++j)  // row offset range-checked too (rows past O read zeros)
+          mv[i][j][v] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, (int)((uint32_t)yoff[j] + (uint32_t)(orow * PQ2)), 0, 0);
       }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -702,39 +769,22 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
     else if (a.act == 2 && !((keep[i][j] >> v) & 1u)) val = 0.f;
     return __builtin_bit_cast(uint16_t, (__bf16)val);
   };
-  float bv[FM][16];
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+  for (int i = 0; i < FM; ++i) {
+    float bv[16];
+    load_bias(i, bv);
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      int o = o0 + wm + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-      bv[i][v] = (a.bias && o < a.O) ? bf16_to_f32(a.bias[o]) : 0.f;
+      const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);  // wave-uniform part of o
+      const bool ok = full_o || orow + (lane >> 5) * 4 < a.O;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if (ok)
+          __builtin_amdgcn_raw_buffer_store_b16(epi(acc[i][j][v] + bv[v], i, j, v), yrsrc, yoff[j], orow * PQ2, 0);
     }
-  if (full_o) {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);  // wave-uniform part of o
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          __builtin_amdgcn_raw_buffer_store_b16(epi(acc[i][j][v] + bv[i][v], i, j, v), yrsrc, yoff[j], orow * PQ2, 0);
-      }
-  } else {
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int orow = o0 + wm + i * 32 + (v >> 2) * 8 + (v & 3);
-        const bool ok = orow + (lane >> 5) * 4 < a.O;
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          if (ok)
-            __builtin_amdgcn_raw_buffer_store_b16(epi(acc[i][j][v] + bv[i][v], i, j, v), yrsrc, yoff[j],
-                                                  orow * PQ2, 0);
-      }
   }
 }
+
 
 // ---------------------------------------------------------------- host side
 namespace {
@@ -742,9 +792,16 @@ namespace {
 template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false, bool PC = false>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   using Cfg = HaloCfg<R, S, WM, XI>;
-  auto kern = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC>;
+  auto k0 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 0>;
+  auto k1 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 1>;
+  auto k2 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 2>;
   // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
-  if (!FUSED) VH_LDS_LIMIT_ONCE(kern);
+  if (!FUSED) {
+    VH_LDS_LIMIT_ONCE(k0);
+    VH_LDS_LIMIT_ONCE(k1);
+    VH_LDS_LIMIT_ONCE(k2);
+  }
+  auto kern = a.vec_epi ? k1 : a.pair_epi ? k2 : k0;
   HaloArgs g = a;
   g.tiles_m = (a.M + Cfg::BN - 1) / Cfg::BN;
   g.tiles_o = (a.O + Cfg::BM - 1) / Cfg::BM;
@@ -931,9 +988,10 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.pair_epi = (!a.vec_epi && Q % 2 == 0 && a.TW % 2 == 0 && ((uintptr_t)y & 3) == 0 &&
                 (act != 2 || ((uintptr_t)mask & 3) == 0))
                    ? 1 : 0;
+  const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
+  const int stage_units = WM * 64 * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
-  const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
   const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= VH_HALO_WPE3_MIN_TILES && halo_xi(a) <= (WM == 1 ? 4 : 2);
   if (wpe3) a.stages = 1;
   const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
@@ -941,7 +999,6 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // Fused form (two register sets, whole channel groups, stages and the
   // vector epilogue within the static stage size): 3x3, 64 x 256 tiles with
   // at most 4 x items per thread.
-  const int stage_units = WM * 64 * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
   const bool fused = !wpe3 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
                      stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16);
   // The fused forward reads W [O][C][3][3] directly (no relayout launch).  Each
