@@ -691,34 +691,15 @@ static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const C
 
 
 // ------------------------------------------------------------------ GEMM entry helper
-// bf16 products on the dense NT kernel: operands whose contraction index is
-// not contiguous (KD_DENSE_MN: stored [K][rows]) are transposed into the
-// workspace first.  Returns VH_ERR_UNSUPPORTED when the shapes do not fit.
+// bf16 products on the dense kernel: either operand may be stored with its
+// contraction index contiguous (KD_DENSE_K) or its row index contiguous
+// (KD_DENSE_MN: stored [K][rows], read by transposing LDS reads).  Returns
+// VH_ERR_UNSUPPORTED when the shapes or alignments do not fit.
 static int dense_bf16(int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc, long M,
                       long N, long K, const void* bias, hipStream_t st) {
-  if (K % 8 || (ak == KD_DENSE_MN && M % 8) || (bk == KD_DENSE_MN && N % 8)) return VH_ERR_UNSUPPORTED;
-  const long lda2 = ak == KD_DENSE_MN ? K : lda, ldb2 = bk == KD_DENSE_MN ? K : ldb;
-  const void* a2 = ak == KD_DENSE_MN ? nullptr : a;
-  const void* b2 = bk == KD_DENSE_MN ? nullptr : b;
-  if ((a2 && ((uintptr_t)a2 & 15)) || (b2 && ((uintptr_t)b2 & 15))) return VH_ERR_UNSUPPORTED;
-  if ((ak == KD_DENSE_MN && ((uintptr_t)a & 15 || lda % 8)) || (bk == KD_DENSE_MN && ((uintptr_t)b & 15 || ldb % 8)))
-    return VH_ERR_UNSUPPORTED;
-  Carve cv;
-  const size_t oa = cv.take(ak == KD_DENSE_MN ? (size_t)M * K * 2 : 0);
-  const size_t ob = cv.take(bk == KD_DENSE_MN ? (size_t)N * K * 2 : 0);
-  if (!dense_nt_bf16_ok(M, N, K, lda2, ldb2, ldc, a2 ? a2 : (const void*)256, b2 ? b2 : (const void*)256, c))
-    return VH_ERR_UNSUPPORTED;
-  void* ws;
-  VH_TRY(ws_get(st, cv.off, &ws));
-  if (!a2) {
-    a2 = at(ws, oa);
-    VH_TRY(transpose_bf16(a, lda, (void*)a2, (int)K, (int)M, st));
-  }
-  if (!b2) {
-    b2 = at(ws, ob);
-    VH_TRY(transpose_bf16(b, ldb, (void*)b2, (int)K, (int)N, st));
-  }
-  return dense_nt_bf16(a2, (int)lda2, b2, (int)ldb2, c, ldc, (int)M, (int)N, (int)K, bias, st);
+  const bool at = ak == KD_DENSE_MN, bt = bk == KD_DENSE_MN;
+  if (!dense_bf16_ok(M, N, K, at, lda, bt, ldb, ldc, a, b, c)) return VH_ERR_UNSUPPORTED;
+  return dense_bf16_gemm(a, lda, at, b, ldb, bt, c, ldc, (int)M, (int)N, (int)K, bias, st);
 }
 
 static int gemm(int dt, int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc,

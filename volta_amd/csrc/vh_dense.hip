@@ -1,14 +1,17 @@
 // vh_dense.hip -- dense bf16 matrix products (matmul, its gradients, Linear) on
 // gfx950 MFMA (v_mfma_f32_32x32x16_bf16), fp32 accumulation.
 //
-// One kernel form, "NT": C[M][N] = A[M][K] . B[N][K]^T, both operands with the
-// contraction index K contiguous (row-major, leading dimensions lda / ldb), so
-// every operand tile is a plain copy of 16-byte units into LDS and every MFMA
-// fragment (8 consecutive k of one row) is one ds_read_b128.  Products whose
-// operands run the other way (matmul's B, the weight gradient's A and G) are
-// first transposed into a workspace by transpose_bf16_kernel (tiled through
-// LDS: both sides coalesced); that pass moves each operand once, a few percent
-// of the product's time at the configs' sizes.
+// One kernel for C[M][N] = A . B with either operand stored either way:
+// "K-major" (row-major [rows][K], the contraction index contiguous: A[M][K],
+// B[N][K]) or "MN-major" ([K][rows], the row index contiguous: A stored
+// [K][M], B stored [K][N] -- matmul's B, the weight gradient's A and G).  Every
+// operand tile is a plain copy of 16-byte units into LDS in its stored order.
+// An MFMA fragment (8 consecutive k of one row) of a K-major tile is one
+// ds_read_b128; of an MN-major tile ([k][row] in LDS) it is two
+// ds_read_b64_tr_b16, gfx950's transposing LDS read: within each group of 16
+// lanes, lane i names 4 consecutive elements of row i/4 (elements
+// 4*(i%4) .. +3), and lane j receives element j of each of the 4 rows, i.e. 4
+// consecutive k of column j.  No operand is transposed in memory.
 //
 // Block: 256 threads (2 x 2 waves), tile BM x BN, K in stages of 64; two LDS
 // stages and two register sets: the loads of stage k+2 are issued before the
@@ -32,8 +35,8 @@ constexpr int kOOR = (int)0x80000000u;  // buffer offset past every range: loads
 constexpr int kGroupM = VH_GEMM_GROUP_M;  // m-tiles per group of the block order
 
 struct DenseArgs {
-  const uint16_t* a;     // [M][lda]
-  const uint16_t* b;     // [N][ldb]
+  const uint16_t* a;     // [M][lda] (K-major) or [K][lda] (MN-major)
+  const uint16_t* b;     // [N][ldb] (K-major) or [K][ldb] (MN-major)
   uint16_t* c;           // [M][ldc]
   const uint16_t* bias;  // [N] or nullptr (added to every row)
   int M, N, K, lda, ldb, ldc;
@@ -41,14 +44,19 @@ struct DenseArgs {
   int tiles_m, tiles_n;
 };
 
-template <int BM, int BN>
+template <int BM, int BN, bool AT = false, bool BT = false>
 struct DenseCfg {
   static constexpr int BK = 64;            // contraction elements per stage
   static constexpr int KU = BK / 8;        // 16-byte units per row per stage
-  static constexpr int PU = KU + 1;        // LDS row pitch in units (odd: conflict-free)
+  static constexpr int PU = KU + 1;        // K-major tile: LDS row pitch in units (odd: conflict-free)
   static constexpr int FM = BM / 64, FN = BN / 64;  // 32x32 tiles per wave (waves 2 x 2)
   static constexpr int AIT = BM * KU / 256, BIT = BN * KU / 256;  // load units per thread
-  static constexpr int STAGE = (BM + BN) * PU;                     // units per LDS stage
+  // MN-major tile: BK rows of R elements, pitch R + 32 elements (row starts 64
+  // bytes apart mod 256: the four rows of a transposing read hit disjoint banks)
+  static constexpr int mn_pitch(int R) { return R / 8 + 4; }
+  static constexpr int A_UNITS = AT ? BK * mn_pitch(BM) : BM * PU;
+  static constexpr int B_UNITS = BT ? BK * mn_pitch(BN) : BN * PU;
+  static constexpr int STAGE = A_UNITS + B_UNITS;  // units per LDS stage
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -60,11 +68,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
 // other LDS buffer (producers, threads 256-511 serving the load map of threads
 // 0-255).  Neither role holds the other's registers, so two waves run per SIMD
 // and the loads leave the multiplying waves' instruction stream.
-template <int BM, int BN, bool BIAS, bool PC = false>
+template <int BM, int BN, bool BIAS, bool PC = false, bool AT = false, bool BT = false>
 __global__ __launch_bounds__(PC ? 512 : 256)
-void gemm_nt_bf16_kernel(DenseArgs g) {
-  using Cfg = DenseCfg<BM, BN>;
+void gemm_bf16_kernel(DenseArgs g) {
+  using Cfg = DenseCfg<BM, BN, AT, BT>;
   constexpr int FM = Cfg::FM, FN = Cfg::FN, PU = Cfg::PU, STAGE = Cfg::STAGE;
+  constexpr int APU = Cfg::mn_pitch(BM), BPU = Cfg::mn_pitch(BN);  // MN-major LDS pitches (units)
   extern __shared__ __attribute__((aligned(16))) u32x4d lds[];
   const bool producer = PC && threadIdx.x >= 256;
   const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
@@ -80,41 +89,66 @@ void gemm_nt_bf16_kernel(DenseArgs g) {
   const int in_grp = lb - grp * kGroupM * g.tiles_n;
   const int m0 = (first_m + in_grp % gm) * BM, n0 = (in_grp / gm) * BN;
 
-  // load items: unit u = tid + 256*it -> row u / KU, column unit u % KU (= tid % KU)
+  // Load items.  K-major operand: unit u = tid + 256*it -> row u / KU, k unit
+  // u % KU (= tid % KU); global offset of k0 = 0 (the stage's k0 is a scalar
+  // offset).  MN-major operand: unit u -> k row u / (R/8), row unit u % (R/8);
+  // the k row's bound is checked per unit (a scalar offset is not range-checked,
+  // so an unused unit carries an out-of-range per-lane offset).
   const int cu = tid % Cfg::KU;
-  int a_off[Cfg::AIT], b_off[Cfg::BIT];
+  int a_off[Cfg::AIT], b_off[Cfg::BIT], a_kr[Cfg::AIT], b_kr[Cfg::BIT], a_l[Cfg::AIT], b_l[Cfg::BIT];
 #pragma unroll
   for (int it = 0; it < Cfg::AIT; ++it) {
-    const int r = (tid + it * 256) / Cfg::KU;
-    a_off[it] = m0 + r < g.M ? ((m0 + r) * g.lda + cu * 8) * 2 : kOOR;
+    const int u = tid + it * 256;
+    if constexpr (AT) {
+      const int kr = u / (BM / 8), ru = u % (BM / 8);
+      a_kr[it] = kr;
+      a_off[it] = m0 + ru * 8 < g.M ? (kr * g.lda + m0 + ru * 8) * 2 : kOOR;
+      a_l[it] = kr * APU + ru;
+    } else {
+      const int r = u / Cfg::KU;
+      a_kr[it] = cu * 8;
+      a_off[it] = m0 + r < g.M ? ((m0 + r) * g.lda + cu * 8) * 2 : kOOR;
+      a_l[it] = r * PU + cu;
+    }
   }
 #pragma unroll
   for (int it = 0; it < Cfg::BIT; ++it) {
-    const int r = (tid + it * 256) / Cfg::KU;
-    b_off[it] = n0 + r < g.N ? ((n0 + r) * g.ldb + cu * 8) * 2 : kOOR;
+    const int u = tid + it * 256;
+    if constexpr (BT) {
+      const int kr = u / (BN / 8), ru = u % (BN / 8);
+      b_kr[it] = kr;
+      b_off[it] = n0 + ru * 8 < g.N ? (kr * g.ldb + n0 + ru * 8) * 2 : kOOR;
+      b_l[it] = Cfg::A_UNITS + kr * BPU + ru;
+    } else {
+      const int r = u / Cfg::KU;
+      b_kr[it] = cu * 8;
+      b_off[it] = n0 + r < g.N ? ((n0 + r) * g.ldb + cu * 8) * 2 : kOOR;
+      b_l[it] = Cfg::A_UNITS + r * PU + cu;
+    }
   }
   const __amdgpu_buffer_rsrc_t ar = rsrc(g.a, g.a_bytes), br = rsrc(g.b, g.b_bytes);
 
   u32x4d areg[2][Cfg::AIT], breg[2][Cfg::BIT];
   auto gload = [&](auto SET, int k0) {
     constexpr int s = decltype(SET)::value;
-    const bool kin = k0 + cu * 8 < g.K;  // K % 8 == 0: a unit is all in or all out
+    // k0 as a scalar offset: k0 elements along a K-major row, k0 rows of an MN-major operand
+    const int ask = AT ? k0 * g.lda * 2 : k0 * 2, bsk = BT ? k0 * g.ldb * 2 : k0 * 2;
 #pragma unroll
-    for (int it = 0; it < Cfg::AIT; ++it)
-      areg[s][it] = __builtin_bit_cast(u32x4d,
-                                       __builtin_amdgcn_raw_buffer_load_b128(ar, kin ? a_off[it] : kOOR, k0 * 2, 0));
+    for (int it = 0; it < Cfg::AIT; ++it)  // K % 8 == 0: a K-major unit is all in or all out
+      areg[s][it] = __builtin_bit_cast(
+          u32x4d, __builtin_amdgcn_raw_buffer_load_b128(ar, k0 + a_kr[it] < g.K ? a_off[it] : kOOR, ask, 0));
 #pragma unroll
     for (int it = 0; it < Cfg::BIT; ++it)
-      breg[s][it] = __builtin_bit_cast(u32x4d,
-                                       __builtin_amdgcn_raw_buffer_load_b128(br, kin ? b_off[it] : kOOR, k0 * 2, 0));
+      breg[s][it] = __builtin_bit_cast(
+          u32x4d, __builtin_amdgcn_raw_buffer_load_b128(br, k0 + b_kr[it] < g.K ? b_off[it] : kOOR, bsk, 0));
   };
   auto sstore = [&](auto SET, int st) {
     constexpr int s = decltype(SET)::value;
     u32x4d* base = lds + st * STAGE;
 #pragma unroll
-    for (int it = 0; it < Cfg::AIT; ++it) base[((tid + it * 256) / Cfg::KU) * PU + cu] = areg[s][it];
+    for (int it = 0; it < Cfg::AIT; ++it) base[a_l[it]] = areg[s][it];
 #pragma unroll
-    for (int it = 0; it < Cfg::BIT; ++it) base[(BM + (tid + it * 256) / Cfg::KU) * PU + cu] = breg[s][it];
+    for (int it = 0; it < Cfg::BIT; ++it) base[b_l[it]] = breg[s][it];
   };
 
   f32x16 acc[FM][FN];
@@ -126,16 +160,35 @@ void gemm_nt_bf16_kernel(DenseArgs g) {
   };
   if (!PC) zero_acc();
   const int row_l = lane & 31, half_l = lane >> 5;
+  // transposing reads of an MN-major tile: lane l reads k row 8*(l/32) + (l%16)/4
+  // (+4 for the second half of the fragment), elements 16*((l/16)%2) + 4*(l%4) .. +3
+  const int tr_row = 8 * half_l + ((lane & 15) >> 2), tr_col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto frag_mn = [&](const u32x4d* tile, int pitch_units, int ks, int col0) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    const __attribute__((address_space(3))) char* p =
+        (const __attribute__((address_space(3))) char*)(tile) +
+        (((ks * 8 + tr_row) * pitch_units) * 16 + (col0 + tr_col) * 2);
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)p);
+    const v4i16 hi =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p + 4 * pitch_units * 16));
+    typedef short v8i16 __attribute__((ext_vector_type(8)));
+    const v8i16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
+  };
   auto compute = [&](int st) {
     const u32x4d* ap = lds + st * STAGE + (wm + row_l) * PU + half_l;
-    const u32x4d* bp = lds + st * STAGE + (BM + wn + row_l) * PU + half_l;
+    const u32x4d* bp = lds + st * STAGE + Cfg::A_UNITS + (wn + row_l) * PU + half_l;
+    const u32x4d* at = lds + st * STAGE;
+    const u32x4d* bt = lds + st * STAGE + Cfg::A_UNITS;
 #pragma unroll
     for (int ks = 0; ks < Cfg::KU; ks += 2) {
       bf16x8 af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = __builtin_bit_cast(bf16x8, ap[i * 32 * PU + ks]);
+      for (int i = 0; i < FM; ++i)
+        af[i] = AT ? frag_mn(at, APU, ks, wm + i * 32) : __builtin_bit_cast(bf16x8, ap[i * 32 * PU + ks]);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) bf[j] = __builtin_bit_cast(bf16x8, bp[j * 32 * PU + ks]);
+      for (int j = 0; j < FN; ++j)
+        bf[j] = BT ? frag_mn(bt, BPU, ks, wn + j * 32) : __builtin_bit_cast(bf16x8, bp[j * 32 * PU + ks]);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -234,44 +287,12 @@ void gemm_nt_bf16_kernel(DenseArgs g) {
   }
 }
 
-// out[c][r] = in[r][c] for a bf16 [R][Cc] matrix (leading dimension ldi) into a
-// dense [Cc][R] one.  64 x 64 tiles: 16-byte loads along rows, the transposed
-// tile in LDS, 16-byte stores along the output rows.  R % 8 == 0, Cc % 8 == 0.
-__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ in, int ldi,
-                                                             uint16_t* __restrict__ out, int R, int Cc) {
-  __shared__ uint16_t t[64][64 + 8];
-  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int u = tid + k * 256;  // 512 units of 8 elements: row u / 8, column unit u % 8
-    const int r = u >> 3, cu = u & 7;
-    if (r0 + r < R && c0 + cu * 8 < Cc) {
-      const u32x4d v = *reinterpret_cast<const u32x4d*>(in + (size_t)(r0 + r) * ldi + c0 + cu * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        t[cu * 8 + 2 * e][r] = (uint16_t)(v[e] & 0xffffu);
-        t[cu * 8 + 2 * e + 1][r] = (uint16_t)(v[e] >> 16);
-      }
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int u = tid + k * 256;  // output row (input column) u / 8, unit u % 8
-    const int c = u >> 3, ru = u & 7;
-    if (c0 + c < Cc && r0 + ru * 8 < R)
-      *reinterpret_cast<u32x4d*>(out + (size_t)(c0 + c) * R + r0 + ru * 8) =
-          *reinterpret_cast<const u32x4d*>(&t[c][ru * 8]);
-  }
-}
-
 bool fits(long bytes) { return bytes >= 0 && bytes < (1L << 31) - 64; }
 
-template <int BM, int BN, bool BIAS, bool PC = false>
-int launch_nt(const DenseArgs& a0, hipStream_t st) {
-  using Cfg = DenseCfg<BM, BN>;
-  auto kern = gemm_nt_bf16_kernel<BM, BN, BIAS, PC>;
+template <int BM, int BN, bool BIAS, bool PC, bool AT, bool BT>
+int launch_gemm(const DenseArgs& a0, hipStream_t st) {
+  using Cfg = DenseCfg<BM, BN, AT, BT>;
+  auto kern = gemm_bf16_kernel<BM, BN, BIAS, PC, AT, BT>;
   const size_t lds = (size_t)2 * Cfg::STAGE * 16;
   VH_LDS_LIMIT_ONCE(kern);
   DenseArgs a = a0;
@@ -282,17 +303,29 @@ int launch_nt(const DenseArgs& a0, hipStream_t st) {
   return VH_OK;
 }
 
-}  // namespace
-
-bool dense_nt_bf16_ok(long M, long N, long K, long lda, long ldb, long ldc, const void* a, const void* b,
-                      const void* c) {
-  if (M <= 0 || N <= 0 || K <= 0 || K % 8 || lda % 8 || ldb % 8) return false;
-  if (((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 1)) return false;
-  return fits(M * lda * 2) && fits(N * ldb * 2) && fits(M * ldc * 2);
+// 128 x 256 tiles (one block per CU, producer / consumer form, 64 x 128 per
+// consumer wave) when the grid still fills the chip, else 128 x 128 (two
+// blocks per CU of four waves that both load and multiply: already two waves
+// per SIMD, and measured as fast as or faster than a split form)
+template <bool AT, bool BT>
+int launch_layout(const DenseArgs& g, bool big, hipStream_t st) {
+  if (big)
+    return g.bias ? launch_gemm<128, 256, true, true, AT, BT>(g, st) : launch_gemm<128, 256, false, true, AT, BT>(g, st);
+  return g.bias ? launch_gemm<128, 128, true, false, AT, BT>(g, st) : launch_gemm<128, 128, false, false, AT, BT>(g, st);
 }
 
-int dense_nt_bf16(const void* a, int lda, const void* b, int ldb, void* c, int ldc, int M, int N, int K,
-                  const void* bias, hipStream_t st) {
+}  // namespace
+
+bool dense_bf16_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, long ldc, const void* a,
+                   const void* b, const void* c) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 8 || lda % 8 || ldb % 8) return false;
+  if ((at && (M % 8 || lda < M)) || (bt && (N % 8 || ldb < N)) || (!at && lda < K) || (!bt && ldb < K)) return false;
+  if (((uintptr_t)a & 15) || ((uintptr_t)b & 15) || ((uintptr_t)c & 1)) return false;
+  return fits((at ? K : M) * lda * 2) && fits((bt ? K : N) * ldb * 2) && fits(M * ldc * 2);
+}
+
+int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
+                    int N, int K, const void* bias, hipStream_t st) {
   DenseArgs g{};
   g.a = (const uint16_t*)a;
   g.b = (const uint16_t*)b;
@@ -304,24 +337,12 @@ int dense_nt_bf16(const void* a, int lda, const void* b, int ldb, void* c, int l
   g.lda = lda;
   g.ldb = ldb;
   g.ldc = ldc;
-  g.a_bytes = (int)((long)M * lda * 2);
-  g.b_bytes = (int)((long)N * ldb * 2);
+  g.a_bytes = (int)((long)(at ? K : M) * lda * 2);
+  g.b_bytes = (int)((long)(bt ? K : N) * ldb * 2);
   g.c_bytes = (int)((long)M * ldc * 2);
-  // 128 x 256 tiles (one block per CU, producer / consumer form, 64 x 128 per
-  // consumer wave) when the grid still fills the chip, else 128 x 128 (two
-  // blocks per CU of four waves that both load and multiply: already two waves
-  // per SIMD, and measured as fast as or faster than a split form)
-  const long big = (long)((M + 127) / 128) * ((N + 255) / 256);
-  if (big >= 256) return bias ? launch_nt<128, 256, true, true>(g, st) : launch_nt<128, 256, false, true>(g, st);
-  return bias ? launch_nt<128, 128, true>(g, st) : launch_nt<128, 128, false>(g, st);
-}
-
-int transpose_bf16(const void* in, int ldi, void* out, int R, int Cc, hipStream_t st) {
-  if (R % 8 || Cc % 8) return set_error(VH_ERR_UNSUPPORTED, "transpose needs multiples of 8");
-  dim3 grid((unsigned)((Cc + 63) / 64), (unsigned)((R + 63) / 64));
-  transpose_bf16_kernel<<<grid, 256, 0, st>>>((const uint16_t*)in, ldi, (uint16_t*)out, R, Cc);
-  VH_LAUNCH_CHECK();
-  return VH_OK;
+  const bool big = (long)((M + 127) / 128) * ((N + 255) / 256) >= 256;
+  if (at) return bt ? launch_layout<true, true>(g, big, st) : launch_layout<true, false>(g, big, st);
+  return bt ? launch_layout<false, true>(g, big, st) : launch_layout<false, false>(g, big, st);
 }
 
 }  // namespace vh

@@ -109,13 +109,13 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
                     int S, int ph, int pw, float* ws, size_t ws_bytes, hipStream_t st);
 
 // ---- dense bf16 products (vh_dense.hip) ----
-// C[M][N] = A[M][K] . B[N][K]^T (+ bias[N] per column), bf16 in and out.
-bool dense_nt_bf16_ok(long M, long N, long K, long lda, long ldb, long ldc, const void* a, const void* b,
-                      const void* c);
-int dense_nt_bf16(const void* a, int lda, const void* b, int ldb, void* c, int ldc, int M, int N, int K,
-                  const void* bias, hipStream_t st);
-// out[Cc][R] = in[R][Cc] (leading dimension ldi), R % 8 == 0, Cc % 8 == 0.
-int transpose_bf16(const void* in, int ldi, void* out, int R, int Cc, hipStream_t st);
+// C[M][N] = A . B (+ bias[N] per column), bf16 in and out.  A is stored
+// [M][lda] (K contiguous) or, with at, [K][lda] (M contiguous); B is stored
+// [N][ldb] or, with bt, [K][ldb].
+bool dense_bf16_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, long ldc, const void* a,
+                   const void* b, const void* c);
+int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
+                    int N, int K, const void* bias, hipStream_t st);
 
 // ---- strided 1x1 bf16 convolutions, pad 0 (vh_pointwise.hip) ----
 // w is the OIHW weight itself ([O][C]).  Each returns VH_ERR_UNSUPPORTED
