@@ -148,6 +148,8 @@ CONV_CASES = [
     (1, 2, 3, 12, 12, 9, 1, 4),      # 81-tap window (element-wise weight relayout)
     (2, 16, 24, 11, 9, 3, 2, 1),     # stride 2, 3x3: phases with 1 and 2 taps per axis, odd sizes
     (2, 8, 16, 10, 10, 1, 2, 0),     # 1x1 stride 2: odd input phases get no taps (zeros)
+    (2, 3, 16, 10, 10, 4, 2, 1),     # 3 input channels, stride 2: input gradient one lane per position
+    (2, 4, 8, 9, 11, 3, 3, 2),       # 4 input channels, stride 3
 ]
 
 
@@ -303,6 +305,9 @@ CT_CASES = [
     (1, 5, 6, 5, 3, 3, 2, 1),
     (2, 8, 5, 5, 7, 3, 2, 0),        # stride 2, no padding, odd output sizes
     (1, 4, 6, 3, 3, 5, 3, 2),        # stride 3, 5x5
+    (2, 8, 2, 5, 5, 3, 1, 1),        # 2 output channels, stride 1 (one lane per output position)
+    (3, 6, 1, 4, 6, 4, 2, 1),        # 1 output channel
+    (2, 16, 4, 1, 1, 3, 1, 0),       # 1x1 input: the layer is one product
 ]
 
 

@@ -449,6 +449,8 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
     *need = n;
     return VH_OK;
   }
+  // at most 4 input channels: one lane per input position, no workspace
+  if (g_fast_paths && dgrad_smallc_ok(g)) return VH_DISPATCH(dt, run_dgrad_smallc, dy, w, nullptr, mask, dx, g, st);
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wd = at(ws, o_w);
@@ -1214,6 +1216,16 @@ static int convt_dims(ConvDims& d, long B, long CI, long CO, long H, long W, lon
   return check_conv(d, true);
 }
 
+// A ConvTranspose2d whose input is 1 x 1 with stride 1 and no padding (a
+// generator's latent projection, conv_transpose.rs:356-435 with H = W = 1): each
+// output position (kh, kw) receives exactly one tap, so the layer is the plain
+// product y[n][co*KH*KW + kh*KW + kw] = sum_ci z[n][ci] W[ci][co][kh][kw] over
+// the IOHW weight viewed as [CI][CO*KH*KW].  In conv terms (d): O = CI, C = CO,
+// H x W = KH x KW, HO = WO = 1.
+static bool convt_is_projection(const ConvDims& d) {
+  return d.HO == 1 && d.WO == 1 && d.SH == 1 && d.SW == 1 && d.PH == 0 && d.PW == 0;
+}
+
 int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight, const void* bias, void* output,
                                 VH_LAYER_ARGS, void* stream) {
   VH_ENTRY();
@@ -1225,6 +1237,16 @@ int vh_conv_transpose2d_forward(int dtype, const void* input, const void* weight
   if (!input || !weight || !output) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   // y = dgrad(dy := x; W viewed OIHW with O = in_channels, C = out_channels) + bias
+  if (g_fast_paths && convt_is_projection(d) && (dtype == VH_F32 || !bias)) {
+    // the product, then the channel bias (for f32 the same single rounding as a fused add)
+    const long NC = d.C * d.H * d.W;
+    VH_TRY(gemm(dtype, KD_DENSE_K, KD_DENSE_MN, input, (int)d.O, weight, (int)NC, output, (int)NC, d.B, NC, d.O,
+                nullptr, 0, st));
+    return bias ? VH_DISPATCH(dtype, run_channel_bias_add, output, bias, d.B, (int)d.C, d.H * d.W, st) : VH_OK;
+  }
+  const ConvGeom gs = geom_of(d);
+  if (g_fast_paths && dgrad_smallc_ok(gs))  // at most 4 output channels
+    return VH_DISPATCH(dtype, run_dgrad_smallc, input, weight, bias, nullptr, output, gs, st);
   if ((d.SH > 1 || d.SW > 1) && g_fast_paths) {
     int r = dgrad_phases(dtype, input, weight, bias, output, d, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
@@ -1272,6 +1294,18 @@ int vh_conv_transpose2d_backward(int dtype, const void* out_grad, const void* in
     return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
   // In conv terms (d): x = out_grad (C = out_channels), dy = input (O = in_channels).
+  if (g_fast_paths && convt_is_projection(d)) {
+    // dz = dY . W^T ([B][CO*KH*KW] . [CO*KH*KW][CI]); dW = z^T . dY
+    const long NC = d.C * d.H * d.W;
+    if (grad_input)
+      VH_TRY(gemm(dtype, KD_DENSE_K, KD_DENSE_K, out_grad, (int)NC, weight, (int)NC, grad_input, (int)d.O, d.B, d.O,
+                  NC, nullptr, 0, st));
+    if (grad_weight)
+      VH_TRY(gemm(dtype, KD_DENSE_MN, KD_DENSE_MN, input, (int)d.O, out_grad, (int)NC, grad_weight, (int)NC, d.O, NC,
+                  d.B, nullptr, 0, st));
+    if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.C, d.H * d.W, st));
+    return VH_OK;
+  }
   if (grad_input) VH_TRY(igemm_fwd(dtype, out_grad, weight, nullptr, grad_input, d, st));
   if (grad_weight) VH_TRY(igemm_wgrad(dtype, input, out_grad, grad_weight, nullptr, nullptr, d, st));
   if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.C, d.H * d.W, st));

@@ -93,6 +93,86 @@ __global__ __launch_bounds__(256) void direct_dgrad_kernel(const typename Elem<T
   }
 }
 
+// Input gradient of a convolution with at most 4 input channels (and
+// ConvTranspose2d's forward to at most 4 output channels, e.g. a generator's
+// last layer to RGB), where an implicit GEMM would spend over 90 % of its MFMA
+// tile on rows past C.  One lane per input position (n, h, w) computes all C of
+// its outputs: for every tap (r, s) that reaches an output position (the other
+// stride phases are skipped) and every output channel o, one dY load and C
+// fused multiply-adds with the weights, held in LDS as fp32 [o][r][s][CC].  fp32
+// accumulation; bias and the ReLU-backward mask (zero where mask <= 0) in the
+// epilogue, one rounding.  Consecutive lanes take consecutive w, so the dY
+// loads of a wave cover one or two runs of a row.
+template <typename T, int CC>
+__global__ __launch_bounds__(256) void dgrad_smallc_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                           const typename Elem<T>::storage* __restrict__ w,
+                                                           const typename Elem<T>::storage* __restrict__ bias,
+                                                           const typename Elem<T>::storage* __restrict__ mask,
+                                                           typename Elem<T>::storage* __restrict__ dx, ConvGeom g,
+                                                           long total) {
+  extern __shared__ float wl[];
+  const int RS = g.R * g.S;
+  for (int i = threadIdx.x; i < g.O * RS * CC; i += 256) {
+    const int c = i % CC, ors = i / CC, o = ors / RS, rs = ors - o * RS;
+    wl[i] = c < g.C ? Elem<T>::to_f32(w[((long)o * g.C + c) * RS + rs]) : 0.f;
+  }
+  __syncthreads();
+  const long PQ = (long)g.P * g.Q;
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
+    const int iw = (int)(i % g.W);
+    const long t = i / g.W;
+    const int ih = (int)(t % g.H), n = (int)(t / g.H);
+    float acc[CC];
+#pragma unroll
+    for (int c = 0; c < CC; ++c) acc[c] = 0.f;
+    const int th = ih + g.ph, tw = iw + g.pw;
+    const auto* dyn = dy + (long)n * g.O * PQ;
+    // taps r = th mod sh, +sh, ... (r <= th): output row p = (th - r) / sh
+    for (int r = th % g.sh; r < g.R && r <= th; r += g.sh) {
+      const int p = (th - r) / g.sh;
+      if (p >= g.P) continue;
+      for (int s = tw % g.sw; s < g.S && s <= tw; s += g.sw) {
+        const int q = (tw - s) / g.sw;
+        if (q >= g.Q) continue;
+        const auto* d0 = dyn + (long)p * g.Q + q;
+        const float* w0 = wl + (r * g.S + s) * CC;
+        int o = 0;
+        for (; o + 4 <= g.O; o += 4) {
+          float v[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) v[u] = Elem<T>::to_f32(d0[(o + u) * PQ]);
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int c = 0; c < CC; ++c) acc[c] = fmaf(v[u], w0[(o + u) * RS * CC + c], acc[c]);
+        }
+        for (; o < g.O; ++o) {
+          const float v = Elem<T>::to_f32(d0[o * PQ]);
+#pragma unroll
+          for (int c = 0; c < CC; ++c) acc[c] = fmaf(v, w0[o * RS * CC + c], acc[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < CC; ++c) {
+      if (c >= g.C) break;
+      const long idx = (((long)n * g.C + c) * g.H + ih) * g.W + iw;
+      float val = acc[c] + (bias ? Elem<T>::to_f32(bias[c]) : 0.f);
+      if (mask && !(Elem<T>::to_f32(mask[idx]) > 0.f)) val = 0.f;
+      dx[idx] = Elem<T>::from_f32(val);
+    }
+  }
+}
+
+// y[n][c][hw] += bias[c] over an NCHW tensor (fp32 add, one rounding).
+template <typename T>
+__global__ __launch_bounds__(256) void channel_bias_add_kernel(typename Elem<T>::storage* __restrict__ y,
+                                                               const typename Elem<T>::storage* __restrict__ bias,
+                                                               int C, long HW, long total) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256)
+    y[i] = Elem<T>::from_f32(Elem<T>::to_f32(y[i]) + Elem<T>::to_f32(bias[(i / HW) % C]));
+}
+
 // Weight gradient: one workgroup per (weight element, position slice); the 256
 // lanes stride over output positions and a wavefront reduction (DPP shuffles)
 // plus an LDS step combine them into one fp32 partial per slice.
@@ -808,6 +888,38 @@ int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g,
   return VH_OK;
 }
 
+bool dgrad_smallc_ok(const ConvGeom& g) { return g.C >= 1 && g.C <= 4 && (long)g.O * g.R * g.S * 4 <= 16384; }
+
+template <typename T>
+int run_dgrad_smallc(const void* dy, const void* w, const void* bias, const void* mask, void* dx, const ConvGeom& g,
+                     hipStream_t st) {
+  if (!dgrad_smallc_ok(g)) return VH_ERR_UNSUPPORTED;
+  using S = typename Elem<T>::storage;
+  const long total = (long)g.N * g.H * g.W;
+  const int cc = g.C <= 1 ? 1 : g.C <= 2 ? 2 : 4;
+  const size_t lds = (size_t)g.O * g.R * g.S * cc * sizeof(float);
+  const int grid = grid_for(total);
+#define VH_SMALLC(CCV)                                                                                        \
+  dgrad_smallc_kernel<T, CCV><<<grid, 256, lds, st>>>((const S*)dy, (const S*)w, (const S*)bias, (const S*)mask, \
+                                                      (S*)dx, g, total)
+  if (cc == 1) VH_SMALLC(1);
+  else if (cc == 2) VH_SMALLC(2);
+  else VH_SMALLC(4);
+#undef VH_SMALLC
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+template <typename T>
+int run_channel_bias_add(void* y, const void* bias, long N, int C, long HW, hipStream_t st) {
+  using S = typename Elem<T>::storage;
+  const long total = N * C * HW;
+  if (total == 0) return VH_OK;
+  channel_bias_add_kernel<T><<<grid_for(total), 256, 0, st>>>((S*)y, (const S*)bias, C, HW, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 template <typename T>
 size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
   long npos = (long)g.N * g.P * g.Q;
@@ -1127,6 +1239,9 @@ int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, floa
   template int run_col2im_t<T>(const float*, void*, int, int, int, int, int, int, int, int, int, int, int, int,  \
                                hipStream_t);                                                            \
   template int run_direct_dgrad<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);      \
+  template int run_dgrad_smallc<T>(const void*, const void*, const void*, const void*, void*,            \
+                                   const ConvGeom&, hipStream_t);                                      \
+  template int run_channel_bias_add<T>(void*, const void*, long, int, long, hipStream_t);               \
   template size_t direct_wgrad_ws<T>(const ConvGeom&, int*, int*);                                      \
   template int run_direct_wgrad<T>(const void*, const void*, void*, const ConvGeom&, float*, int, int,  \
                                    hipStream_t);                                                        \

@@ -30,6 +30,14 @@ template <typename T>
 int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int PH,
                  int PW, int HO, int WO, hipStream_t st);
 template <typename T> int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g, hipStream_t st);
+// Input gradient for at most 4 input channels (one lane per input position; bias
+// and mask optional).  VH_ERR_UNSUPPORTED when the weights exceed 16 KB of fp32.
+bool dgrad_smallc_ok(const ConvGeom& g);
+template <typename T>
+int run_dgrad_smallc(const void* dy, const void* w, const void* bias, const void* mask, void* dx, const ConvGeom& g,
+                     hipStream_t st);
+// y[n][c][hw] += bias[c]
+template <typename T> int run_channel_bias_add(void* y, const void* bias, long N, int C, long HW, hipStream_t st);
 template <typename T> size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len);
 template <typename T>
 int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g, float* ws, int slices,
