@@ -303,6 +303,12 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wt = at(ws, o_w);
+  if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths && d.C <= 4 && act <= 1) {
+    // few input channels: K packed as (c, r, s) instead of 16-channel groups
+    int r = smallc_conv_bf16(x, w, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH, (int)d.KW,
+                             (int)d.PH, (int)d.PW, act, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
     int r = halo_conv_bf16(x, w, 0, wt, bias, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
                            (int)d.KW, (int)d.PH, (int)d.PW, st, act);

@@ -103,6 +103,10 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
 // input gradient of a stride-1 convolution).  ws (O*C*R*S*2 bytes) receives the
 // re-laid-out copy.  Returns VH_ERR_UNSUPPORTED without launching anything when
 // the shape is outside the kernel's envelope.
+// bf16 stride-1 forward for C*R*S <= 128 with K packed as (c, r, s) (vh_smallc.hip);
+// act 0 none, 1 ReLU.  VH_ERR_UNSUPPORTED outside that range.
+int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, int N, int C, int H, int W, int O,
+                     int R, int S, int ph, int pw, int act, hipStream_t st);
 size_t halo_conv_bf16_ws(int C, int O, int R, int S);
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
                    int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st, int act = 0,
