@@ -37,7 +37,7 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 struct HaloArgs {
   const uint16_t* x;     // [N][C][H][W]
-  const uint16_t* wt;    // grouped [C/16][O][R*S][16]
+  const uint16_t* wt;    // grouped [C/16][O][2*R*S+1][8] (last unit zero)
   const uint16_t* bias;  // [O] or nullptr
   uint16_t* y;           // [N][O][P][Q]
   int N, C, H, W, O, P, Q, ph, pw;
@@ -79,8 +79,8 @@ struct HaloCfg {
   static constexpr int WN = 4 / WM;               // waves along positions
   static constexpr int BM = WM * FM * 32;
   static constexpr int BN = WN * FN * 32;
-  static constexpr int WUNITS = BM * RS * 2;      // 16-byte weight units per stage
-  static constexpr int WPU = 2 * RS + 1;          // LDS pitch per output channel (odd: conflict-free)
+  static constexpr int WPU = 2 * RS + 1;          // units per output channel (odd: conflict-free reads)
+  static constexpr int WUNITS = BM * WPU;         // 16-byte weight units per stage
   static constexpr int WITER = (WUNITS + 255) / 256;
   static constexpr int XITER = XI;                // x items per thread per stage (8 dwords each)
 };
@@ -148,7 +148,8 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   extern __shared__ __attribute__((aligned(16))) u32x4 lds_dyn[];
   u32x4* const lds = FUSED ? lds0 : lds_dyn;
 
-  const bool producer = PC && threadIdx.x >= 256;
+  // wave-uniform (scalar) role: the producer branches and loops stay scalar
+  const bool producer = PC && __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6) >= 4;
   const int tid = PC ? (int)(threadIdx.x & 255u) : (int)threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int wm = (wave / Cfg::WN) * FM * 32;  // wave's first output channel in the tile
@@ -248,8 +249,10 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 
   const bool full_o = o0 + BM <= a.O;  // uniform: no per-row checks needed
   // W load items, fixed for the block: byte offset of the 16-byte unit in
-  // channel group 0 (out of range for rows past O) and its LDS unit index
-  const int OG2 = a.O * RS * 2;  // bytes per channel of the grouped weights: group offset = c0 * OG2
+  // channel group 0 (out of range for rows past O) and its LDS unit index.  The
+  // grouped copy has the LDS tile's pitch, so unit u of the tile is unit u of
+  // the LDS stage: consecutive lanes load and store consecutive units.
+  const int OGP = a.O * Cfg::WPU;  // bytes per channel of the grouped weights: group offset = c0 * OGP
   const __amdgpu_buffer_rsrc_t wrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.wt, (short)0, a.w_bytes, 0x00020000);
   int w_goff[Cfg::WITER], w_loff[Cfg::WITER];
@@ -264,12 +267,9 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int it = 0; it < (WD ? 0 : Cfg::WITER); ++it) {
     const int u = tid + it * 256;
-    const int o = u / (RS * 2), rem = u % (RS * 2);
-    const int og = o0 + o;
-    const bool ok = u < Cfg::WUNITS && (full_o || og < a.O);
-    // the tile of one channel group is contiguous: unit u of the block's rows
-    w_goff[it] = ok ? ((o0 * RS * 2 + u) * 16) : (int)0x80000000u;
-    w_loff[it] = u < Cfg::WUNITS ? o * Cfg::WPU + rem : w_units + 2 * cells;  // sink
+    const bool ok = u < Cfg::WUNITS && (full_o || o0 + u / Cfg::WPU < a.O);
+    w_goff[it] = ok ? (o0 * Cfg::WPU + u) * 16 : (int)0x80000000u;
+    w_loff[it] = u < Cfg::WUNITS ? u : w_units + 2 * cells;  // sink
   }
 
   // With two register sets (DEPTH 2) the global loads of channel group kt+2
@@ -287,8 +287,11 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   // Loads of channel group c0 .. c0+15.  Every load is issued (no branches, so
   // the compiler's wait counts stay exact across the pipeline): channels past C
   // and groups past the last one read through the zero-length buffer.
-  auto gload = [&](auto SET, int c0) {
+  auto gload = [&](auto SET, int c0_) {
     constexpr int sI = decltype(SET)::value;
+    // the group's channel offset goes into the scalar offset operand: keep it in
+    // a scalar register (a per-lane value there costs a loop per load)
+    const int c0 = __builtin_amdgcn_readfirstlane(c0_);
     const int crem = a.C - c0;  // channels left from c0 (<= 0 past the last group)
     // groups past the last one (c0 >= C) read zeros through the zero-length
     // buffer: the channel offset is a scalar offset, which is not range-checked
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int it = 0; it < Cfg::WITER; ++it)
         wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                     crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OG2, 0));
+                                                     crem > 0 ? wrsrc : zrsrc, w_goff[it], c0 * OGP, 0));
     }
 #pragma unroll
     for (int it = 0; it < Cfg::XITER; ++it) {
@@ -423,21 +426,42 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       // two register sets: at an even kt set 1 holds group kt+1 and set 0
       // group kt+2 (in flight).  Every load is issued (groups past the last
       // read zeros), so each wait covers only the set about to be stored.
+      // swap: the LDS stores of one register set with the loads of its next
+      // group into the same registers, alternating item by item, so that the
+      // address unit works on this wave's loads while its stores go to LDS.
+      auto swap = [&](auto SET, int st, int c0n) {
+        sstore(SET, st);
+        gload(SET, c0n);
+        constexpr int NW = WD ? 9 : Cfg::WITER;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+        }
+#pragma unroll
+        for (int it = 0; it < Cfg::XITER; ++it) {
+          __builtin_amdgcn_sched_group_barrier(0x200, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);
+        }
+      };
       gload(I0{}, 0);
       gload(I1{}, 16);
       __builtin_amdgcn_sched_barrier(0);
-      sstore(I0{}, 0);
-      gload(I0{}, 32);
+      swap(I0{}, 0, 32);
       __syncthreads();
-      for (int kt = 0; kt < nk; kt += 2) {
-        if (kt + 1 < nk) sstore(I1{}, 1);
-        gload(I1{}, (kt + 3) * 16);
+      int kt = 0;
+      for (; kt + 2 < nk; kt += 2) {
+        swap(I1{}, 1, (kt + 3) * 16);
         __syncthreads();
-        if (kt + 1 >= nk) break;
-        if (kt + 2 < nk) sstore(I0{}, 0);
-        gload(I0{}, (kt + 4) * 16);
+        swap(I0{}, 0, (kt + 4) * 16);
         __syncthreads();
       }
+      // nk - kt (1 or 2) barriers left: one per remaining group of the consumers
+      if (kt + 1 < nk) {
+        sstore(I1{}, 1);
+        __syncthreads();
+      }
+      __syncthreads();
       return;
     }
     __syncthreads();
@@ -865,14 +889,14 @@ static int halo_rows_max(long Mv, int BN, long PQv, int TW, int Hp, int R) {
 
 // Returns VH_ERR_UNSUPPORTED (without launching) when the shape is outside what
 // the halo kernel handles; the caller then uses the generic implicit GEMM.
-size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)((C + 15) / 16 * 16) * O * R * S * 2; }
+size_t halo_conv_bf16_ws(int C, int O, int R, int S) { return (size_t)((C + 15) / 16) * O * (2 * R * S + 1) * 16; }
 
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
                    int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st, int act, const void* mask) {
   const int P = H + 2 * ph - R + 1, Q = W + 2 * pw - S + 1;
   if (P <= 0 || Q <= 0) return VH_ERR_UNSUPPORTED;
   if (C < 1 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
-  const int nk = (C + 15) / 16, Cp = nk * 16;  // channel groups; weights padded with zeros to Cp
+  const int nk = (C + 15) / 16;  // channel groups; the grouped weights are padded with zeros to whole groups
   if (!((R == 3 && S == 3) || (R == 5 && S == 5) || (R == 1 && S == 1))) return VH_ERR_UNSUPPORTED;
   const void* wt = ws;
   HaloArgs a;
@@ -890,7 +914,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   const long yb_ = (long)N * O * P * Q * 2;
   if (yb_ >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.y_bytes = (int)yb_;
-  const long wb = (long)O * R * S * Cp * 2;
+  const long wb = (long)nk * O * (2 * R * S + 1) * 16;
   if (wb >= (1L << 31) - 16) return VH_ERR_UNSUPPORTED;
   a.w_bytes = (int)wb;
   a.fHp = FastDiv((uint32_t)a.Hp);

@@ -445,31 +445,36 @@ __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::s
 
 // Grouped weight layout of the bf16 stride-1 kernel (vh_halo.hip): for a
 // GEMM with M rows (output channels of the convolution the kernel computes) and
-// contraction channels K (multiple of 16), dst[kg][m][tap][16] holds channel
-// 16*kg + i in slot i, so the tile of one 16-channel group and a range of rows
-// is one contiguous run.  mode 0: M = O, K = C, from W[m][k][tap] (forward);
-// mode 1: M = C, K = O, from W[k][m][tap] with the taps rotated 180 degrees
-// (input gradient as a forward convolution).  Walks dst in order.
+// contraction channels K (multiple of 16), dst[kg][m][unit][8] holds, in units
+// 2*tap and 2*tap+1, channels 16*kg + 0..7 and 16*kg + 8..15 of tap `tap`, and
+// zeros in the last unit (2*RS): each row m is 2*RS+1 16-byte units, the pitch
+// the kernel's LDS copy of a weight tile uses, so the tile of one 16-channel
+// group and a range of rows is one contiguous run that lands in LDS unchanged.
+// mode 0: M = O, K = C, from W[m][k][tap] (forward); mode 1: M = C, K = O, from
+// W[k][m][tap] with the taps rotated 180 degrees (input gradient as a forward
+// convolution).  Walks dst in order.
 __global__ __launch_bounds__(256) void relayout_grouped_kernel(const uint16_t* __restrict__ src,
                                                                uint16_t* __restrict__ dst, int M, int K, int RS,
-                                                               int mode, FastDiv fRS, FastDiv fM) {
+                                                               int mode, FastDiv fU, FastDiv fM) {
   // K is padded to whole groups of 16; the padding channels are zero
-  const uint32_t total = (uint32_t)M * ((K + 15) & ~15) * RS;
+  const uint32_t U = 2u * (uint32_t)RS + 1u;  // units per row
+  const uint32_t total = (uint32_t)M * (uint32_t)((K + 15) / 16) * U * 8u;
   for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < total; d += gridDim.x * 256u) {
-    const uint32_t i = d & 15u, t = d >> 4;
-    uint32_t t2, tap, kg, m;
-    fRS.divmod(t, t2, tap);
+    const uint32_t i8 = d & 7u;
+    uint32_t t2, unit, kg, m;
+    fU.divmod(d >> 3, t2, unit);
     fM.divmod(t2, kg, m);
-    const uint32_t k = kg * 16u + i;
-    const uint32_t s = mode == 0 ? (m * (uint32_t)K + k) * RS + tap
-                                 : (k * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap);
-    dst[d] = k < (uint32_t)K ? src[s] : (uint16_t)0;
+    const uint32_t tap = unit >> 1, k = kg * 16u + (unit & 1u) * 8u + i8;
+    uint16_t v = 0;
+    if (unit + 1u < U && k < (uint32_t)K)
+      v = src[mode == 0 ? (m * (uint32_t)K + k) * RS + tap : (k * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap)];
+    dst[d] = v;
   }
 }
 
 int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st) {
-  relayout_grouped_kernel<<<grid_for((long)M * ((K + 15) / 16 * 16) * RS), 256, 0, st>>>(
-      (const uint16_t*)w, (uint16_t*)dst, M, K, RS, mode, FastDiv((uint32_t)RS), FastDiv((uint32_t)M));
+  relayout_grouped_kernel<<<grid_for((long)M * ((K + 15) / 16) * (2 * RS + 1) * 8), 256, 0, st>>>(
+      (const uint16_t*)w, (uint16_t*)dst, M, K, RS, mode, FastDiv((uint32_t)(2 * RS + 1)), FastDiv((uint32_t)M));
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
