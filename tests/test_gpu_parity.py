@@ -263,12 +263,15 @@ HALO_CASES = [
     (4, 18, 17, 256, 256, 3, 1, 1),  # the same over column strips (no vector epilogue)
     (2, 3, 64, 20, 24, 5, 1, 2),     # 3 input channels, 5x5: one partial group, one LDS stage
     (1, 5, 20, 8, 10, 3, 1, 1),      # C = 5 forward; input gradient over 20 = 16 + 4 channels
+    (3, 48, 64, 30, 30, 3, 1, 1),    # W % 8 != 0: halo kernel for a shape the resident-weight kernel declines
+    (2, 48, 64, 24, 32, 3, 1, 1),    # resident weights: three channel groups, tiles across images
+    (3, 64, 40, 16, 24, 3, 1, 1),    # resident weights, O = 40: partly empty 64-row tile
+    (2, 40, 24, 20, 16, 3, 1, 1),    # resident weights, C = 40: partial channel group (grouped copy)
+    (1, 64, 64, 16, 16, 3, 1, 1),    # one tile per block (fewer tiles than CUs)
 ]
 
 
-@pytest.mark.parametrize("case", HALO_CASES, ids=_conv_ids)
-@pytest.mark.parametrize("policy", [volta_amd._lib.POLICY_FASTEST, volta_amd._lib.POLICY_GENERIC])
-def test_conv2d_bf16_fast_and_generic_paths(case, policy):
+def _bf16_conv_case(case, policy):
     B, C, O, H, W, K, S, P = case
     dt = "bf16"
     volta_amd.check(volta_amd.lib().vh_set_kernel_policy(policy))
@@ -293,6 +296,24 @@ def test_conv2d_bf16_fast_and_generic_paths(case, policy):
         check(db, oracle.conv_bias_grad, (dy,), dt, "db", k=kwg)
     finally:
         volta_amd.check(volta_amd.lib().vh_set_kernel_policy(volta_amd._lib.POLICY_FASTEST))
+
+
+@pytest.mark.parametrize("case", HALO_CASES, ids=_conv_ids)
+@pytest.mark.parametrize("policy", [volta_amd._lib.POLICY_FASTEST, volta_amd._lib.POLICY_GENERIC])
+def test_conv2d_bf16_fast_and_generic_paths(case, policy):
+    _bf16_conv_case(case, policy)
+
+
+# 3x3 stride-1 shapes with at most 64 input and output channels: the
+# resident-weight kernel takes the masked input gradient by default;
+# VOLTA_HIP_WRES=1 sends every shape in its envelope there (the others fall back).
+WRES_CASES = [c for c in HALO_CASES if c[5] == 3 and c[6] == 1 and c[1] <= 64 and c[2] <= 64]
+
+
+@pytest.mark.parametrize("case", WRES_CASES, ids=_conv_ids)
+def test_conv2d_bf16_3x3_resident_weight_kernel(case, monkeypatch):
+    monkeypatch.setenv("VOLTA_HIP_WRES", "1")
+    _bf16_conv_case(case, volta_amd._lib.POLICY_FASTEST)
 
 
 # ------------------------------------------------------------------ ConvTranspose2d
@@ -475,6 +496,15 @@ def test_conv2d_fused_relu_fwd_and_masked_dgrad(case, algo, dt):
     kwg = k_conv_wgrad(B, got.shape[2], got.shape[3])
     check(dw, oracle.direct_conv_backward_weight, (dy, x, w.shape), dt, "dw", kw, k=kwg)
     check(db, oracle.conv_bias_grad, (dy,), dt, "db", k=kwg)
+
+
+@pytest.mark.parametrize("case", [c for c in RELU_CASES if c[5] == 3 and c[6] == 1 and c[1] <= 64 and c[2] <= 64]
+                         + [(2, 64, 64, 20, 24, 3, 1, 1), (3, 32, 64, 16, 32, 3, 1, 1), (2, 64, 32, 24, 16, 3, 1, 1),
+                            (2, 27, 32, 12, 16, 3, 1, 1)], ids=_conv_ids)
+@pytest.mark.parametrize("wres", ["0", "1"])
+def test_conv2d_bf16_fused_relu_both_3x3_kernels(case, wres, monkeypatch):
+    monkeypatch.setenv("VOLTA_HIP_WRES", wres)
+    test_conv2d_fused_relu_fwd_and_masked_dgrad(case, vnn.ConvAlgo.IGEMM, "bf16")
 
 
 # ------------------------------------------------------------------ the step after dW

@@ -93,24 +93,40 @@ int run_sum_partials(const float* part, int splits, long n, void* out, hipStream
 template <typename T>
 int run_pixel_shuffle(const void* in, void* out, int B, int C, int H, int W, int r, int backward, hipStream_t st);
 
-// Grouped bf16 weight layout [K/16][M][RS][16] of the halo kernel (vh_kernels.hip).
+// Grouped bf16 weight layout [K/16][M][2*RS+1][8] of the halo kernels
+// (vh_kernels.hip): units 2*tap and 2*tap+1 hold channels 0-7 and 8-15 of a
+// 16-channel group, the last unit is zero.
 int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st);
+
+// bf16 stride-1 forward for C*R*S <= 128 with K packed as (c, r, s) (vh_smallc.hip);
+// act 0 none, 1 ReLU.  VH_ERR_UNSUPPORTED outside that range.
+int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, int N, int C, int H, int W, int O,
+                     int R, int S, int ph, int pw, int act, hipStream_t st);
 
 // ---- stride-1 bf16 halo convolution (vh_halo.hip) ----
 // Computes y = conv(x, W') with C input and O output channels, where W' is
 // taken from the OIHW weight w: w_mode 0 uses w as is (w is [O][C][R][S]);
 // w_mode 1 uses w transposed and rotated 180 degrees (w is [C][O][R][S]: the
-// input gradient of a stride-1 convolution).  ws (O*C*R*S*2 bytes) receives the
-// re-laid-out copy.  Returns VH_ERR_UNSUPPORTED without launching anything when
-// the shape is outside the kernel's envelope.
-// bf16 stride-1 forward for C*R*S <= 128 with K packed as (c, r, s) (vh_smallc.hip);
-// act 0 none, 1 ReLU.  VH_ERR_UNSUPPORTED outside that range.
-int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, int N, int C, int H, int W, int O,
-                     int R, int S, int ph, int pw, int act, hipStream_t st);
+// input gradient of a stride-1 convolution).  ws (halo_conv_bf16_ws bytes)
+// receives the grouped copy.  Returns VH_ERR_UNSUPPORTED without launching
+// anything when the shape is outside the kernel's envelope.
 size_t halo_conv_bf16_ws(int C, int O, int R, int S);
 int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
                    int H, int W, int O, int R, int S, int ph, int pw, hipStream_t st, int act = 0,
                    const void* mask = nullptr);
+// Most ext rows (padded input rows, R - 1 halo rows included) any block of BN
+// consecutive positions spans, positions in virtual images of P x TW (PQv) over
+// Hp ext rows each; Mv positions in all.  Cached per shape.
+int halo_rows_max(long Mv, int BN, long PQv, int TW, int Hp, int R);
+
+// ---- 3x3 stride-1 bf16 convolution with resident weights (vh_wres.hip) ----
+// C <= 64 and O <= 64, W and the output width even; w and w_mode as for
+// halo_conv_bf16 (the forward with C % 16 == 0 reads w itself, every other case
+// writes the grouped copy into ws, halo_conv_bf16_ws bytes).  act 0 none,
+// 1 ReLU, 2 zero where mask (laid out like y) is not positive.
+// VH_ERR_UNSUPPORTED without launching outside that envelope.
+int wres_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const void* bias, void* y, int N, int C,
+                   int H, int W, int O, int ph, int pw, hipStream_t st, int act, const void* mask);
 
 // ---- stride-1 bf16 weight gradient (vh_wgrad.hip) ----
 // Workspace bytes needed (0 if the shape is outside the kernel's envelope).
