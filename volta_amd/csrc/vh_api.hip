@@ -707,7 +707,18 @@ static int dense_bf16(int ak, int bk, const void* a, int lda, const void* b, int
                       long N, long K, const void* bias, hipStream_t st) {
   const bool at = ak == KD_DENSE_MN, bt = bk == KD_DENSE_MN;
   if (!dense_bf16_ok(M, N, K, at, lda, bt, ldb, ldc, a, b, c)) return VH_ERR_UNSUPPORTED;
+  // a grid of few tiles over a long K: the split-K implicit GEMM fills the chip instead
+  if (((M + 127) / 128) * ((N + 127) / 128) < 64 && K > 2048) return VH_ERR_UNSUPPORTED;
   return dense_bf16_gemm(a, lda, at, b, ldb, bt, c, ldc, (int)M, (int)N, (int)K, bias, st);
+}
+
+static int dense_f32(int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc, long M,
+                     long N, long K, const void* bias, hipStream_t st) {
+  const bool at = ak == KD_DENSE_MN, bt = bk == KD_DENSE_MN;
+  if (!dense_f32_ok(M, N, K, at, lda, bt, ldb, ldc, a, b, c)) return VH_ERR_UNSUPPORTED;
+  // a grid of few tiles over a long K: the split-K implicit GEMM fills the chip instead
+  if (((M + 63) / 64) * ((N + 127) / 128) < 128 && K > 1024) return VH_ERR_UNSUPPORTED;
+  return dense_f32_gemm(a, lda, at, b, ldb, bt, c, ldc, (int)M, (int)N, (int)K, bias, st);
 }
 
 static int gemm(int dt, int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc,
@@ -715,6 +726,10 @@ static int gemm(int dt, int ak, int bk, const void* a, int lda, const void* b, i
   VH_TRY(check_sizes({M * K, K * N, M * N}));
   if (dt == VH_BF16 && g_fast_paths && (bias == nullptr || bias_mode == 2)) {
     int r = dense_bf16(ak, bk, a, lda, b, ldb, c, ldc, M, N, K, bias, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
+  if (dt == VH_F32 && g_fast_paths && (bias == nullptr || bias_mode == 2)) {
+    int r = dense_f32(ak, bk, a, lda, b, ldb, c, ldc, M, N, K, bias, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
   }
   IgemmPlan p{};

@@ -144,6 +144,11 @@ bool dense_bf16_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb,
                    const void* b, const void* c);
 int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
                     int N, int K, const void* bias, hipStream_t st);
+// The same in fp32 (vh_dense_f32.hip): K % 4 == 0, 16-byte aligned A and B.
+bool dense_f32_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, long ldc, const void* a,
+                  const void* b, const void* c);
+int dense_f32_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
+                   int N, int K, const void* bias, hipStream_t st);
 
 // ---- strided 1x1 bf16 convolutions, pad 0 (vh_pointwise.hip) ----
 // w is the OIHW weight itself ([O][C]).  Each returns VH_ERR_UNSUPPORTED
