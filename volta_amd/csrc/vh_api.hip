@@ -384,6 +384,13 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
   VH_TRY(VH_DISPATCH(dt, run_relayout_phase, w, at(ws, o_w), (int)d.O, (int)d.C, (int)d.KH, (int)d.KW, SH, SW, tab,
                      st));
   const int vec = dt == VH_BF16 ? 8 : 4;
+  // Phases of one shape (every phase has taps, equal extents): one launch with
+  // the phase in blockIdx.y, when the phases' tiles together fill the chip
+  // without split K.
+  bool uniform = ph.size() >= 2 && ph.size() <= 4;
+  for (size_t pi = 0; uniform && pi < ph.size(); ++pi)
+    uniform = ph[pi].Rc > 0 && ph[pi].Sc > 0 && ph[pi].Rc == ph[0].Rc && ph[pi].Sc == ph[0].Sc &&
+              ph[pi].Hc == ph[0].Hc && ph[pi].Wc == ph[0].Wc;
   for (size_t pi = 0; pi < ph.size(); ++pi) {
     const DgradPhase& f = ph[pi];
     const int K = f.Rc * f.Sc * (int)d.O;
@@ -413,9 +420,18 @@ static int dgrad_phases(int dt, const void* dy, const void* w, const void* bias,
     p.args.act = mask ? 2 : 0;
     p.args.mask = mask;
     p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
-    igemm_prepare(p);
     p.args.a = Operand{wp, std::max(K, 1), (int)d.C, (K % vec) == 0};
     p.args.b = Operand{dy, 0, p.args.N, 0};
+    if (uniform && pi == 0 && pick_splits(p.args.M, p.args.N * (int)ph.size(), p.args.K, dt) == 1) {
+      p.splits = 1;
+      p.args.nphase = (int)ph.size();
+      for (size_t q = 0; q < ph.size(); ++q)
+        p.args.ph[q] = PhaseArg{at(ws, o_w + (size_t)tab.off[q] * elem_size(dt)), ph[q].offa, ph[q].offb, ph[q].a,
+                                ph[q].b};
+      igemm_prepare(p);
+      return run_igemm(p, (float*)at(ws, o_g), st);
+    }
+    igemm_prepare(p);
     VH_TRY(run_igemm(p, (float*)at(ws, o_g), st));
   }
   return VH_OK;

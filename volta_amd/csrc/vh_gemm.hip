@@ -29,7 +29,8 @@ struct Tile {
   int bm, bn;
 };
 
-Tile pick_tile(int M, int N, int dtype = VH_F32) {
+// nphase: launches of several stride phases at once multiply the grid
+Tile pick_tile(int M, int N, int dtype = VH_F32, int nphase = 1) {
   Tile t{128, 128};
   if (M <= 64) t.bm = 64;
   // f32 (16x16 MFMA tiles) also has 32-row tiles: a 32-channel output would
@@ -37,8 +38,10 @@ Tile pick_tile(int M, int N, int dtype = VH_F32) {
   if (M <= 32 && dtype == VH_F32) t.bm = 32;
   if (N <= 64) t.bn = 64;
   // f32 blocks are latency-bound with one block per CU: narrower tiles when the
-  // wide ones would not give every CU two blocks
-  if (dtype == VH_F32 && t.bn == 128 && (long)((M + t.bm - 1) / t.bm) * ((N + 127) / 128) < 512) t.bn = 64;
+  // wide ones would not give every CU two blocks (then lower ones, where those do)
+  auto grid = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn) * std::max(1, nphase); };
+  if (dtype == VH_F32 && t.bn == 128 && grid(t.bm, 128) < 512) t.bn = 64;
+  if (dtype == VH_F32 && t.bm == 128 && grid(128, t.bn) < 512 && grid(64, t.bn) >= 512) t.bm = 64;
   return t;
 }
 
@@ -46,7 +49,7 @@ template <typename T, int AK, int BKIND, int OUT, int BM, int BN, int BK = bk_fo
 int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
   IgemmArgs a = p.args;
   const int tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-  dim3 grid((unsigned)tiles, 1, (unsigned)p.splits);
+  dim3 grid((unsigned)tiles, (unsigned)std::max(1, a.nphase), (unsigned)p.splits);
   if (p.f32_out) {  // fp32 row-major result, one split
     IgemmArgs pa = a;
     pa.d = ws;
@@ -70,7 +73,7 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
 
 template <typename T, int AK, int BKIND, int OUT>
 int launch_kinds(IgemmPlan& p, float* ws, hipStream_t st) {
-  Tile t = pick_tile(p.args.M, p.args.N, std::is_same<T, float>::value ? VH_F32 : VH_BF16);
+  Tile t = pick_tile(p.args.M, p.args.N, std::is_same<T, float>::value ? VH_F32 : VH_BF16, p.args.nphase);
   if constexpr (std::is_same<T, float>::value) {
     // 32-row tiles take 32-deep K steps so that all 256 threads have a load unit
     if (t.bm == 32 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 32, 128, 32>(p, ws, st);

@@ -13,6 +13,8 @@
 // pitch BK+PADK elements = 80 bytes) and is double-buffered: global loads for
 // step k+1 are in flight while the MFMAs of step k run.
 #pragma once
+#include <type_traits>
+
 #include "vh_common.hpp"
 
 namespace vh {
@@ -49,6 +51,13 @@ struct Operand {
   int vec_ok;  // dense K-major: 16-byte vector loads allowed (aligned ld/base)
 };
 
+// One stride phase of a multi-phase launch (blockIdx.y): its A operand, the
+// gather's padding and the output phase (OK_NCHW_SUB).
+struct PhaseArg {
+  const void* a;
+  int offa, offb, sub_a, sub_b;
+};
+
 struct IgemmArgs {
   int M, N, K;
   Operand a, b;
@@ -66,6 +75,8 @@ struct IgemmArgs {
   int act;           // epilogue: 0 none, 1 ReLU, 2 zero where mask <= 0 (mask laid out like d)
   const void* mask;
   ConvGeom g;
+  int nphase;        // > 1: blockIdx.y selects ph[blockIdx.y] (same M, N, K for every phase)
+  PhaseArg ph[4];
 };
 
 // ---------------------------------------------------------------- operand loaders
@@ -259,6 +270,20 @@ template <> struct Mma<bf16> {
   __device__ static inline int acc_col(int lane) { return lane & 31; }
 };
 
+// fp32, 32 x 32 tiles (v_mfma_f32_32x32x2_f32): for block tiles of at least
+// 64 x 64; the same fragment and accumulator layout as the bf16 32 x 32 tile
+struct MmaF32x32 {
+  static constexpr int TM = 32, TN = 32, TK = 2, NACC = 16;
+  using acc_t = f32x16;
+  __device__ static inline int frag_row(int lane) { return lane & 31; }
+  __device__ static inline int frag_k(int lane) { return lane >> 5; }
+  __device__ static inline acc_t mma(const float* a, const float* b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(*a, *b, c, 0, 0, 0);
+  }
+  __device__ static inline int acc_row(int lane, int v) { return (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3); }
+  __device__ static inline int acc_col(int lane) { return lane & 31; }
+};
+
 template <> struct Mma<float> {
   static constexpr int TM = 16, TN = 16, TK = 4, NACC = 4;
   using acc_t = f32x4;
@@ -323,11 +348,25 @@ __device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int co
 
 // ---------------------------------------------------------------- the kernel
 template <typename T, int AK, int BKIND, int OUT, int BM, int BN, int BK>
-__global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
+__global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args_in) {
+  IgemmArgs args = args_in;
+  if (args.nphase > 1) {
+    const PhaseArg& f = args_in.ph[blockIdx.y];
+    args.a.p = f.a;
+    args.g.ph = f.offa;
+    args.g.pw = f.offb;
+    args.sub_a = f.sub_a;
+    args.sub_b = f.sub_b;
+  }
   using S = typename Elem<T>::storage;
-  using MM = Mma<T>;
+  // fp32 tiles of at least 64 x 64 use the 32 x 32 fp32 MFMA: its fragment
+  // (32 rows of one k per half-wave) is conflict-free with a row pitch of
+  // BK + 2 floats (32 rows land on the 32 even banks, k + 1 on the odd ones);
+  // the 16-byte units are then stored as two 8-byte halves
+  constexpr bool F32_32 = std::is_same<T, float>::value && BM >= 64 && BN >= 64;
+  using MM = std::conditional_t<F32_32, MmaF32x32, Mma<T>>;
   constexpr int VEC = Elem<T>::vec;
-  constexpr int PADK = VEC;            // row pitch (BK + VEC) elements
+  constexpr int PADK = F32_32 ? 2 : VEC;  // row pitch (BK + PADK) elements
   constexpr int LDK = BK + PADK;
   constexpr int KU = BK / VEC;         // units per row per K step
   constexpr int UA = BM * KU / 256;    // units per thread, A
@@ -386,15 +425,21 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args) {
 #pragma unroll
     for (int u = 0; u < UB; ++u) lb[u].load(args.b, args.g, k0 + b_k[u], ke, rb[u]);
   };
+  auto st16 = [&](S* dst, const S* src) {
+    if constexpr (F32_32) {
+      reinterpret_cast<uint2*>(dst)[0] = reinterpret_cast<const uint2*>(src)[0];
+      reinterpret_cast<uint2*>(dst)[1] = reinterpret_cast<const uint2*>(src)[1];
+    } else {
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+    }
+  };
   auto sstore = [&](int buf) {
     S* a = As + buf * BM * LDK;
     S* b = Bs + buf * BN * LDK;
 #pragma unroll
-    for (int u = 0; u < UA; ++u)
-      *reinterpret_cast<uint4*>(a + a_r[u] * LDK + a_k[u]) = *reinterpret_cast<const uint4*>(ra[u]);
+    for (int u = 0; u < UA; ++u) st16(a + a_r[u] * LDK + a_k[u], ra[u]);
 #pragma unroll
-    for (int u = 0; u < UB; ++u)
-      *reinterpret_cast<uint4*>(b + b_r[u] * LDK + b_k[u]) = *reinterpret_cast<const uint4*>(rb[u]);
+    for (int u = 0; u < UB; ++u) st16(b + b_r[u] * LDK + b_k[u], rb[u]);
   };
 
   typename MM::acc_t acc[FM][FN];
