@@ -418,12 +418,15 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args_in) {
     lb[u].init(args.b, args.g, n0 + b_r[u]);
   }
 
-  S ra[UA][VEC], rb[UB][VEC];
-  auto gload = [&](int k0) {
+  // fp32: two register sets, the loads of stage k+3 issued after the MFMAs of
+  // stage k (every load has two stages of MFMAs to arrive); bf16 uses set 0 only
+  S ra[2][UA][VEC], rb[2][UB][VEC];
+  auto gload = [&](auto SET, int k0) {
+    constexpr int s = decltype(SET)::value;
 #pragma unroll
-    for (int u = 0; u < UA; ++u) la[u].load(args.a, args.g, k0 + a_k[u], ke, ra[u]);
+    for (int u = 0; u < UA; ++u) la[u].load(args.a, args.g, k0 + a_k[u], ke, ra[s][u]);
 #pragma unroll
-    for (int u = 0; u < UB; ++u) lb[u].load(args.b, args.g, k0 + b_k[u], ke, rb[u]);
+    for (int u = 0; u < UB; ++u) lb[u].load(args.b, args.g, k0 + b_k[u], ke, rb[s][u]);
   };
   auto st16 = [&](S* dst, const S* src) {
     if constexpr (F32_32) {
@@ -433,13 +436,14 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args_in) {
       *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](auto SET, int buf) {
+    constexpr int s = decltype(SET)::value;
     S* a = As + buf * BM * LDK;
     S* b = Bs + buf * BN * LDK;
 #pragma unroll
-    for (int u = 0; u < UA; ++u) st16(a + a_r[u] * LDK + a_k[u], ra[u]);
+    for (int u = 0; u < UA; ++u) st16(a + a_r[u] * LDK + a_k[u], ra[s][u]);
 #pragma unroll
-    for (int u = 0; u < UB; ++u) st16(b + b_r[u] * LDK + b_k[u], rb[u]);
+    for (int u = 0; u < UB; ++u) st16(b + b_r[u] * LDK + b_k[u], rb[s][u]);
   };
 
   typename MM::acc_t acc[FM][FN];
@@ -450,15 +454,8 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args_in) {
 #pragma unroll
       for (int v = 0; v < MM::NACC; ++v) acc[i][j][v] = 0.f;
 
-  if (nk > 0) {
-    gload(kb);
-    sstore(0);
-  }
-  __syncthreads();
   const int fr = MM::frag_row(lane), fk = MM::frag_k(lane);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) gload(kb + (kt + 1) * BK);
+  auto compute = [&](int buf) {
     const S* a = As + buf * BM * LDK;
     const S* b = Bs + buf * BN * LDK;
 #pragma unroll
@@ -470,8 +467,48 @@ __global__ __launch_bounds__(256) void igemm_kernel(IgemmArgs args_in) {
           acc[i][j] = MM::mma(a + (wm + i * MM::TM + fr) * LDK + kk + fk,
                               b + (wn + j * MM::TN + fr) * LDK + kk + fk, acc[i][j]);
     }
-    if (kt + 1 < nk) sstore(buf ^ 1);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  if constexpr (std::is_same<T, float>::value) {
+    // fp32: register set s holds stages s, s+2, ...; LDS buffer k & 1 holds
+    // stage k.  Loads past the block's K range read zeros (never multiplied).
+    if (nk > 0) {
+      gload(I0{}, kb);
+      gload(I1{}, kb + BK);
+      sstore(I0{}, 0);
+      gload(I0{}, kb + 2 * BK);
+    }
     __syncthreads();
+    int kt = 0;
+    for (; kt + 1 < nk; kt += 2) {
+      compute(0);
+      sstore(I1{}, 1);
+      gload(I1{}, kb + (kt + 3) * BK);
+      __syncthreads();
+      compute(1);
+      if (kt + 2 < nk) {
+        sstore(I0{}, 0);
+        gload(I0{}, kb + (kt + 4) * BK);
+      }
+      __syncthreads();
+    }
+    if (kt < nk) compute(0);  // odd stage count: the last stage is in buffer 0
+  } else {
+    // bf16 (16-bit elements take a register each): one register set, the loads
+    // of stage k+1 in flight during the MFMAs of stage k
+    if (nk > 0) {
+      gload(I0{}, kb);
+      sstore(I0{}, 0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      if (kt + 1 < nk) gload(I0{}, kb + (kt + 1) * BK);
+      compute(buf);
+      if (kt + 1 < nk) sstore(I0{}, buf ^ 1);
+      __syncthreads();
+    }
   }
 
   // the act-2 mask values are read before the first store (a load may not pass
