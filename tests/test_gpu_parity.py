@@ -150,6 +150,8 @@ CONV_CASES = [
     (2, 8, 16, 10, 10, 1, 2, 0),     # 1x1 stride 2: odd input phases get no taps (zeros)
     (2, 3, 16, 10, 10, 4, 2, 1),     # 3 input channels, stride 2: input gradient one lane per position
     (2, 4, 8, 9, 11, 3, 3, 2),       # 4 input channels, stride 3
+    (2, 2, 8, 17, 16, 4, 2, 1),      # 4x4 stride 2 pad 1, 2 input channels: cell-wise input gradient, odd height
+    (1, 4, 6, 16, 17, 4, 2, 1),      # the same with 4 input channels, odd width (a cell past the last dY column)
 ]
 
 
@@ -329,6 +331,9 @@ CT_CASES = [
     (2, 8, 2, 5, 5, 3, 1, 1),        # 2 output channels, stride 1 (one lane per output position)
     (3, 6, 1, 4, 6, 4, 2, 1),        # 1 output channel
     (2, 16, 4, 1, 1, 3, 1, 0),       # 1x1 input: the layer is one product
+    (2, 8, 1, 8, 4, 4, 2, 1),        # k4 s2 p1 to 1 channel: cell-wise kernel, one 4-wide load per dY row
+    (2, 12, 4, 6, 8, 4, 2, 1),       # k4 s2 p1 to 4 channels
+    (3, 10, 2, 5, 12, 4, 2, 1),      # k4 s2 p1 to 2 channels, 10 input channels (uneven split over waves)
 ]
 
 
@@ -462,6 +467,7 @@ RELU_CASES = [
     (2, 64, 128, 16, 16, 1, 2, 0),   # strided 1x1 (bf16 pointwise kernels: separate ReLU pass)
     (2, 16, 24, 11, 9, 3, 2, 1),     # strided 3x3: stride phases
     (2, 1, 32, 12, 12, 3, 1, 1),     # one input channel (MI355X selector: direct)
+    (2, 3, 16, 16, 17, 4, 2, 1),     # k4 s2 p1, 3 input channels: masked cell-wise input gradient
 ]
 
 

@@ -164,6 +164,224 @@ __global__ __launch_bounds__(256) void dgrad_smallc_kernel(const typename Elem<T
   }
 }
 
+// Tap offsets of one axis of a fixed geometry (taps K, stride ST, padding PD)
+// seen from cells: a cell t covers input positions ST*t + e, e < ST.  Position
+// e reaches taps k = a(e) + ST*j, j < nj(e), and reads output index
+// t + base(e) - j there; dmin..dmax is the span of those offsets over the cell.
+template <int K, int ST, int PD> struct CellAxis {
+  static constexpr int a(int e) { return (e + PD) % ST; }
+  static constexpr int base(int e) { return (e + PD) / ST; }
+  static constexpr int nj(int e) { return a(e) < K ? (K - a(e) + ST - 1) / ST : 0; }
+  static constexpr int dmin() {
+    int m = 1 << 20;
+    for (int e = 0; e < ST; ++e)
+      if (nj(e) && base(e) - nj(e) + 1 < m) m = base(e) - nj(e) + 1;
+    return m;
+  }
+  static constexpr int dmax() {
+    int m = -(1 << 20);
+    for (int e = 0; e < ST; ++e)
+      if (nj(e) && base(e) > m) m = base(e);
+    return m;
+  }
+};
+
+// dY loads of the cell kernel: buffer loads, so an offset of kCellOOR (past
+// any tensor the launch accepts) reads zeros without a branch.
+constexpr uint32_t kCellOOR = 0x80000000u;
+template <typename T> struct CellLoad;
+template <> struct CellLoad<float> {
+  static __device__ inline void four(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float* v) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 u = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
+    v[0] = u.x, v[1] = u.y, v[2] = u.z, v[3] = u.w;
+  }
+  static __device__ inline float one(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+  }
+};
+template <> struct CellLoad<bf16> {
+  static __device__ inline void four(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float* v) {
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    const u2 u = __builtin_bit_cast(u2, __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0));
+    v[0] = __uint_as_float(u.x << 16), v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16), v[3] = __uint_as_float(u.y & 0xffff0000u);
+  }
+  static __device__ inline float one(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0) << 16);
+  }
+};
+
+// Input gradient with at most 4 input channels for one fixed tap geometry
+// (R, S, stride and padding known at compile time).  A lane owns one cell row
+// and four cell columns of one image, a cell being the SH x SW block of input
+// positions that together read dY rows t + dmin..dmax and columns v +
+// dmin..dmax of the axis; each dY value it loads (one 4-wide load for the
+// cells' own columns, single loads for the rest) feeds every tap of every
+// position that reads it.  The four waves of a block own the same cells and
+// split the output channels; waves 1-3 hand their sums to wave 0 through LDS,
+// which adds bias, applies the ReLU-backward mask and stores.  Weights are
+// uniform across the block (scalar loads).  fp32 accumulation, one rounding.
+template <typename T, int C, int R, int S, int SH, int SW, int PH, int PW>
+__global__ __launch_bounds__(256) void dgrad_cell_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                         const typename Elem<T>::storage* __restrict__ w,
+                                                         const typename Elem<T>::storage* __restrict__ bias,
+                                                         const typename Elem<T>::storage* __restrict__ mask,
+                                                         typename Elem<T>::storage* __restrict__ dx, ConvGeom g,
+                                                         int ncq, int nct, long nlanes) {
+  using RA = CellAxis<R, SH, PH>;
+  using CA = CellAxis<S, SW, PW>;
+  constexpr int R0 = RA::dmin(), NR = RA::dmax() - R0 + 1;
+  constexpr int C0 = CA::dmin(), NCOL = 4 + CA::dmax() - C0;
+  static_assert(C0 <= 0 && R0 <= 0, "cell offsets must include the cell's own row and column");
+  constexpr int NOUT = SH * 4 * SW * C, KW = C * R * S;
+  static_assert(std::is_same<T, float>::value || KW % 2 == 0, "bf16 weights are read in pairs");
+  __shared__ float red[4][3][SH * SW * C][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long gl = (long)blockIdx.x * 64 + lane;
+  const bool active = gl < nlanes;
+  const int vq = (int)(gl % ncq);
+  const long rest = gl / ncq;
+  const int t = (int)(rest % nct), n = (int)(rest / nct);
+  const int v0 = 4 * vq;
+  const long PQ = (long)g.P * g.Q;
+  const int ow = (g.O + 3) / 4, o_beg = wv * ow, o_end = min(g.O, o_beg + ow);
+
+  float acc[NOUT];
+#pragma unroll
+  for (int k = 0; k < NOUT; ++k) acc[k] = 0.f;
+  // byte offsets of the lane's dY values in channel 0 of its image; channel o
+  // adds o * P * Q elements through the scalar offset
+  constexpr int ES = sizeof(typename Elem<T>::storage);
+  constexpr int NEDGE = NCOL - 4;
+  uint32_t off_mid[NR], off_edge[NR][NEDGE > 0 ? NEDGE : 1];
+  {
+    const long img = (long)(active ? n : 0) * g.O * PQ;
+#pragma unroll
+    for (int rr = 0; rr < NR; ++rr) {
+      const int p = t + R0 + rr;
+      const bool rowok = active && p >= 0 && p < g.P;
+      const long row = img + (long)p * g.Q;
+      off_mid[rr] = rowok && v0 < g.Q ? (uint32_t)((row + v0) * ES) : kCellOOR;
+#pragma unroll
+      for (int e = 0, cc = 0; cc < NCOL; ++cc) {
+        const int dq = C0 + cc;
+        if (dq >= 0 && dq < 4) continue;
+        const int q = v0 + dq;
+        off_edge[rr][e++] = rowok && q >= 0 && q < g.Q ? (uint32_t)((row + q) * ES) : kCellOOR;
+      }
+    }
+  }
+  const __amdgpu_buffer_rsrc_t rsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void*)dy, (short)0, (int)((long)g.N * g.O * PQ * ES), 0x00020000);
+  auto load = [&](int o, float (&d)[NR][NCOL]) {
+    const uint32_t so = (uint32_t)((long)o * PQ * ES);
+#pragma unroll
+    for (int rr = 0; rr < NR; ++rr) {
+      float m4[4];
+      CellLoad<T>::four(rsrc, off_mid[rr], so, m4);
+#pragma unroll
+      for (int e = 0, cc = 0; cc < NCOL; ++cc) {
+        const int dq = C0 + cc;
+        if (dq >= 0 && dq < 4) d[rr][cc] = m4[dq];
+        else d[rr][cc] = CellLoad<T>::one(rsrc, off_edge[rr][e++], so);
+      }
+    }
+  };
+
+  auto compute = [&](int o, const float (&d)[NR][NCOL]) {
+    float wk[KW];
+    if constexpr (std::is_same<T, float>::value) {
+#pragma unroll
+      for (int i = 0; i < KW; ++i) wk[i] = w[(long)o * KW + i];
+    } else {
+      const uint32_t* w32 = reinterpret_cast<const uint32_t*>(w) + (long)o * (KW / 2);
+#pragma unroll
+      for (int i = 0; i < KW / 2; ++i) {
+        const uint32_t u = w32[i];
+        wk[2 * i] = __uint_as_float(u << 16), wk[2 * i + 1] = __uint_as_float(u & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int er = 0; er < SH; ++er)
+#pragma unroll
+      for (int j = 0; j < RA::nj(er); ++j) {
+        const int r = RA::a(er) + SH * j, rr = RA::base(er) - j - R0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int ec = 0; ec < SW; ++ec)
+#pragma unroll
+            for (int i = 0; i < CA::nj(ec); ++i) {
+              const int s = CA::a(ec) + SW * i, cc = k + CA::base(ec) - i - C0;
+#pragma unroll
+              for (int c = 0; c < C; ++c)
+                acc[((er * 4 + k) * SW + ec) * C + c] =
+                    fmaf(d[rr][cc], wk[(c * R + r) * S + s], acc[((er * 4 + k) * SW + ec) * C + c]);
+            }
+      }
+  };
+
+  // two register sets: the loads of channel o + 1 are in flight while o is
+  // summed (the last one repeats a channel instead of branching)
+  float da[NR][NCOL], db[NR][NCOL];
+  int o = o_beg;
+  if (o < o_end) load(o, da);
+  for (; o + 1 < o_end; o += 2) {
+    load(o + 1, db);
+    compute(o, da);
+    load(min(o + 2, o_end - 1), da);
+    compute(o + 1, db);
+  }
+  if (o < o_end) compute(o, da);
+
+  // wave k finishes cell column k of the lane: the other three waves hand it
+  // their sums for that column through LDS
+  constexpr int NCELL = SH * SW * C;  // outputs per cell
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    if (k == wv) continue;
+    const int slot = wv < k ? wv : wv - 1;
+#pragma unroll
+    for (int er = 0; er < SH; ++er)
+#pragma unroll
+      for (int j = 0; j < SW * C; ++j) red[k][slot][er * SW * C + j][lane] = acc[(er * 4 + k) * SW * C + j];
+  }
+  __syncthreads();
+  if (!active) return;
+  auto finish = [&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    const int iw0 = SW * (v0 + k);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const float bc = bias ? Elem<T>::to_f32(bias[c]) : 0.f;
+#pragma unroll
+      for (int er = 0; er < SH; ++er) {
+        const int ih = SH * t + er;
+        if (ih >= g.H) continue;
+        const long row = (((long)n * C + c) * g.H + ih) * g.W;
+#pragma unroll
+        for (int ec = 0; ec < SW; ++ec) {
+          const int iw = iw0 + ec, j = (er * SW + ec) * C + c;
+          if (iw >= g.W) continue;
+          float val = acc[(er * 4 + k) * SW * C + ec * C + c] + red[k][0][j][lane] + red[k][1][j][lane] +
+                      red[k][2][j][lane] + bc;
+          if (mask && !(Elem<T>::to_f32(mask[row + iw]) > 0.f)) val = 0.f;
+          dx[row + iw] = Elem<T>::from_f32(val);
+        }
+      }
+    }
+  };
+  switch (wv) {
+    case 0: finish(std::integral_constant<int, 0>()); break;
+    case 1: finish(std::integral_constant<int, 1>()); break;
+    case 2: finish(std::integral_constant<int, 2>()); break;
+    default: finish(std::integral_constant<int, 3>()); break;
+  }
+}
+
 // y[n][c][hw] += bias[c] over an NCHW tensor (fp32 add, one rounding).
 template <typename T>
 __global__ __launch_bounds__(256) void channel_bias_add_kernel(typename Elem<T>::storage* __restrict__ y,
@@ -903,6 +1121,28 @@ int run_dgrad_smallc(const void* dy, const void* w, const void* bias, const void
   const long total = (long)g.N * g.H * g.W;
   const int cc = g.C <= 1 ? 1 : g.C <= 2 ? 2 : 4;
   const size_t lds = (size_t)g.O * g.R * g.S * cc * sizeof(float);
+  // 4x4 taps at stride 2, padding 1 (the up-sampling ConvTranspose2d layer):
+  // the cell kernel, when a dY row splits into aligned 4-wide loads
+  if (g.R == 4 && g.S == 4 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.Q % 4 == 0 &&
+      (reinterpret_cast<uintptr_t>(dy) % (4 * sizeof(S))) == 0 && (reinterpret_cast<uintptr_t>(w) % 4) == 0) {
+    const int nct = (g.H + 1) / 2, ncq = ((g.W + 1) / 2 + 3) / 4;
+    const long nlanes = (long)g.N * nct * ncq, nblk = (nlanes + 63) / 64;
+    // dY addressed by 32-bit buffer offsets, below the out-of-range marker
+    if (nblk < (1L << 31) && (long)g.N * g.O * g.P * g.Q * (long)sizeof(S) < (1L << 31) - 16) {
+#define VH_CELL(CV)                                                                                           \
+  dgrad_cell_kernel<T, CV, 4, 4, 2, 2, 1, 1><<<(unsigned)nblk, 256, 0, st>>>(                                  \
+      (const S*)dy, (const S*)w, (const S*)bias, (const S*)mask, (S*)dx, g, ncq, nct, nlanes)
+      switch (g.C) {
+        case 1: VH_CELL(1); break;
+        case 2: VH_CELL(2); break;
+        case 3: VH_CELL(3); break;
+        default: VH_CELL(4); break;
+      }
+#undef VH_CELL
+      VH_LAUNCH_CHECK();
+      return VH_OK;
+    }
+  }
   const int grid = grid_for(total);
 #define VH_SMALLC(CCV)                                                                                        \
   dgrad_smallc_kernel<T, CCV><<<grid, 256, lds, st>>>((const S*)dy, (const S*)w, (const S*)bias, (const S*)mask, \
