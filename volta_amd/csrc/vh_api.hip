@@ -1130,7 +1130,7 @@ static int conv2d_forward_impl(int dtype, int algo, const void* input, const voi
     VH_TRY(im2col_fwd(dtype, input, weight, bias, output, d, st));
   } else {
     ConvGeom g = geom_of(d);
-    VH_TRY(VH_DISPATCH(dtype, run_direct_fwd, input, weight, bias, output, g, st));
+    return VH_DISPATCH(dtype, run_direct_fwd, input, weight, bias, output, g, st, act);  // ReLU fused
   }
   return act ? relu_after(dtype, output, d.B * d.O * d.HO * d.WO, st) : VH_OK;
 }

@@ -26,7 +26,7 @@ __global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>:
                                                          const typename Elem<T>::storage* __restrict__ w,
                                                          const typename Elem<T>::storage* __restrict__ bias,
                                                          typename Elem<T>::storage* __restrict__ y,
-                                                         ConvGeom g, long total) {
+                                                         ConvGeom g, long total, int act) {
 #pragma clang fp contract(off)
   for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < total; i += (long)gridDim.x * 256) {
     int q = (int)(i % g.Q);
@@ -51,7 +51,10 @@ __global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>:
         }
       }
     if (bias) s += Elem<T>::to_f32(bias[o]);
-    y[i] = Elem<T>::from_f32(s);
+    auto v = Elem<T>::from_f32(s);
+    // act 1: ReLU of the rounded value (zero unless it is positive)
+    if (act == 1 && !(Elem<T>::to_f32(v) > 0.f)) v = Elem<T>::from_f32(0.f);
+    y[i] = v;
   }
 }
 
@@ -846,6 +849,35 @@ __global__ __launch_bounds__(256) void column_sum_vec_kernel(const typename Elem
   for (int k = 0; k < VE; k += 4) *reinterpret_cast<float4*>(o + k) = make_float4(s[k], s[k + 1], s[k + 2], s[k + 3]);
 }
 
+// Channel sums from column sums of [N][C * HW]: block c adds part[z][c * HW +
+// hw] over every slice z and position hw, in a fixed order (four interleaved
+// accumulators per lane, then the lanes' butterfly, then the waves in order).
+template <typename T>
+__global__ __launch_bounds__(256) void channel_segment_sum_kernel(const float* __restrict__ part, int slices, int C,
+                                                                  int HW, FastDiv fHW,
+                                                                  typename Elem<T>::storage* __restrict__ out) {
+  const int c = blockIdx.x, tid = threadIdx.x;
+  const long L = (long)C * HW;
+  const int tot = slices * HW;
+  auto at = [&](int i) {
+    uint32_t z, hw;
+    fHW.divmod((uint32_t)i, z, hw);
+    return part[(long)z * L + (long)c * HW + hw];
+  };
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  int i = tid;
+  for (; i + 768 < tot; i += 1024) {
+    const float v0 = at(i), v1 = at(i + 256), v2 = at(i + 512), v3 = at(i + 768);
+    a0 += v0, a1 += v1, a2 += v2, a3 += v3;
+  }
+  for (; i < tot; i += 256) a0 += at(i);
+  const float s = wave_sum((a0 + a1) + (a2 + a3));
+  __shared__ float red[4];
+  if ((tid & 63) == 0) red[tid >> 6] = s;
+  __syncthreads();
+  if (tid == 0) out[c] = Elem<T>::from_f32((red[0] + red[1]) + (red[2] + red[3]));
+}
+
 // Fixed-order sum of partial slabs part[z][i] (z < splits, i < n, n % 4 == 0,
 // 16-byte aligned slabs) read as float4 quads (reduce_splits_vec4_block).
 template <typename T>
@@ -1094,10 +1126,12 @@ __global__ __launch_bounds__(256) void fill_kernel(typename Elem<T>::storage* __
 
 // ============================================================== typed launchers
 template <typename T>
-int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st) {
+int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st,
+                   int act) {
   long total = (long)g.N * g.O * g.P * g.Q;
   using S = typename Elem<T>::storage;
-  direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, total);
+  direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, total,
+                                                        act);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -1301,19 +1335,49 @@ static int channel_sum_plane_slices(int N, int C, int HW, size_t esize) {
   return std::min(hsl, 65535);
 }
 
+// Short planes (under 128 16-byte chunks, where a block per plane leaves most
+// lanes idle): column sums of the [N][C * HW] matrix over slices of rows_per
+// images, 16 bytes per lane, then per-channel segment sums.  Returns the slice
+// count, 0 when the shape does not qualify.
+static int channel_rows_slices(int N, int C, int HW, size_t esize, int* rows_per) {
+  const int ve = (int)(16 / esize);
+  const long L = (long)C * HW;
+  if (N < 1 || HW % ve || HW / ve >= 128 || L >= (1L << 31) || (long)N * L >= (1L << 40)) return 0;
+  const long cb = (L / ve + 255) / 256;  // column blocks per slice
+  const int s = (int)std::max<long>(1, std::min<long>(N / 8, std::max<long>(1, 512 / cb)));
+  *rows_per = (N + s - 1) / s;
+  return (N + *rows_per - 1) / *rows_per;
+}
+
 size_t channel_sum_ws(int N, int C, int HW, int* nslice) {
+  int rp;
+  const size_t rows_ws = (size_t)std::max(channel_rows_slices(N, C, HW, 2, &rp), channel_rows_slices(N, C, HW, 4, &rp)) *
+                         C * HW * sizeof(float);
   long len = (long)N * HW;
   int s = (int)std::max<long>(1, std::min<long>(std::max<long>(1, 1024 / std::max(C, 1)), len / 4096));
   // the plane-vectorised form keeps N * slices partials (bounded by the larger of the two)
   const int hsl = std::max(channel_sum_plane_slices(N, C, HW, 2), channel_sum_plane_slices(N, C, HW, 4));
   const int sp = hsl ? N * hsl : 0;
   *nslice = s;
-  return (size_t)std::max(s, sp) * C * sizeof(float);
+  return std::max((size_t)std::max(s, sp) * C * sizeof(float), rows_ws);
 }
 
 template <typename T>
 int run_channel_sum(const void* x, int N, int C, int HW, void* out, float* ws, int nslice, hipStream_t st) {
   using S = typename Elem<T>::storage;
+  {
+    int rp;
+    const int rs = channel_rows_slices(N, C, HW, sizeof(S), &rp);
+    if (rs && (((uintptr_t)x | (uintptr_t)ws) & 15) == 0) {
+      constexpr int VE = 16 / sizeof(S);
+      const int L = C * HW;
+      column_sum_vec_kernel<T><<<dim3((L / VE + 255) / 256, rs), 256, 0, st>>>((const S*)x, N, L, ws, rp);
+      VH_LAUNCH_CHECK();
+      channel_segment_sum_kernel<T><<<C, 256, 0, st>>>(ws, rs, C, HW, FastDiv((uint32_t)HW), (S*)out);
+      VH_LAUNCH_CHECK();
+      return VH_OK;
+    }
+  }
   const int hsl = ((uintptr_t)x & 15) ? 0 : channel_sum_plane_slices(N, C, HW, sizeof(S));
   if (hsl) {
     channel_sum_planes_kernel<T><<<dim3(C, N, hsl), 256, 0, st>>>((const S*)x, C, HW / (int)(16 / sizeof(S)), hsl,
@@ -1480,7 +1544,7 @@ int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, floa
 }
 
 #define VH_INST(T)                                                                                      \
-  template int run_direct_fwd<T>(const void*, const void*, const void*, void*, const ConvGeom&, hipStream_t); \
+  template int run_direct_fwd<T>(const void*, const void*, const void*, void*, const ConvGeom&, hipStream_t, int); \
   template int run_col2im_t<T>(const float*, void*, int, int, int, int, int, int, int, int, int, int, int, int,  \
                                hipStream_t);                                                            \
   template int run_direct_dgrad<T>(const void*, const void*, void*, const ConvGeom&, hipStream_t);      \

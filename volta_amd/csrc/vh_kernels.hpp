@@ -25,7 +25,8 @@ ConvGeom make_geom(int N, int C, int H, int W, int O, int R, int S, int P, int Q
 
 // ---- other kernels (vh_kernels.hip) ----
 template <typename T>
-int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st);
+int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, hipStream_t st,
+                   int act = 0);
 template <typename T>
 int run_col2im_t(const float* dcolT, void* x, int B, int C, int H, int W, int KH, int KW, int SH, int SW, int PH,
                  int PW, int HO, int WO, hipStream_t st);
