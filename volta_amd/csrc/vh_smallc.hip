@@ -37,18 +37,21 @@ struct SmallcArgs {
   int tpb;               // position tiles per block
   int act;               // 0 none, 1 ReLU
   int vec_epi;           // 16-byte stores of 8 positions (P*Q % 8 == 0, 16-byte aligned y)
-  FastDiv fPQ, fQ, fHp, fRS, fS, fWp, fRows;
+  int wpl, col0;         // halo row pitch in LDS and LDS column of padded column 0
+  int vec_halo;          // halo rows as 16-byte chunks (W % 8 == 0, 16-byte aligned x), prefetched a tile ahead
+  int nch;               // 16-byte chunks of one tile's halo (vec_halo)
+  FastDiv fPQ, fQ, fHp, fRS, fS, fWp, fRows, fWc;
 };
 
 constexpr int kEP = 72;  // epilogue LDS pitch (elements) of a wave's 64 x 64 tile
 
 template <int KP>
-__global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_smallc_fwd_bf16_kernel(SmallcArgs a) {
   constexpr int WPITCH = KP + 8;  // weight row pitch (elements): 16-byte aligned rows, shifted banks
   extern __shared__ __attribute__((aligned(16))) uint16_t sm[];
   uint16_t* wl = sm;                                              // [64][WPITCH]
   int* koff = reinterpret_cast<int*>(sm + 64 * WPITCH);           // [KP]
-  const int nh = a.C * a.rows_max * a.Wp;                          // halo elements (real channels)
+  const int nh = a.C * a.rows_max * a.wpl;                         // halo elements (real channels)
   float* bl = reinterpret_cast<float*>(koff + KP);                // [64] fp32 bias of the o tile
   uint16_t* xl = reinterpret_cast<uint16_t*>(bl + 64);            // [C + 1][rows_max][Wp], plane C zeros
   const int tid = threadIdx.x, lane = tid & 63;
@@ -59,7 +62,7 @@ __global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a)
   const int groups = (a.tiles_m + a.tpb - 1) / a.tpb;
   const int lb = xcd_block(groups * a.tiles_o);
   const int tm0 = (lb / a.tiles_o) * a.tpb, o0 = (lb % a.tiles_o) * 64;
-  const int plane = a.rows_max * a.Wp;  // halo elements per channel
+  const int plane = a.rows_max * a.wpl;  // halo elements per channel
 
   // weights: [64][KP], zero for k >= K and o >= O; all loads issued before the
   // LDS stores (a load-store pair per iteration would wait out each load)
@@ -84,7 +87,7 @@ __global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a)
       uint32_t c, rs, r, s;
       a.fRS.divmod((uint32_t)k, c, rs);
       a.fS.divmod(rs, r, s);
-      koff[k] = (int)c * plane + (int)r * a.Wp + (int)s;
+      koff[k] = (int)c * plane + (int)r * a.wpl + (int)s + a.col0;
     } else {
       koff[k] = a.C * plane;  // padded k: the zero plane (its weights are zero too)
     }
@@ -92,14 +95,52 @@ __global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a)
 
   const int half = lane >> 5, row_l = lane & 31;
   const int PQ = a.P * a.Q;
-  for (int tm = tm0; tm < min(tm0 + a.tpb, a.tiles_m); ++tm) {
+  // first ext row of tile tm (row of its first position)
+  auto first_row = [&](int tm) {
+    uint32_t n_a, pq_a, p_a, q_a;
+    a.fPQ.divmod((uint32_t)(tm * 256), n_a, pq_a);
+    a.fQ.divmod(pq_a, p_a, q_a);
+    return (int)n_a * a.Hp + (int)p_a;
+  };
+  // vector halo: chunk i = (c, e, 8-column chunk) of the tile starting at ext
+  // row es, zeros outside the image, loaded into registers and then stored
+  constexpr int kHU = 4;  // chunks per lane at most
+  uint4 hreg[kHU];
+  int hoff[kHU];
+  auto hload = [&](int es) {
+#pragma unroll
+    for (int u = 0; u < kHU; ++u) {
+      const int i = tid + u * 256;
+      hreg[u] = uint4{0u, 0u, 0u, 0u};
+      hoff[u] = -1;
+      if (i < a.nch) {
+        uint32_t row, ch, c, e, img, hr;
+        a.fWc.divmod((uint32_t)i, row, ch);
+        a.fRows.divmod(row, c, e);
+        a.fHp.divmod((uint32_t)(es + (int)e), img, hr);
+        const int h = (int)hr - a.ph;
+        hoff[u] = (int)row * a.wpl + 8 + (int)ch * 8;
+        if ((int)img < a.N && h >= 0 && h < a.H)
+          hreg[u] = *reinterpret_cast<const uint4*>(a.x + (((long)img * a.C + c) * a.H + h) * a.W + ch * 8);
+      }
+    }
+  };
+  const int tm_end = min(tm0 + a.tpb, a.tiles_m);
+  for (int tm = tm0; tm < tm_end; ++tm) {
   const int m0 = tm * 256;
-  // first ext row of the tile (row of its first position)
-  uint32_t n_a, pq_a, p_a, q_a;
-  a.fPQ.divmod((uint32_t)m0, n_a, pq_a);
-  a.fQ.divmod(pq_a, p_a, q_a);
-  const int e_start = (int)n_a * a.Hp + (int)p_a;
+  const int e_start = first_row(tm);
+  if (a.vec_halo) hload(e_start);  // issued before the barrier: the loads overlap the other waves' epilogue
   if (tm != tm0) __syncthreads();  // the previous tile's epilogue is done with the LDS
+  if (a.vec_halo) {
+#pragma unroll
+    for (int u = 0; u < kHU; ++u)
+      if (hoff[u] >= 0) *reinterpret_cast<uint4*>(xl + hoff[u]) = hreg[u];
+    // the 8 columns either side of every row (the padding) are zeros
+    for (int i = tid; i < a.C * a.rows_max * 2; i += 256) {
+      const int row = i >> 1;
+      *reinterpret_cast<uint4*>(xl + row * a.wpl + ((i & 1) ? a.W + 8 : 0)) = uint4{0u, 0u, 0u, 0u};
+    }
+  } else {
   // halo: ext rows e_start .. e_start + rows_max - 1 of every channel, padded
   // columns (zeros outside the image); rows past the tensor are zeros.  Element
   // i = (c, e, col) of the [C][rows_max][Wp] halo; batches of 8 loads per lane
@@ -127,6 +168,7 @@ __global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a)
       if (i < nh) xl[i] = hv[u];
     }
   }
+  }
   // the zero plane (padded k), rewritten per tile: the epilogue tile overlaps it
   for (int i = tid; i < plane; i += 256) xl[nh + i] = 0;
   __syncthreads();
@@ -141,7 +183,7 @@ __global__ __launch_bounds__(256) void conv_smallc_fwd_bf16_kernel(SmallcArgs a)
       uint32_t n, pq, p, q;
       a.fPQ.divmod((uint32_t)m, n, pq);
       a.fQ.divmod(pq, p, q);
-      cidx = ((int)n * a.Hp + (int)p - e_start) * a.Wp + (int)q;
+      cidx = ((int)n * a.Hp + (int)p - e_start) * a.wpl + (int)q;
     }
     bcell[j] = cidx;
   }
@@ -257,7 +299,12 @@ int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, in
   // the block's halo: cached per shape like the halo kernel's row-span scan is not
   // needed here (one pass over M / 256 blocks, a few thousand iterations)
   a.rows_max = smallc_rows_max(a.M, (long)P * Q, Q, a.Hp, R);
-  const size_t halo = (size_t)(C + 1) * a.rows_max * a.Wp;
+  // vector halo: rows of W + 16 elements, image column w at LDS column w + 8
+  a.vec_halo = W % 8 == 0 && pw <= 8 && ((uintptr_t)x & 15) == 0 && (long)C * a.rows_max * (W / 8) <= 4 * 256;
+  a.wpl = a.vec_halo ? W + 16 : a.Wp;
+  a.col0 = a.vec_halo ? 8 - pw : 0;
+  a.nch = a.vec_halo ? C * a.rows_max * (W / 8) : 0;
+  const size_t halo = (size_t)(C + 1) * a.rows_max * a.wpl;
   a.vec_epi = ((long)P * Q) % 8 == 0 && ((uintptr_t)y & 15) == 0;
   // weights and offsets stay; the halo and the epilogue tile share the rest
   const size_t lds = (size_t)64 * (KP + 8) * 2 + (size_t)KP * 4 + 64 * 4 +
@@ -276,6 +323,7 @@ int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, in
   a.fS = FastDiv((uint32_t)S);
   a.fWp = FastDiv((uint32_t)a.Wp);
   a.fRows = FastDiv((uint32_t)a.rows_max);
+  a.fWc = FastDiv((uint32_t)std::max(1, W / 8));
   const dim3 grid((unsigned)((a.tiles_m + a.tpb - 1) / a.tpb * a.tiles_o));
 #define VH_SMALLC_FWD(KPV)                                                    \
   if (KP == KPV) {                                                            \
