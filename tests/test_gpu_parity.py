@@ -152,6 +152,7 @@ CONV_CASES = [
     (2, 4, 8, 9, 11, 3, 3, 2),       # 4 input channels, stride 3
     (2, 2, 8, 17, 16, 4, 2, 1),      # 4x4 stride 2 pad 1, 2 input channels: cell-wise input gradient, odd height
     (1, 4, 6, 16, 17, 4, 2, 1),      # the same with 4 input channels, odd width (a cell past the last dY column)
+    (2, 16, 128, 12, 12, 3, 1, 1),   # fp32 weight gradient on 128 x 128 tiles with split K (O and C*R*S >= 128)
 ]
 
 
@@ -334,6 +335,7 @@ CT_CASES = [
     (2, 8, 1, 8, 4, 4, 2, 1),        # k4 s2 p1 to 1 channel: cell-wise kernel, one 4-wide load per dY row
     (2, 12, 4, 6, 8, 4, 2, 1),       # k4 s2 p1 to 4 channels
     (3, 10, 2, 5, 12, 4, 2, 1),      # k4 s2 p1 to 2 channels, 10 input channels (uneven split over waves)
+    (2, 128, 16, 4, 4, 4, 2, 1),     # fp32 dW on 128 x 128 tiles (128 input channels x 16 x 16 taps)
 ]
 
 

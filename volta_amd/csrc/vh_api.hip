@@ -552,7 +552,8 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   p.args.d = dw;
   p.args.a = Operand{dy, 0, (int)d.O, aligned16(dy)};
   p.args.b = Operand{x, 0, p.args.N, 0};
-  p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt);
+  p.wide = 1;
+  p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt, p.wide);
   size_t ws_gemm = igemm_prepare(p);
   if (need) {
     *need = std::max(most, ws_gemm);

@@ -30,8 +30,11 @@ struct Tile {
 };
 
 // nphase: launches of several stride phases at once multiply the grid
-Tile pick_tile(int M, int N, int dtype = VH_F32, int nphase = 1) {
+Tile pick_tile(int M, int N, int dtype = VH_F32, int nphase = 1, int wide = 0) {
   Tile t{128, 128};
+  // fp32 weight gradients: the gathers of 128 x 128 tiles feed four times the
+  // MFMAs of 64 x 64 ones; split K fills the grid
+  if (wide && dtype == VH_F32 && M >= 128 && N >= 128) return t;
   if (M <= 64) t.bm = 64;
   // f32 (16x16 MFMA tiles) also has 32-row tiles: a 32-channel output would
   // leave half of a 64-row tile empty
@@ -73,7 +76,7 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
 
 template <typename T, int AK, int BKIND, int OUT>
 int launch_kinds(IgemmPlan& p, float* ws, hipStream_t st) {
-  Tile t = pick_tile(p.args.M, p.args.N, std::is_same<T, float>::value ? VH_F32 : VH_BF16, p.args.nphase);
+  Tile t = pick_tile(p.args.M, p.args.N, std::is_same<T, float>::value ? VH_F32 : VH_BF16, p.args.nphase, p.wide);
   if constexpr (std::is_same<T, float>::value) {
     // 32-row tiles take 32-deep K steps so that all 256 threads have a load unit
     if (t.bm == 32 && t.bn == 128) return launch_tile<T, AK, BKIND, OUT, 32, 128, 32>(p, ws, st);
@@ -106,8 +109,8 @@ int launch_typed(IgemmPlan& p, float* ws, hipStream_t st) {
 
 }  // namespace
 
-int pick_splits(int M, int N, int K, int dtype) {
-  Tile t = pick_tile(M, N, dtype);
+int pick_splits(int M, int N, int K, int dtype, int wide) {
+  Tile t = pick_tile(M, N, dtype, 1, wide);
   const int bk = dtype == VH_BF16 ? 32 : 16;
   long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
   // Split K only when the tile grid leaves most of the 256 CUs idle and K is

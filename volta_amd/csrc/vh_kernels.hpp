@@ -12,6 +12,7 @@ struct IgemmPlan {
   IgemmArgs args;
   int splits;               // requested split-K factor (1 = none)
   int f32_out;              // internal: store fp32 row-major D (run_igemm_f32out)
+  int wide;                 // fp32: 128 x 128 tiles (with split K) when M and N are both >= 128
 };
 // Fills args.k_chunk / splits and returns the fp32 workspace bytes needed.
 size_t igemm_prepare(IgemmPlan& plan);
@@ -19,7 +20,7 @@ int run_igemm(IgemmPlan& plan, float* ws, hipStream_t st);
 // Runs the plan with splits = 1 and stores D[M][N] row-major in fp32 to `out`.
 int run_igemm_f32out(IgemmPlan& plan, float* out, hipStream_t st);
 // Heuristic split-K factor for a problem with the given tile grid and K.
-int pick_splits(int M, int N, int K, int dtype);
+int pick_splits(int M, int N, int K, int dtype, int wide = 0);
 ConvGeom make_geom(int N, int C, int H, int W, int O, int R, int S, int P, int Q, int sh, int sw, int ph,
                    int pw);
 
