@@ -271,6 +271,8 @@ HALO_CASES = [
     (3, 64, 40, 16, 24, 3, 1, 1),    # resident weights, O = 40: partly empty 64-row tile
     (2, 40, 24, 20, 16, 3, 1, 1),    # resident weights, C = 40: partial channel group (grouped copy)
     (1, 64, 64, 16, 16, 3, 1, 1),    # one tile per block (fewer tiles than CUs)
+    (8, 3, 16, 64, 64, 5, 1, 2),     # few-channel weight gradient, 5x5: two steps per split (x rows reused)
+    (16, 8, 16, 48, 32, 3, 1, 1),    # few-channel weight gradient, 3x3 pad 1: steps cross a column chunk
 ]
 
 

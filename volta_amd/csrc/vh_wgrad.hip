@@ -652,7 +652,8 @@ __global__ __launch_bounds__(256) void wgrad_reduce_frag_bf16_kernel(const float
 // aligned 8-column chunks v-8, v, v+8 of its dY row (the windows of the S taps
 // are funnel shifts of these) and the chunk v of its x channel in the R rows.
 // Wave w of a block owns o0 + 16w .. +16 and walks the block's range of K steps
-// (n, p, 32-column chunk) with the next step's loads in flight.  Partials:
+// (n, 32-column chunk, p), p fastest, with the next step's loads in flight; a
+// step of the same chunk keeps R - 1 x rows of the previous one in registers.  Partials:
 // [split][tap][O][C] and [split][O] for the bias, reduced like the row kernel's.
 // af[i] = the 8 bf16 starting START - i elements into (c0, c1, c2), i < NW
 template <int START, int NW>
@@ -703,36 +704,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   struct Ops {
     u32x4w cm, cz, cp, x[R];
   };
-  // position of a step: (n, p, column chunk); advanced incrementally
+  // position of a step: (n, column chunk, p), p fastest, advanced
+  // incrementally: consecutive steps of a chunk share R - 1 of their x rows
   int n, p, qc;
   {
     const int PN = a.P * a.nq;
     n = step_b / PN;
     const int rem = step_b - n * PN;
-    p = rem / a.nq;
-    qc = rem - p * a.nq;
+    qc = rem / a.P;
+    p = rem - qc * a.P;
   }
-  auto load = [&](Ops& f) {
+  auto xrow_ld = [&](int r) {
+    const int v = qc * 32 + kg * 8;
+    const int h = p - a.ph + r;
+    return BufLoad<8>::ld(xrr, c_ok && v < a.W && h >= 0 && h < a.H ? ((n * a.C + c) * HW + h * a.W + v) * 2 : OOR,
+                          0);
+  };
+  auto load_dy = [&](Ops& f) {
     const int v = qc * 32 + kg * 8;  // this lane's 8 x columns v .. v+7
     const int drow = o_ok ? ((n * a.O + o) * PQ + p * a.Q) * 2 : 0;
     const int vm = v - 8, vp = v + 8;
     f.cm = BufLoad<8>::ld(dyr, o_ok && vm >= 0 && vm < a.Q ? drow + vm * 2 : OOR, 0);
     f.cz = BufLoad<8>::ld(dyr, o_ok && v < a.Q ? drow + v * 2 : OOR, 0);
     f.cp = BufLoad<8>::ld(dyr, o_ok && vp < a.Q ? drow + vp * 2 : OOR, 0);
-    const int xrow = ((n * a.C + c) * HW + v) * 2;
+  };
+  auto load = [&](Ops& f) {
+    load_dy(f);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int h = p - a.ph + r;
-      f.x[r] = BufLoad<8>::ld(xrr, c_ok && v < a.W && h >= 0 && h < a.H ? xrow + h * a.W * 2 : OOR, 0);
+    for (int r = 0; r < R; ++r) f.x[r] = xrow_ld(r);
+  };
+  // the step after prev's: within a chunk, x rows 1.. of prev are this step's
+  // rows 0.. and only the last row is loaded (when the position did not move,
+  // the final prefetch, the rows are never used)
+  auto load_next = [&](Ops& f, const Ops& prev) {
+    if (p == 0) {
+      load(f);
+    } else {
+      load_dy(f);
+#pragma unroll
+      for (int r = 0; r + 1 < R; ++r) f.x[r] = prev.x[r + 1];
+      f.x[R - 1] = xrow_ld(R - 1);
     }
   };
   auto advance = [&]() {
-    ++qc;
-    const int w1 = qc == a.nq;
-    qc = w1 ? 0 : qc;
-    p += w1;
-    const int w2 = p == a.P;
-    p = w2 ? 0 : p;
+    ++p;
+    const int w1 = p == a.P;
+    p = w1 ? 0 : p;
+    qc += w1;
+    const int w2 = qc == a.nq;
+    qc = w2 ? 0 : qc;
     n += w2;
   };
 
@@ -768,12 +788,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   int k = 0;
   for (; k + 2 <= nsteps; k += 2) {
     advance();
-    load(fb);
+    load_next(fb, fa);
     __builtin_amdgcn_sched_barrier(0);
     compute(fa);
     __builtin_amdgcn_sched_barrier(0);
     if (k + 2 < nsteps) advance();
-    load(fa);
+    load_next(fa, fb);
     __builtin_amdgcn_sched_barrier(0);
     compute(fb);
     __builtin_amdgcn_sched_barrier(0);
