@@ -338,6 +338,10 @@ CT_CASES = [
     (2, 12, 4, 6, 8, 4, 2, 1),       # k4 s2 p1 to 4 channels
     (3, 10, 2, 5, 12, 4, 2, 1),      # k4 s2 p1 to 2 channels, 10 input channels (uneven split over waves)
     (2, 128, 16, 4, 4, 4, 2, 1),     # fp32 dW on 128 x 128 tiles (128 input channels x 16 x 16 taps)
+    (2, 64, 3, 32, 32, 4, 2, 1),     # config 4 last layer at batch 2: fp32 dW and dB in one MFMA pass
+    (2, 16, 3, 4, 32, 4, 2, 1),      # the same kernel, 4 input rows
+    (1, 64, 4, 2, 64, 4, 2, 1),      # two 32-position segments per input row, 4 output channels
+    (2, 8, 1, 3, 32, 4, 2, 1),       # 1 output channel, odd input height
 ]
 
 

@@ -1345,6 +1345,18 @@ int vh_conv_transpose2d_backward(int dtype, const void* out_grad, const void* in
     return VH_OK;
   }
   if (grad_input) VH_TRY(igemm_fwd(dtype, out_grad, weight, nullptr, grad_input, d, st));
+  if (grad_weight && dtype == VH_F32 && g_fast_paths) {
+    // up-sampling layer to a few channels: dW (and dB) in one MFMA pass over the positions
+    const ConvGeom g = geom_of(d);
+    const size_t nb = convt_cell_wgrad_ws(g);
+    if (nb) {
+      void* ws;
+      VH_TRY(ws_get(st, nb, &ws));
+      const int r = convt_cell_wgrad_f32(input, out_grad, grad_weight, grad_bias, g, (float*)ws, nb, st);
+      if (r == VH_OK) return VH_OK;
+      if (r != VH_ERR_UNSUPPORTED) return r;
+    }
+  }
   if (grad_weight) VH_TRY(igemm_wgrad(dtype, input, out_grad, grad_weight, nullptr, nullptr, d, st));
   if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.C, d.H * d.W, st));
   return VH_OK;

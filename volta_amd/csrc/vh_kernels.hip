@@ -167,6 +167,13 @@ __global__ __launch_bounds__(256) void dgrad_smallc_kernel(const typename Elem<T
   }
 }
 
+// Sum over the 64 lanes of a wave (butterfly, the same order on every lane).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
 // Tap offsets of one axis of a fixed geometry (taps K, stride ST, padding PD)
 // seen from cells: a cell t covers input positions ST*t + e, e < ST.  Position
 // e reaches taps k = a(e) + ST*j, j < nj(e), and reads output index
@@ -342,7 +349,6 @@ __global__ __launch_bounds__(256) void dgrad_cell_kernel(const typename Elem<T>:
 
   // wave k finishes cell column k of the lane: the other three waves hand it
   // their sums for that column through LDS
-  constexpr int NCELL = SH * SW * C;  // outputs per cell
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     if (k == wv) continue;
@@ -385,6 +391,163 @@ __global__ __launch_bounds__(256) void dgrad_cell_kernel(const typename Elem<T>:
   }
 }
 
+// Weight gradient of the same layer shape (4x4 taps, stride 2, padding 1, at
+// most 4 input channels, at most 64 output channels), fp32 on
+// v_mfma_f32_32x32x2f32: D[o][(c, r, s)] = sum over positions (n, p, q) of
+// dY[n][o][p][q] * x[n][c][2p - 1 + r][2q - 1 + s].  A stage is one 32-position
+// segment of a dY row: its dY tile [o][q] and the four x rows 2p - 1 .. 2p + 2 of
+// every channel (columns -1 .. 64 of the segment, zeros outside the image) go
+// to LDS through registers, double-buffered, and each wave multiplies a 32 x 32
+// quadrant of the 64 x 64 (o x (c, r, s)) tile over the stage's 32 positions.
+// Blocks own ranges of stages and write fp32 partials [block][O][C][4][4]
+// followed by the bias sums [block][C] (x rows 2p and 2p + 1 of each stage
+// cover every row once); a second kernel adds them in block order.
+constexpr int kCwQ = 32;                  // positions per stage
+constexpr int kCwAP = kCwQ + 2;           // dY tile pitch (o rows): k and k + 1 on even / odd banks
+constexpr int kCwXP = 76;                 // x row pitch: 12 * row mod 64 keeps 12 rows' taps apart
+constexpr int kCwXR = 17;                 // 16 x rows (c, r) + a zero row for padded columns
+
+__global__ __launch_bounds__(256) void convt_cell_wgrad_kernel(const float* __restrict__ dy,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ part, ConvGeom g, int nseg,
+                                                              int stages, int per_block) {
+  __shared__ __attribute__((aligned(16))) float as[2][64 * kCwAP];
+  __shared__ __attribute__((aligned(16))) float xs[2][kCwXR * kCwXP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int fr = lane & 31, fk = lane >> 5;
+  const int C = g.C, O = g.O, NCOL = C * 16;
+  const long PQ = (long)g.P * g.Q, HW = (long)g.H * g.W;
+  // this lane's fragment rows: A row m = o, B column n = (c, r, s)
+  const int aoff = (wm + fr) * kCwAP + fk;
+  const int n = wn + fr;
+  const int boff = n < NCOL ? ((n >> 2) * kCwXP + (n & 3) + 3 + 2 * fk) : 16 * kCwXP;
+  // zero row (padded columns of B) in both buffers
+  for (int i = tid; i < 2 * kCwXP; i += 256) xs[i / kCwXP][16 * kCwXP + i % kCwXP] = 0.f;
+
+  const int s_b = blockIdx.x * per_block, s_e = min(stages, s_b + per_block);
+  // stage -> (image, dY row, 32-position segment)
+  auto decode = [&](int st, int& img, int& p, int& seg) {
+    seg = st % nseg;
+    const int t = st / nseg;
+    p = t % g.P;
+    img = t / g.P;
+  };
+  float4 ra[2];  // dY: 64 o x 8 float4 per stage, two per thread
+  float4 rx[2];  // x: 16 rows x 18 float4 (columns 64 seg - 4 + 4j), at most two per thread
+  // bias: sums of the x chunks of rows r = 1, 2 (x rows 2p, 2p + 1) and
+  // columns 64 seg .. 64 seg + 63, per slot (a slot's channel is fixed)
+  float bsum[2] = {0.f, 0.f};
+  auto gload = [&](int st) {
+    int img, p, seg;
+    decode(st, img, p, seg);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * 256, o = i >> 3, q4 = i & 7;
+      ra[u] = o < O ? *reinterpret_cast<const float4*>(dy + ((long)img * O + o) * PQ + (long)p * g.Q + seg * kCwQ +
+                                                       q4 * 4)
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * 256;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < C * 4 * 18) {
+        const int row = i / 18, j = i - row * 18;  // row = (c, r)
+        const int c = row >> 2, r = row & 3;
+        const int h = 2 * p - 1 + r, col = seg * 2 * kCwQ - 4 + 4 * j;
+        if (h >= 0 && h < g.H && col >= 0 && col < g.W)
+          v = *reinterpret_cast<const float4*>(x + ((long)img * C + c) * HW + (long)h * g.W + col);
+        if ((r == 1 || r == 2) && j >= 1 && j <= 16) bsum[u] += ((v.x + v.y) + v.z) + v.w;
+      }
+      rx[u] = v;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * 256, o = i >> 3, q4 = i & 7;
+      // pitch 34: two 8-byte halves
+      float* d = &as[buf][o * kCwAP + q4 * 4];
+      *reinterpret_cast<float2*>(d) = make_float2(ra[u].x, ra[u].y);
+      *reinterpret_cast<float2*>(d + 2) = make_float2(ra[u].z, ra[u].w);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * 256;
+      if (i < C * 4 * 18) {
+        const int row = i / 18, j = i - row * 18;
+        *reinterpret_cast<float4*>(&xs[buf][row * kCwXP + 4 * j]) = rx[u];
+      }
+    }
+  };
+  f32x16 acc = f32x16{};
+  auto compute = [&](int buf) {
+    const float* a = as[buf] + aoff;
+    const float* b = xs[buf] + boff;
+#pragma unroll
+    for (int kk = 0; kk < kCwQ; kk += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], b[2 * kk], acc, 0, 0, 0);
+  };
+  if (s_b < s_e) {
+    gload(s_b);
+    sstore(0);
+  }
+  __syncthreads();
+  for (int st = s_b; st < s_e; ++st) {
+    const int buf = (st - s_b) & 1;
+    if (st + 1 < s_e) gload(st + 1);
+    compute(buf);
+    if (st + 1 < s_e) sstore(buf ^ 1);
+    __syncthreads();
+  }
+  // partials: lane holds D[o = wm + row(v)][n]
+  const long nw = (long)O * NCOL;
+  float* pb = part + (long)blockIdx.x * ((nw + C + 3) & ~3L);  // slabs of whole 16-byte quads
+  if (n < NCOL) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int o = wm + (v >> 2) * 8 + fk * 4 + (v & 3);
+      if (o < O) pb[(long)o * NCOL + n] = acc[v];
+    }
+  }
+  {
+    // per-channel block sums in a fixed order: slot i = tid + 256 u holds
+    // channel (i / 18) / 4; wave c adds channel c's 512 slots
+    float* red = as[0];  // [4][512], free after the last stage's barrier
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int i = tid + u * 256, ci = i < C * 72 ? (i / 18) >> 2 : -1;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) red[c * 512 + i] = c == ci ? bsum[u] : 0.f;
+    }
+    __syncthreads();
+    if (wave < C) {
+      float t = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) t += red[wave * 512 + k * 64 + lane];
+      t = wave_sum(t);
+      if (lane == 0) pb[nw + wave] = t;
+    }
+  }
+}
+
+// out: dW [O][C][4][4] = sum over blocks of the partials (slabs of np floats,
+// a multiple of 4), then dB [C]; split groups as in the float4 slab reduction
+template <typename T>
+__global__ __launch_bounds__(256) void convt_cell_wgrad_reduce_kernel(const float* __restrict__ part, int blocks,
+                                                                     long np, long nw, int C, int lg_g,
+                                                                     typename Elem<T>::storage* __restrict__ dw,
+                                                                     typename Elem<T>::storage* __restrict__ db) {
+  reduce_splits_vec4_block(
+      part, blocks, np, lg_g,
+      [&](long i, float v) {
+        if (i < nw) dw[i] = Elem<T>::from_f32(v);
+        else if (db && i < nw + C) db[i - nw] = Elem<T>::from_f32(v);
+      },
+      (int)blockIdx.x, (int)gridDim.x);
+}
+
 // y[n][c][hw] += bias[c] over an NCHW tensor (fp32 add, one rounding).
 template <typename T>
 __global__ __launch_bounds__(256) void channel_bias_add_kernel(typename Elem<T>::storage* __restrict__ y,
@@ -397,11 +560,6 @@ __global__ __launch_bounds__(256) void channel_bias_add_kernel(typename Elem<T>:
 // Weight gradient: one workgroup per (weight element, position slice); the 256
 // lanes stride over output positions and a wavefront reduction (DPP shuffles)
 // plus an LDS step combine them into one fp32 partial per slice.
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 template <typename T>
 __global__ __launch_bounds__(256) void direct_wgrad_kernel(const typename Elem<T>::storage* __restrict__ dy,
@@ -1141,6 +1299,40 @@ int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g,
   long total = (long)g.N * g.C * g.H * g.W;
   using S = typename Elem<T>::storage;
   direct_dgrad_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)dy, (const S*)w, (S*)dx, g, total);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
+// Few-channel ConvTranspose-shaped weight gradient (fp32): the geometry the
+// cell kernels take (4x4 taps, stride 2, padding 1, H = 2P, W = 2Q) with C <= 4,
+// O <= 64, Q a multiple of 32 and W of 4, 16-byte aligned operands.
+static bool convt_cell_wgrad_ok(const ConvGeom& g, const void* dy, const void* x) {
+  return g.R == 4 && g.S == 4 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.C >= 1 && g.C <= 4 &&
+         g.O >= 1 && g.O <= 64 && g.Q % kCwQ == 0 && g.H == 2 * g.P && g.W == 2 * g.Q &&
+         ((((uintptr_t)dy) | ((uintptr_t)x)) & 15) == 0 && (long)g.N * g.P * (g.Q / kCwQ) < (1L << 30);
+}
+static int convt_cell_wgrad_blocks(const ConvGeom& g) {
+  const int stages = g.N * g.P * (g.Q / kCwQ);
+  const int per = std::max(1, (stages + 511) / 512);
+  return (stages + per - 1) / per;
+}
+size_t convt_cell_wgrad_ws(const ConvGeom& g) {
+  if (!(g.R == 4 && g.S == 4 && g.sh == 2 && g.sw == 2 && g.C >= 1 && g.C <= 4 && g.O <= 64 && g.Q % kCwQ == 0))
+    return 0;
+  return (size_t)convt_cell_wgrad_blocks(g) * (((size_t)g.O * g.C * 16 + g.C + 3) & ~(size_t)3) * sizeof(float);
+}
+int convt_cell_wgrad_f32(const void* dy, const void* x, void* dw, void* db, const ConvGeom& g, float* ws,
+                         size_t ws_bytes, hipStream_t st) {
+  if (!convt_cell_wgrad_ok(g, dy, x)) return VH_ERR_UNSUPPORTED;
+  const int nseg = g.Q / kCwQ, stages = g.N * g.P * nseg;
+  const int per = std::max(1, (stages + 511) / 512), blocks = (stages + per - 1) / per;
+  const long nw = (long)g.O * g.C * 16, np = (nw + g.C + 3) & ~3L;
+  if ((size_t)blocks * np * sizeof(float) > ws_bytes || ((uintptr_t)ws & 15)) return VH_ERR_UNSUPPORTED;
+  convt_cell_wgrad_kernel<<<blocks, 256, 0, st>>>((const float*)dy, (const float*)x, ws, g, nseg, stages, per);
+  VH_LAUNCH_CHECK();
+  const int lg_g = reduce_vec4_lg_groups(blocks);
+  convt_cell_wgrad_reduce_kernel<float><<<reduce_vec4_grid(np, lg_g), 256, 0, st>>>(ws, blocks, np, nw, g.C, lg_g,
+                                                                                   (float*)dw, (float*)db);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }

@@ -102,6 +102,12 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
 
 // bf16 stride-1 forward for C*R*S <= 128 with K packed as (c, r, s) (vh_smallc.hip);
 // act 0 none, 1 ReLU.  VH_ERR_UNSUPPORTED outside that range.
+// Few-channel weight gradient of a 4x4 stride-2 pad-1 layer (fp32; dW and,
+// when db is non-null, the bias gradient of x's channels): VH_ERR_UNSUPPORTED
+// outside its envelope or when ws is smaller than convt_cell_wgrad_ws.
+size_t convt_cell_wgrad_ws(const ConvGeom& g);
+int convt_cell_wgrad_f32(const void* dy, const void* x, void* dw, void* db, const ConvGeom& g, float* ws,
+                         size_t ws_bytes, hipStream_t st);
 int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, int N, int C, int H, int W, int O,
                      int R, int S, int ph, int pw, int act, hipStream_t st);
 
