@@ -153,6 +153,7 @@ CONV_CASES = [
     (2, 2, 8, 17, 16, 4, 2, 1),      # 4x4 stride 2 pad 1, 2 input channels: cell-wise input gradient, odd height
     (1, 4, 6, 16, 17, 4, 2, 1),      # the same with 4 input channels, odd width (a cell past the last dY column)
     (2, 16, 128, 12, 12, 3, 1, 1),   # fp32 weight gradient on 128 x 128 tiles with split K (O and C*R*S >= 128)
+    (2, 3, 16, 64, 64, 4, 2, 1),     # 4x4 stride 2 from 3 channels, 32-column output rows: fp32 cell forward
 ]
 
 
@@ -476,6 +477,7 @@ RELU_CASES = [
     (2, 16, 24, 11, 9, 3, 2, 1),     # strided 3x3: stride phases
     (2, 1, 32, 12, 12, 3, 1, 1),     # one input channel (MI355X selector: direct)
     (2, 3, 16, 16, 17, 4, 2, 1),     # k4 s2 p1, 3 input channels: masked cell-wise input gradient
+    (1, 2, 8, 16, 64, 4, 2, 1),      # k4 s2 p1 to 32-column rows: fp32 cell forward with the ReLU fused
 ]
 
 

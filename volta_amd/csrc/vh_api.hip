@@ -279,6 +279,11 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
   }
   ConvGeom g = geom_of(d);
   const long RS = d.KH * d.KW;
+  if (dt == VH_F32 && g_fast_paths) {
+    // 4x4 stride 2 from a few channels (the up-sampling layer's input gradient)
+    int r = cell_fwd_f32(x, w, bias, y, g, act, st);
+    if (r != VH_ERR_UNSUPPORTED) return r;
+  }
   // weight staging: the generic layout, or the halo kernel's channel-grouped one (padded to 16 channels)
   const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
                                  halo_conv_bf16_ws((int)d.C, (int)d.O, (int)d.KH, (int)d.KW));

@@ -1303,6 +1303,120 @@ int run_direct_dgrad(const void* dy, const void* w, void* dx, const ConvGeom& g,
   return VH_OK;
 }
 
+// Forward of the same geometry seen from the other side (fp32): y[n][o][p][q] =
+// sum over (c, r, s) of x[n][c][2p - 1 + r][2q - 1 + s] w[o][c][r][s] with at
+// most 4 input channels and 64 output channels (the input gradient of the
+// up-sampling ConvTranspose2d layer), on v_mfma_f32_32x32x2f32: rows o, columns
+// the 128 positions of 4 output rows x 32 columns, K = (c, r, s) = 16 C.  A
+// block stages the weights [o][k] and the 10 x rows its positions read (zeros
+// outside the image) in LDS; wave w takes o 32 (w >> 1) .. + 31 and the 64
+// positions of output rows 2 (w & 1), 2 (w & 1) + 1.
+constexpr int kCfXP = 76;  // x row pitch (12 * row mod 64 spreads the rows' banks)
+constexpr int kCfWP = 66;  // weight row pitch (k and k + 1 on even / odd banks)
+
+__global__ __launch_bounds__(256) void cell_fwd_f32_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           const float* __restrict__ bias, float* __restrict__ y,
+                                                           ConvGeom g, int nseg, int tiles, int act) {
+  __shared__ __attribute__((aligned(16))) float xs[4 * 10 * kCfXP];
+  __shared__ __attribute__((aligned(16))) float wsh[64 * kCfWP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int C = g.C, O = g.O, K = C * 16;
+  const int t = blockIdx.x;
+  if (t >= tiles) return;
+  const int seg = t % nseg, rest = t / nseg;
+  const int prt = g.P / 4 + (g.P % 4 != 0);
+  const int p0 = (rest % prt) * 4, img = rest / prt;
+  const long HW = (long)g.H * g.W;
+  // every load of the prologue is issued before its LDS stores: the weights
+  // [o][k] (K % 4 == 0: float4 units, at most 1024 = 4 per thread; rows past O
+  // zero) and x rows 2 p0 - 1 .. 2 p0 + 8, columns 64 seg - 4 + 4j (18 float4
+  // chunks per row, at most 720 = 3 per thread; zeros outside the image)
+  float4 wv[4], xv[3];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = tid + u * 256;
+    wv[u] = i < O * K / 4 ? reinterpret_cast<const float4*>(w)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = tid + u * 256;
+    xv[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < C * 10 * 18) {
+      const int row = i / 18, j = i - row * 18;
+      const int c = row / 10, e = row - c * 10;
+      const int h = 2 * p0 - 1 + e, col = seg * 64 - 4 + 4 * j;
+      if (h >= 0 && h < g.H && col >= 0 && col < g.W)
+        xv[u] = *reinterpret_cast<const float4*>(x + ((long)img * C + c) * HW + (long)h * g.W + col);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = tid + u * 256;
+    if (i < 64 * K / 4) {  // rows o >= O get the zeros loaded for them
+      const int o = i / (K / 4), k = (i - o * (K / 4)) * 4;
+      *reinterpret_cast<float2*>(&wsh[o * kCfWP + k]) = make_float2(wv[u].x, wv[u].y);
+      *reinterpret_cast<float2*>(&wsh[o * kCfWP + k + 2]) = make_float2(wv[u].z, wv[u].w);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 3; ++u) {
+    const int i = tid + u * 256;
+    if (i < C * 10 * 18) {
+      const int row = i / 18, j = i - row * 18;
+      *reinterpret_cast<float4*>(&xs[row * kCfXP + 4 * j]) = xv[u];
+    }
+  }
+  __syncthreads();
+  const int om = (wave >> 1) * 32, pr0 = (wave & 1) * 2;
+  const int fr = lane & 31, fk = lane >> 5;
+  f32x16 acc[2] = {f32x16{}, f32x16{}};
+  const float* wa = wsh + (om + fr) * kCfWP + fk;
+  // column j of the wave: output row pr0 + j, column fr of the segment
+  for (int kk = 0; kk < K; kk += 2) {
+    const int c = kk >> 4, r = (kk >> 2) & 3, s0 = kk & 3;  // k = kk + fk: s = s0 + fk
+    const float a = wa[kk];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float b = xs[(c * 10 + 2 * (pr0 + j) + r) * kCfXP + 2 * fr + 3 + s0 + fk];
+      acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, acc[j], 0, 0, 0);
+    }
+  }
+  const long PQ = (long)g.P * g.Q;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = p0 + pr0 + j;
+    if (p >= g.P) continue;
+    const long base = (long)img * O * PQ + (long)p * g.Q + seg * 32 + fr;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int o = om + (v >> 2) * 8 + fk * 4 + (v & 3);
+      if (o < O) {
+        float val = acc[j][v] + (bias ? bias[o] : 0.f);
+        if (act == 1) val = fmaxf(val, 0.f);
+        y[base + (long)o * PQ] = val;
+      }
+    }
+  }
+}
+
+// Envelope of cell_fwd_f32: 4x4 taps, stride 2, padding 1, H = 2P, W = 2Q,
+// Q % 32 == 0, C <= 4, O <= 64, 16-byte aligned x.
+int cell_fwd_f32(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, int act,
+                 hipStream_t st) {
+  if (!(g.R == 4 && g.S == 4 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.C >= 1 && g.C <= 4 &&
+        g.O >= 1 && g.O <= 64 && g.Q % 32 == 0 && g.H == 2 * g.P && g.W == 2 * g.Q && act >= 0 && act <= 1 &&
+        ((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0))
+    return VH_ERR_UNSUPPORTED;
+  const int nseg = g.Q / 32, prt = (g.P + 3) / 4;
+  const long tiles = (long)g.N * prt * nseg;
+  if (tiles >= (1L << 31)) return VH_ERR_UNSUPPORTED;
+  cell_fwd_f32_kernel<<<(unsigned)tiles, 256, 0, st>>>((const float*)x, (const float*)w, (const float*)bias,
+                                                      (float*)y, g, nseg, (int)tiles, act);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 // Few-channel ConvTranspose-shaped weight gradient (fp32): the geometry the
 // cell kernels take (4x4 taps, stride 2, padding 1, H = 2P, W = 2Q) with C <= 4,
 // O <= 64, Q a multiple of 32 and W of 4, 16-byte aligned operands.

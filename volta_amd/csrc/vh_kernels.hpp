@@ -102,6 +102,10 @@ int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mod
 
 // bf16 stride-1 forward for C*R*S <= 128 with K packed as (c, r, s) (vh_smallc.hip);
 // act 0 none, 1 ReLU.  VH_ERR_UNSUPPORTED outside that range.
+// Forward of a 4x4 stride-2 pad-1 layer with at most 4 input and 64 output
+// channels (fp32; act 0 or 1 = ReLU): VH_ERR_UNSUPPORTED outside that envelope.
+int cell_fwd_f32(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g, int act,
+                 hipStream_t st);
 // Few-channel weight gradient of a 4x4 stride-2 pad-1 layer (fp32; dW and,
 // when db is non-null, the bias gradient of x's channels): VH_ERR_UNSUPPORTED
 // outside its envelope or when ws is smaller than convt_cell_wgrad_ws.
