@@ -605,6 +605,27 @@ __global__ __launch_bounds__(256) void wgrad_reduce_bf16_kernel(const float* __r
   }
 }
 
+// The same reduction read as float4 quads in split groups (many splits, few
+// outputs: the few-channel kernel's 512 slabs), for R*S*O*C % 4 == 0 and
+// O % 4 == 0 with 16-byte aligned slabs; the same fixed order for every run.
+__global__ __launch_bounds__(256) void wgrad_reduce_vec4_bf16_kernel(const float* __restrict__ part, int splits,
+                                                                     int RS, int O, int C, uint16_t* __restrict__ dw,
+                                                                     const float* __restrict__ bpart,
+                                                                     uint16_t* __restrict__ db, int nbw, int lg_g) {
+  if ((int)blockIdx.x < nbw) {
+    reduce_splits_vec4_block(part, splits, (long)RS * O * C, lg_g, [&](long i, float s) {
+      const int c = (int)(i % C);
+      const long t = i / C;
+      const int o = (int)(t % O);
+      const int tap = (int)(t / O);
+      dw[((long)o * C + c) * RS + tap] = f32_to_bf16(s);
+    }, (int)blockIdx.x, nbw);
+  } else {
+    reduce_splits_vec4_block(bpart, splits, (long)O, lg_g, [&](long i, float s) { db[i] = f32_to_bf16(s); },
+                             (int)blockIdx.x - nbw, (int)gridDim.x - nbw);
+  }
+}
+
 // The same for partials in the row kernel's accumulator layout (see the top of
 // this file): element i of a split is ((((tile * 4 + wave) * RS + tap) * 4 + j)
 // * 64 + lane) * 4 + k, i.e. dW[o][c][tap] with
@@ -1069,6 +1090,15 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
     sa.dbias_part = db ? (float*)((char*)ws + ((pbytes + 255) & ~size_t(255))) : nullptr;
     VH_TRY_W(launch_smallc(sa, R, S, pw, st));
     const long total = (long)R * S * O * C;
+    if (total % 4 == 0 && O % 4 == 0) {
+      // slabs start 16-byte aligned (ws, and the bias slabs at a 256-byte offset)
+      const int lg_g = reduce_vec4_lg_groups(splits);
+      const int nbw = reduce_vec4_grid(total, lg_g), nbb = db ? reduce_vec4_grid(O, lg_g) : 0;
+      wgrad_reduce_vec4_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, splits, R * S, O, C, (uint16_t*)dw,
+                                                               sa.dbias_part, (uint16_t*)db, nbw, lg_g);
+      VH_LAUNCH_CHECK();
+      return VH_OK;
+    }
     const int nbw = reduce_splits_grid(total), nbb = db ? reduce_splits_grid(O) : 0;
     wgrad_reduce_bf16_kernel<<<nbw + nbb, 256, 0, st>>>(ws, splits, R * S, O, C, (uint16_t*)dw, sa.dbias_part,
                                                         (uint16_t*)db, nbw);
