@@ -670,8 +670,10 @@ __global__ __launch_bounds__(256) void wgrad_reduce_frag_bf16_kernel(const float
 //   A[o][k] = dY[o][p][v + pw - s]   (lane: o = lane % 16, k = 8 * (lane / 16) ..)
 //   B[k][c] = x[c][p + r - ph][v]    (lane: c = lane % 16, same k)
 // Operands come straight from global memory (no LDS): each lane loads the
-// aligned 8-column chunks v-8, v, v+8 of its dY row (the windows of the S taps
-// are funnel shifts of these) and the chunk v of its x channel in the R rows.
+// aligned 8-column chunk v of its dY row -- its neighbours' chunks v-8 and v+8
+// come from the lanes 16 below and above (ds_bpermute), the wave's outer ones
+// from one more load -- (the windows of the S taps are funnel shifts of these)
+// and the chunk v of its x channel in the R rows.
 // Wave w of a block owns o0 + 16w .. +16 and walks the block's range of K steps
 // (n, 32-column chunk, p), p fastest, with the next step's loads in flight; a
 // step of the same chunk keeps R - 1 x rows of the previous one in registers.  Partials:
@@ -722,8 +724,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int step_e = min(a.total_steps, step_b + a.steps_per_split);
   const int nsteps = step_e - step_b;  // >= 1 (splits are sized so)
 
+  // cz: this lane's dY chunk (columns v .. v+7); ce: the chunk past the
+  // wave's 32 columns on its side (v - 8 for kg = 0, v + 8 for kg = 3, zeros
+  // elsewhere) -- the other lanes take their neighbours' cz at compute time
   struct Ops {
-    u32x4w cm, cz, cp, x[R];
+    u32x4w ce, cz, x[R];
   };
   // position of a step: (n, column chunk, p), p fastest, advanced
   // incrementally: consecutive steps of a chunk share R - 1 of their x rows
@@ -744,10 +749,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto load_dy = [&](Ops& f) {
     const int v = qc * 32 + kg * 8;  // this lane's 8 x columns v .. v+7
     const int drow = o_ok ? ((n * a.O + o) * PQ + p * a.Q) * 2 : 0;
-    const int vm = v - 8, vp = v + 8;
-    f.cm = BufLoad<8>::ld(dyr, o_ok && vm >= 0 && vm < a.Q ? drow + vm * 2 : OOR, 0);
+    const int ve = kg == 0 ? v - 8 : v + 8;
+    const bool edge = kg == 0 || kg == 3;
     f.cz = BufLoad<8>::ld(dyr, o_ok && v < a.Q ? drow + v * 2 : OOR, 0);
-    f.cp = BufLoad<8>::ld(dyr, o_ok && vp < a.Q ? drow + vp * 2 : OOR, 0);
+    f.ce = BufLoad<8>::ld(dyr, edge && o_ok && ve >= 0 && ve < a.Q ? drow + ve * 2 : OOR, 0);
   };
   auto load = [&](Ops& f) {
     load_dy(f);
@@ -784,9 +789,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool do_bias = a.dbias_part != nullptr;
 
   auto compute = [&](const Ops& f) {
-    // dY columns v + PW - s: window start 8 + PW - s in (cm, cz, cp)
+    // dY columns v + PW - s: window start 8 + PW - s in (cm, cz, cp); cm and
+    // cp are the cz of the lanes 16 below / above (same o, the next 8 columns)
+    u32x4w cm, cp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (uint32_t)__shfl((int)f.cz[i], lane - 16, 64);
+      const uint32_t hi = (uint32_t)__shfl((int)f.cz[i], lane + 16, 64);
+      cm[i] = kg == 0 ? f.ce[i] : lo;
+      cp[i] = kg == 3 ? f.ce[i] : hi;
+    }
     bf16x8 af[S];
-    DyWindows<8 + PW, S>::run(af, f.cm, f.cz, f.cp);
+    DyWindows<8 + PW, S>::run(af, cm, f.cz, cp);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const bf16x8 bx = __builtin_bit_cast(bf16x8, f.x[r]);
