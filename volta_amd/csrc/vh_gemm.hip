@@ -65,7 +65,14 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
     pa.d = ws;
     igemm_kernel<T, AK, BKIND, OK_PARTIAL, BM, BN, BK><<<grid, 256, 0, st>>>(pa);
     VH_LAUNCH_CHECK();
-    splitk_reduce_kernel<T, OUT><<<reduce_splits_grid((long)a.M * a.N), 256, 0, st>>>(a, ws, p.splits);
+    // few splits of a large weight gradient: the coalesced OIHW reduction
+    if (OUT == OK_WGRAD_OIHW && a.bias_mode == 0 && a.act == 0 && a.wg_rs <= 64 && p.splits <= 8 &&
+        (long)a.wg_c * a.wg_rs == a.N) {
+      splitk_reduce_oihw_kernel<T><<<dim3((unsigned)a.M, (unsigned)((a.wg_c + 63) / 64)), 256,
+                                     (size_t)a.wg_rs * 65 * sizeof(float), st>>>(a, ws, p.splits);
+    } else {
+      splitk_reduce_kernel<T, OUT><<<reduce_splits_grid((long)a.M * a.N), 256, 0, st>>>(a, ws, p.splits);
+    }
     VH_LAUNCH_CHECK();
   } else {
     igemm_kernel<T, AK, BKIND, OUT, BM, BN, BK><<<grid, 256, 0, st>>>(a);

@@ -544,4 +544,35 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(IgemmArgs args, cons
   });
 }
 
+// The same for the weight-gradient scatter (OK_WGRAD_OIHW, no bias or
+// activation): block (o, 64-channel chunk) sums the partials of its 64 c x R*S
+// columns (rows of the [RS][C] column order, contiguous in c) in split order
+// into LDS, then writes dW[o][c0 .. c0+63][0 .. RS) as one contiguous run.
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_reduce_oihw_kernel(IgemmArgs args, const float* __restrict__ ws,
+                                                                 int splits) {
+  using S = typename Elem<T>::storage;
+  extern __shared__ float tile[];  // [RS][65]
+  const int o = blockIdx.x, c0 = blockIdx.y * 64;
+  const int C = args.wg_c, RS = args.wg_rs;
+  const int nc = min(64, C - c0);
+  const long MN = (long)args.M * args.N;
+  for (int i = threadIdx.x; i < RS * 64; i += 256) {
+    const int rs = i >> 6, cl = i & 63;
+    float s = 0.f;
+    if (cl < nc) {
+      const float* p = ws + (long)o * args.N + (long)rs * C + c0 + cl;
+#pragma unroll 8
+      for (int z = 0; z < splits; ++z) s += p[z * MN];
+    }
+    tile[rs * 65 + cl] = s;
+  }
+  __syncthreads();
+  S* d = reinterpret_cast<S*>(args.d) + ((long)o * C + c0) * RS;
+  for (int i = threadIdx.x; i < nc * RS; i += 256) {
+    const int cl = i / RS, rs = i - cl * RS;
+    d[i] = Elem<T>::from_f32(tile[rs * 65 + cl]);
+  }
+}
+
 }  // namespace vh
