@@ -705,8 +705,9 @@ static int im2col_bwd(int dt, const void* dy, const void* x, const void* w, void
   return VH_OK;
 }
 
+// db non-null: the bias gradient too where the per-tap kernel applies (*db_done).
 static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const ConvDims& d, hipStream_t st,
-                        size_t* need = nullptr) {
+                        size_t* need = nullptr, void* db = nullptr, bool* db_done = nullptr) {
   ConvGeom g = geom_of(d);
   int slices, len;
   size_t bytes = VH_DISPATCH(dt, direct_wgrad_ws, g, &slices, &len);
@@ -716,7 +717,7 @@ static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const C
   }
   void* ws;
   VH_TRY(ws_get(st, bytes, &ws));
-  return VH_DISPATCH(dt, run_direct_wgrad, dy, x, dw, g, (float*)ws, slices, len, st);
+  return VH_DISPATCH(dt, run_direct_wgrad, dy, x, dw, g, (float*)ws, slices, len, st, db, db_done);
 }
 
 
@@ -1204,7 +1205,11 @@ static int conv2d_backward_impl(int dtype, int algo, const void* out_grad, const
     ConvGeom g = geom_of(d);
     if (grad_input) VH_TRY(VH_DISPATCH(dtype, run_direct_dgrad, out_grad, weight, grad_input, g, st));
     if (mask) VH_TRY(mask_after(dtype, mask, grad_input, d.B * d.C * d.H * d.W, st));
-    if (grad_weight) VH_TRY(direct_wgrad(dtype, out_grad, input, grad_weight, d, st));
+    if (grad_weight) {
+      bool db_done = false;
+      VH_TRY(direct_wgrad(dtype, out_grad, input, grad_weight, d, st, nullptr, grad_bias, &db_done));
+      if (db_done) grad_bias = nullptr;
+    }
   }
   if (grad_bias) VH_TRY(bias_grad_nchw(dtype, out_grad, grad_bias, d.B, d.O, d.HO * d.WO, st));
   return VH_OK;

@@ -608,7 +608,8 @@ __global__ __launch_bounds__(256) void sum_partials_kernel(const float* __restri
 template <typename T, int R, int S>
 __global__ __launch_bounds__(256) void direct_wgrad_taps_kernel(const typename Elem<T>::storage* __restrict__ dy,
                                                                 const typename Elem<T>::storage* __restrict__ x,
-                                                                float* __restrict__ part, ConvGeom g, int slice) {
+                                                                float* __restrict__ part, ConvGeom g, int slice,
+                                                                float* __restrict__ bpart) {
   const int oc = blockIdx.x;
   const int c = oc % g.C, o = oc / g.C;
   const int npos = g.N * g.P * g.Q;
@@ -616,11 +617,13 @@ __global__ __launch_bounds__(256) void direct_wgrad_taps_kernel(const typename E
   float acc[R * S];
 #pragma unroll
   for (int t = 0; t < R * S; ++t) acc[t] = 0.f;
+  float bsum = 0.f;  // the bias partial: dY over the slice (blocks of channel 0)
   for (int i = b + threadIdx.x; i < e; i += 256) {
     uint32_t n, pq, p, q;
     g.fPQ.divmod((uint32_t)i, n, pq);
     g.fQ.divmod(pq, p, q);
     const float gv = Elem<T>::to_f32(dy[(((long)n * g.O + o) * g.P + p) * g.Q + q]);
+    bsum += gv;
     const long xb = ((long)n * g.C + c) * g.H * g.W;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -642,6 +645,29 @@ __global__ __launch_bounds__(256) void direct_wgrad_taps_kernel(const typename E
   __syncthreads();
   for (int t = threadIdx.x; t < R * S; t += 256)
     part[((long)blockIdx.y * gridDim.x + oc) * (R * S) + t] = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+  if (bpart && c == 0) {
+    const float v = wave_sum(bsum);
+    __shared__ float bred[4];
+    if ((threadIdx.x & 63) == 0) bred[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) bpart[(long)blockIdx.y * g.O + o] = (bred[0] + bred[1]) + (bred[2] + bred[3]);
+  }
+}
+
+// dW = sum of the slices' partials [slice][nw], and (db non-null) dB = sum of
+// the bias partials [slice][O] that follow them; fixed split order.
+template <typename T>
+__global__ __launch_bounds__(256) void direct_wgrad_reduce_kernel(const float* __restrict__ part, int slices, long nw,
+                                                                  int O, typename Elem<T>::storage* __restrict__ dw,
+                                                                  typename Elem<T>::storage* __restrict__ db,
+                                                                  int nbw) {
+  if ((int)blockIdx.x < nbw)
+    reduce_splits_block(part, slices, nw, [&](long i, float v) { dw[i] = Elem<T>::from_f32(v); }, (int)blockIdx.x,
+                        nbw);
+  else
+    reduce_splits_block(part + (long)slices * nw, slices, (long)O,
+                        [&](long i, float v) { db[i] = Elem<T>::from_f32(v); }, (int)blockIdx.x - nbw,
+                        (int)gridDim.x - nbw);
 }
 
 static bool direct_wgrad_taps_ok(const ConvGeom& g) {
@@ -1513,7 +1539,7 @@ size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
     const int sl = direct_wgrad_taps_slices(g);
     *slice_len = (int)((npos + sl - 1) / sl);
     *slices = (int)((npos + *slice_len - 1) / *slice_len);
-    return (size_t)(*slices) * nw * sizeof(float);
+    return (size_t)(*slices) * (nw + g.O) * sizeof(float);  // + the bias partials
   }
   int sl = (int)std::min<long>(std::max<long>(1, (2048 + nw - 1) / nw), std::max<long>(1, npos / 1024));
   sl = std::min(sl, 1024);
@@ -1525,17 +1551,26 @@ size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
 
 template <typename T>
 int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g, float* ws, int slices,
-                     int slice_len, hipStream_t st) {
+                     int slice_len, hipStream_t st, void* db, bool* db_done) {
   using S = typename Elem<T>::storage;
   long nw = (long)g.O * g.C * g.R * g.S;
+  if (db_done) *db_done = false;
   if (direct_wgrad_taps_ok(g)) {
+    if (db_done) *db_done = db != nullptr;
+    // the bias partials ride along (dB of the same pass, one reduction launch)
+    float* bp = db ? ws + (long)slices * nw : nullptr;
     dim3 grid((unsigned)(g.O * g.C), (unsigned)slices);
     if (g.R == 3)
-      direct_wgrad_taps_kernel<T, 3, 3><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+      direct_wgrad_taps_kernel<T, 3, 3><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len, bp);
     else if (g.R == 5)
-      direct_wgrad_taps_kernel<T, 5, 5><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+      direct_wgrad_taps_kernel<T, 5, 5><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len, bp);
     else
-      direct_wgrad_taps_kernel<T, 1, 1><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
+      direct_wgrad_taps_kernel<T, 1, 1><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len, bp);
+    VH_LAUNCH_CHECK();
+    const int nbw = reduce_splits_grid(nw), nbb = db ? reduce_splits_grid(g.O) : 0;
+    direct_wgrad_reduce_kernel<T><<<nbw + nbb, 256, 0, st>>>(ws, slices, nw, g.O, (S*)dw, (S*)db, nbw);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
   } else {
     dim3 grid((unsigned)nw, (unsigned)slices);
     direct_wgrad_kernel<T><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, slice_len);
@@ -1859,7 +1894,7 @@ int run_optimizer_step(int op, float lr, float beta1, float beta2, float t, floa
   template int run_channel_bias_add<T>(void*, const void*, long, int, long, hipStream_t);               \
   template size_t direct_wgrad_ws<T>(const ConvGeom&, int*, int*);                                      \
   template int run_direct_wgrad<T>(const void*, const void*, void*, const ConvGeom&, float*, int, int,  \
-                                   hipStream_t);                                                        \
+                                   hipStream_t, void*, bool*);                                          \
   template int run_pad<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);               \
   template int run_crop<T>(const void*, void*, int, int, int, int, int, int, hipStream_t);              \
   template int run_im2col<T>(const void*, void*, int, int, int, int, int, int, int, int, int, int,      \

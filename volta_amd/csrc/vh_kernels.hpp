@@ -41,9 +41,11 @@ int run_dgrad_smallc(const void* dy, const void* w, const void* bias, const void
 // y[n][c][hw] += bias[c]
 template <typename T> int run_channel_bias_add(void* y, const void* bias, long N, int C, long HW, hipStream_t st);
 template <typename T> size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len);
+// db non-null: the bias gradient in the same passes where the per-tap kernel
+// applies (*db_done set true), else left to the caller.
 template <typename T>
 int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g, float* ws, int slices,
-                     int slice_len, hipStream_t st);
+                     int slice_len, hipStream_t st, void* db = nullptr, bool* db_done = nullptr);
 template <typename T> int run_pad(const void* x, void* xp, int B, int C, int H, int W, int ph, int pw, hipStream_t st);
 template <typename T> int run_crop(const void* xp, void* x, int B, int C, int H, int W, int ph, int pw, hipStream_t st);
 template <typename T>
