@@ -45,34 +45,34 @@ METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
 # `bench.py --profile-op headline` (FETCH_SIZE, then WRITE_SIZE, KiB per
 # dispatch, summed over the pass's kernels).  Calibration on the 256 MiB copy
 # of the same runs (one dispatch): WRITE_SIZE reads 262144 KiB (factor 1),
-# FETCH_SIZE 131089 KiB (factor 2).  Summary: profiles/c3_pass_traffic.md.
+# FETCH_SIZE 131088 KiB (factor 2).  Summary: profiles/c3_pass_traffic.md.
 # Keyed by pass name; used for roofline.traffic when that pass is the dominant
 # one (which pass is the slowest varies by a few percent from run to run).
 MEASURED_TRAFFIC_BYTES = {
-    # relayout_grouped_kernel: fetch 79 x2, write 72; conv_halo_bf16_kernel: fetch 25683 x2, write 50176
-    "3x3 64->64 @56 fwd": int((25762 * 2 + 50248) * 1024),
-    # relayout_grouped_kernel: fetch 214 x2, write 72; conv_halo_bf16_kernel: fetch 25683 x2, write 50176
-    "3x3 64->64 @56 dgrad": int((25897 * 2 + 50248) * 1024),
-    # wgrad_rows_bf16_kernel: fetch 52796 x2, write 9216; wgrad_reduce_frag_bf16_kernel: fetch 4646 x2, write 72
-    "3x3 64->64 @56 wgrad": int((57442 * 2 + 9288) * 1024),
-    # conv_halo_bf16_kernel: fetch 13840 x2, write 25159
-    "3x3 128->128 @28 fwd": int((13840 * 2 + 25159) * 1024),
-    # relayout_grouped_kernel: fetch 838 x2, write 288; conv_halo_bf16_kernel: fetch 13832 x2, write 25150
-    "3x3 128->128 @28 dgrad": int((14670 * 2 + 25438) * 1024),
-    # wgrad_rows_bf16_kernel: fetch 25195 x2, write 9216; wgrad_reduce_frag_bf16_kernel: fetch 4646 x2, write 288
-    "3x3 128->128 @28 wgrad": int((29841 * 2 + 9504) * 1024),
-    # conv_halo_bf16_kernel: fetch 11551 x2, write 12640
-    "3x3 256->256 @14 fwd": int((11551 * 2 + 12640) * 1024),
-    # relayout_grouped_kernel: fetch 3334 x2, write 1152; conv_halo_bf16_kernel: fetch 11550 x2, write 12653
-    "3x3 256->256 @14 dgrad": int((14884 * 2 + 13805) * 1024),
+    # relayout_grouped_kernel: fetch 77 x2, write 76; conv_halo_bf16_kernel: fetch 25684 x2, write 50176
+    "3x3 64->64 @56 fwd": int((25761 * 2 + 50252) * 1024),
+    # relayout_grouped_kernel: fetch 202 x2, write 76; conv_halo_bf16_kernel: fetch 25682 x2, write 50176
+    "3x3 64->64 @56 dgrad": int((25884 * 2 + 50252) * 1024),
+    # wgrad_rows_bf16_kernel: fetch 52800 x2, write 9216; wgrad_reduce_frag_bf16_kernel: fetch 4646 x2, write 72
+    "3x3 64->64 @56 wgrad": int((57446 * 2 + 9288) * 1024),
+    # conv_halo_bf16_kernel: fetch 13811 x2, write 25152
+    "3x3 128->128 @28 fwd": int((13811 * 2 + 25152) * 1024),
+    # relayout_grouped_kernel: fetch 796 x2, write 304; conv_halo_bf16_kernel: fetch 13880 x2, write 25149
+    "3x3 128->128 @28 dgrad": int((14676 * 2 + 25453) * 1024),
+    # wgrad_rows_bf16_kernel: fetch 25199 x2, write 9216; wgrad_reduce_frag_bf16_kernel: fetch 4646 x2, write 288
+    "3x3 128->128 @28 wgrad": int((29845 * 2 + 9504) * 1024),
+    # conv_halo_bf16_kernel: fetch 11549 x2, write 12686
+    "3x3 256->256 @14 fwd": int((11549 * 2 + 12686) * 1024),
+    # relayout_grouped_kernel: fetch 3172 x2, write 1216; conv_halo_bf16_kernel: fetch 11801 x2, write 12650
+    "3x3 256->256 @14 dgrad": int((14973 * 2 + 13866) * 1024),
     # wgrad_rows_bf16_kernel: fetch 12651 x2, write 36864; wgrad_reduce_frag_bf16_kernel: fetch 18469 x2, write 1152
     "3x3 256->256 @14 wgrad": int((31120 * 2 + 38016) * 1024),
-    # pw_fwd_bf16_kernel: fetch 27989 x2, write 25122
-    "1x1 s2 64->128 @56 fwd": int((27989 * 2 + 25122) * 1024),
-    # pw_dgrad_bf16_kernel: fetch 17766 x2, write 53372
-    "1x1 s2 64->128 @56 dgrad": int((17766 * 2 + 53372) * 1024),
-    # pw_wgrad_s2_bf16_kernel: fetch 39874 x2, write 7168; sum_partials_vec4_kernel: fetch 3606 x2, write 16
-    "1x1 s2 64->128 @56 wgrad": int((43480 * 2 + 7184) * 1024),
+    # pw_fwd_vec_bf16_kernel: fetch 26593 x2, write 25111
+    "1x1 s2 64->128 @56 fwd": int((26593 * 2 + 25111) * 1024),
+    # pw_dgrad_vec_bf16_kernel: fetch 15727 x2, write 51674
+    "1x1 s2 64->128 @56 dgrad": int((15727 * 2 + 51674) * 1024),
+    # pw_wgrad_s2_bf16_kernel: fetch 39878 x2, write 7168; sum_partials_vec4_kernel: fetch 3606 x2, write 16
+    "1x1 s2 64->128 @56 wgrad": int((43484 * 2 + 7184) * 1024),
 }
 
 # (name, C, O, H, K, stride, pad) at N=128
