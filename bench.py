@@ -458,9 +458,11 @@ def _dx_literal_per_iter(O, K, S, P, W, rows=8):
 
 
 def cpu_config0():
-    """configs[0] on Volta's CPU path (auto-select: conv1 Im2col, conv2 Direct,
-    conv.rs:55-68): everything in full except the Direct input-gradient scan of
-    conv2 (8.0e10 iterations), timed on a strip and extrapolated."""
+    """configs[0] on Volta's CPU path in full (auto-select: conv1 Im2col, conv2
+    Direct, conv.rs:55-68): forward, sum loss, seed, conv2's Direct weight
+    gradient and its literal O(B*C*H*W*O*P*Q) input-gradient scan
+    (conv.rs:450-515, 8.0e10 iterations), the ReLU backward and conv1's Im2col
+    backward, all at N=64."""
     import numpy as np
 
     import oracle
@@ -470,44 +472,41 @@ def cpu_config0():
     w1 = rng.uniform(-0.8165, 0.8165, (32, 1, 3, 3)).astype(np.float32)
     w2 = rng.uniform(-0.1443, 0.1443, (64, 32, 3, 3)).astype(np.float32)
     kw = dict(stride=(1, 1), pad=(1, 1))
-    t = 0.0
     t0 = time.perf_counter()
     h = oracle.relu(oracle.im2col_conv_forward(x, w1, **kw))
     y = oracle.direct_conv(h, w2, **kw)
     oracle.sum_all(y)
     dy = oracle.sum_backward(1.0, y.shape)
     oracle.direct_conv_backward_weight(dy, h, w2.shape, **kw)
-    dh = oracle.relu_backward(np.ones_like(h), h)
+    dh = oracle.direct_conv_backward_input(dy, w2, h.shape, literal=True, **kw)
+    dh = oracle.relu_backward(dh, h)
     oracle.im2col_conv_backward(dh, x, w1, **kw)
     t = time.perf_counter() - t0
-    per, ts = _dx_literal_per_iter(64, 3, 1, 1, 28)
-    tdx = per * N * 32 * 28 * 28 * 64 * 28 * 28
-    return t + tdx, t + ts, ("full graph except conv2's literal Direct dX scan, which is timed on an 8-row strip "
-                             "of 1 input channel of 1 image and extrapolated")
+    return t, t, "the full graph at N=64, conv2's input gradient as Volta's literal Direct scan"
 
 
 _LINEAR_CPU = {}
 
 
 def cpu_config1_linear():
-    """configs[1] Linear 4096x1024 -> 4096 fwd + dX + dW + db (MatMulGradFn,
-    matmul.rs:450-460, 563-574; bias grad binary.rs:533-598) on 256 of the 4096
-    rows (every pass is linear in the rows), x16.  bf16 has no CPU arithmetic in
-    the reference (f32 math on bf16-rounded values): the same loops."""
+    """configs[1] Linear 4096x1024 -> 4096 fwd + dX + dW + db in full
+    (MatMulGradFn, matmul.rs:450-460, 563-574; bias grad binary.rs:533-598).
+    bf16 has no CPU arithmetic in the reference (f32 math on bf16-rounded
+    values): the same loops, timed once."""
     if "v" not in _LINEAR_CPU:
         import numpy as np
 
         import oracle
         rng = np.random.default_rng(0)
-        ms = 256
-        x = rng.standard_normal((ms, 1024)).astype(np.float32)
+        m = 4096
+        x = rng.standard_normal((m, 1024)).astype(np.float32)
         w = rng.uniform(-0.0765, 0.0765, (1024, 4096)).astype(np.float32)
         b = np.zeros(4096, np.float32)
-        dy = rng.standard_normal((ms, 4096)).astype(np.float32)
+        dy = rng.standard_normal((m, 4096)).astype(np.float32)
         t = _t(oracle.linear_forward, x, w, b) + _t(oracle.linear_backward, dy, x, w)
-        _LINEAR_CPU["v"] = (t * 4096 / ms, t)
+        _LINEAR_CPU["v"] = (t, t)
     tot, meas = _LINEAR_CPU["v"]
-    return tot, meas, "256 of 4096 rows of fwd, dX, dW and db, x16"
+    return tot, meas, "all 4096 rows of fwd, dX, dW and db (timed once for both dtypes)"
 
 
 def cpu_config1_square():
@@ -528,15 +527,14 @@ def cpu_config1_square():
 
 def cpu_config3():
     """configs[3] ConvTranspose2d layers (conv_transpose.rs:356-435 forward,
-    161-341 backward) on 4 of the 128 images (every loop is linear in the batch), x32."""
+    161-341 backward) in full: every layer's forward and backward at N=128."""
     import numpy as np
 
     import oracle
     rng = np.random.default_rng(0)
-    ns = 4
     t = 0.0
     for CI, CO, H, K, S, P in C4_LAYERS:
-        x = rng.standard_normal((ns, CI, H, H)).astype(np.float32)
+        x = rng.standard_normal((C4_BATCH, CI, H, H)).astype(np.float32)
         w = rng.normal(0, 0.02, (CI, CO, K, K)).astype(np.float32)
         b = np.zeros(CO, np.float32)
         kw = dict(stride=(S, S), pad=(P, P))
@@ -544,7 +542,7 @@ def cpu_config3():
         y = oracle.conv_transpose_forward(x, w, b, **kw)
         oracle.conv_transpose_backward(np.ones_like(y), x, w, **kw)
         t += time.perf_counter() - t0
-    return t * C4_BATCH / ns, t, f"{ns} of {C4_BATCH} images of every layer's forward and backward, x{C4_BATCH // ns}"
+    return t, t, f"every layer's forward and backward at N={C4_BATCH}, in full"
 
 
 def cpu_config4(rows=8):

@@ -29,13 +29,19 @@
  *  - Every tensor must hold fewer than 2^31 elements (VH_ERR_UNSUPPORTED otherwise).
  *  - Workspace (split-K partials, re-laid-out weights, im2col matrices) is taken
  *    from one grow-only device buffer per stream inside the library; calls on
- *    one stream reuse it in stream order.  A buffer that a call outgrows is
- *    retired, not freed, so a HIP graph captured earlier from library calls
- *    stays valid; retired and current workspaces are freed only by
- *    vh_release_cache(), which therefore invalidates every such graph.  While a
- *    stream is being captured the library never allocates, frees or
- *    synchronises for it: a call whose workspace would have to grow returns
- *    VH_ERR_CAPTURE (run the call once eagerly on that stream before capturing).
+ *    one stream reuse it in stream order.  A HIP graph captured from library
+ *    calls on a stream holds that stream's workspace address: its replays
+ *    share the buffer with the capture stream's eager calls and with every
+ *    other graph captured on that stream, wherever they are replayed, so such
+ *    replays must be ordered with those calls and with each other (replay on
+ *    the capture stream, or synchronise between them).  A buffer that a call
+ *    outgrows is freed (after a synchronisation of its stream) when no
+ *    captured call used it, and otherwise retired, so such a graph stays
+ *    valid; retired and current workspaces are freed by vh_release_cache(),
+ *    which therefore invalidates every such graph.  While a stream is being
+ *    captured the library never allocates, frees or synchronises for it: a
+ *    call whose workspace would have to grow returns VH_ERR_CAPTURE (run the
+ *    call once eagerly on that stream before capturing).
  */
 #ifndef VOLTA_HIP_H
 #define VOLTA_HIP_H
@@ -84,6 +90,11 @@ int vh_stream_sync(void* stream);
  * synchronisation.  Invalidates every HIP graph captured from library calls;
  * must not be called while a stream is being captured. */
 int vh_release_cache(void);
+/* Diagnostics (no reference counterpart): the current workspace of `stream`
+ * (*ptr NULL and *bytes 0 when it has none yet) and how many outgrown
+ * workspaces are kept because a call captured into a HIP graph used them.  Any
+ * output pointer may be NULL. */
+int vh_workspace_info(void* stream, void** ptr, size_t* bytes, size_t* retired);
 /* Kernel choice inside an algorithm (no reference counterpart: Volta has one
  * shader per op).  VH_POLICY_FASTEST (default) uses specialised kernels where
  * their shape envelope allows; VH_POLICY_GENERIC forces the generic MFMA

@@ -137,3 +137,89 @@ def test_workspace_growth_during_capture_is_an_error():
     g2.replay()
     torch.cuda.synchronize()
     assert torch.equal(o["dw"], ref)
+
+
+def _hip_runtime():
+    """The HIP runtime already mapped into this process (torch's, which the
+    library shares through its soname)."""
+    import ctypes
+    paths = sorted({l.split()[-1] for l in open("/proc/self/maps") if "libamdhip64" in l})
+    assert len(paths) == 1, f"expected one HIP runtime in the process, found {paths}"
+    rt = ctypes.CDLL(paths[0])
+    rt.hipMemGetAddressRange.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t),
+                                         ctypes.c_void_p]
+    rt.hipMemGetAddressRange.restype = ctypes.c_int
+    return rt
+
+
+def _ws_info(stream):
+    import ctypes
+    from volta_amd import lib
+    p, b, r = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_size_t()
+    assert lib().vh_workspace_info(ctypes.c_void_p(stream.cuda_stream), ctypes.byref(p), ctypes.byref(b),
+                                   ctypes.byref(r)) == 0
+    return p.value, b.value, r.value
+
+
+def test_workspace_retire_rule():
+    """The rule that keeps captured graphs valid, pinned on the allocations
+    themselves: a workspace that a captured call used is retired when the
+    stream's workspace grows (it stays a live allocation of its full size, and
+    a replay still reproduces the eager result), while one that no capture
+    used is freed on growth (the retired count does not change).  A library
+    that freed every outgrown workspace fails the first part; one that
+    retired every outgrown workspace (unbounded memory) fails the second."""
+    import ctypes
+    rt = _hip_runtime()
+    conv, x, dy, o = _layer(64, 64, 3, 1, 1, 2, 14, seed=21)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+
+    def wgrad(layer, xx, gg, oo):
+        layer.backward(gg, xx, input_grad=False, weight_grad=True, algo=layer.algo, outs=(None, oo["dw"], oo["db"]))
+
+    with torch.cuda.stream(s):
+        wgrad(conv, x, dy, o)
+    torch.cuda.synchronize()
+    ref = o["dw"].clone()
+    p1, b1, r0 = _ws_info(s)
+    assert p1 and b1 > 0, "the weight gradient should take split-K workspace"
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        wgrad(conv, x, dy, o)
+    torch.cuda.synchronize()
+    assert _ws_info(s)[0] == p1, "a capture must not move the workspace"
+
+    # larger layers, run eagerly on `s` one after the other until the workspace grows
+    cands = iter([(64, 64, 16, 56), (128, 128, 32, 28), (256, 256, 32, 14), (256, 256, 128, 14),
+                  (128, 128, 128, 28), (64, 64, 128, 56)])
+
+    def grow():
+        before = _ws_info(s)
+        for i, (C, O, n, h) in enumerate(cands):
+            layer, xx, gg, oo = _layer(C, O, 3, 1, 1, n, h, seed=22 + i)
+            with torch.cuda.stream(s):
+                wgrad(layer, xx, gg, oo)
+            torch.cuda.synchronize()
+            if _ws_info(s)[1] > before[1]:
+                return _ws_info(s)
+        raise AssertionError("no candidate layer grew the workspace")
+
+    # growth after a capture: p1 retired, still allocated in full
+    p2, b2, r1 = grow()
+    assert p2 != p1 and b2 > b1
+    assert r1 == r0 + 1, "the workspace a captured call used must be retired"
+    base, size = ctypes.c_void_p(), ctypes.c_size_t()
+    assert rt.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ctypes.c_void_p(p1)) == 0, \
+        "the captured graph's workspace was freed"
+    assert base.value == p1 and size.value >= b1
+    o["dw"].fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(o["dw"], ref), "replay after the workspace grew differs from the eager result"
+
+    # growth with no capture in between: p2 is freed, nothing more is retired
+    p3, b3, r2 = grow()
+    assert b3 > b2
+    assert r2 == r1, "an outgrown workspace that no capture used must be freed, not retired"

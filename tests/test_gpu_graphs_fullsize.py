@@ -7,15 +7,19 @@ Every layer is checked on a few images against the oracle fed with the
 device's own inputs to that layer (so one bf16 rounding of an earlier layer
 does not propagate into the comparison): forward + bias + ReLU, the masked
 input gradient, the tail and the loss seed bit for bit, the loss against a
-float64 sum of the device output.  Weight gradients: configs[0] against the
-oracle over the whole batch; configs[4] (too large for the oracle in seconds)
-bit-identical to a separate call of the same pass, and its bias gradient
-against a float64 sum of the device's output gradient."""
+float64 sum of the device output.  Weight gradients of every layer against the
+oracle over the whole batch (configs[4]'s over image chunks in a thread pool,
+`tests/oracle_pool.py`), and bit-identical to a separate call of the same
+pass; bias gradients against a float64 sum of the device's output gradient.
+
+The same step captured in a HIP graph (as bench.py times it) is replayed at
+full size and must reproduce every buffer of the eager step bit for bit."""
 import numpy as np
 import pytest
 import torch
 
 import oracle
+from tests.oracle_pool import batch_sum
 from tests.parity import assert_parity, k_conv_dgrad, k_conv_fwd, k_conv_wgrad
 from volta_amd import nn as vnn
 
@@ -86,13 +90,11 @@ def test_config_graph_full_size(name, images):
         db_ref = gl.astype(np.float64).sum(axis=(0, 2, 3))
         db_sc = np.abs(gl).astype(np.float64).sum(axis=(0, 2, 3))
         assert_parity(db, db_ref, db_sc, dt, f"{name} L{li} db", k=kwg)
-        if name == "configs[0]":
-            ref = oracle.direct_conv_backward_weight(gl, acts[li], w.shape, **kw)
-            sc = oracle.direct_conv_backward_weight(np.abs(gl), np.abs(acts[li]), w.shape, **kw)
-            assert_parity(dw, ref, sc, dt, f"{name} L{li} dw", k=kwg)
-        else:
-            _, dw2, _ = conv.backward(chain.grads[li + 1], chain.acts[li], input_grad=False, weight_grad=True)
-            assert np.array_equal(dw, host(dw2)), f"{name} L{li} dw differs from the same pass called alone"
+        print(f"{name} L{li}: oracle weight gradient over the whole batch", flush=True)
+        ref, sc = batch_sum(oracle.direct_conv_backward_weight, (gl, acts[li]), (w.shape,), kw)
+        assert_parity(dw, ref, sc, dt, f"{name} L{li} dw", k=kwg)
+        _, dw2, _ = conv.backward(chain.grads[li + 1], chain.acts[li], input_grad=False, weight_grad=True)
+        assert np.array_equal(dw, host(dw2)), f"{name} L{li} dw differs from the same pass called alone"
     out = host(chain.output)
     if chain.tail is not None:
         assert np.array_equal(out, oracle.pixel_shuffle(acts[L], 3)), "PixelShuffle tail differs"
@@ -102,3 +104,35 @@ def test_config_graph_full_size(name, images):
         assert np.array_equal(grads[L], np.ones_like(acts[L])), "loss seed is not 1 everywhere"
     exact = float(out.astype(np.float64).sum())
     assert abs(float(host(loss)[0]) - exact) <= 1e-6 * float(np.abs(out).astype(np.float64).sum())
+
+
+@pytest.mark.parametrize("name", ["configs[0]", "configs[4]"])
+def test_config_graph_capture_replay_full_size(name):
+    """ConvChain.step() captured in a HIP graph after an eager warm-up on the
+    capture stream (bench.py's graph_ms_per_step): each replay, with the
+    buffers poisoned before it and eager library work between replays, equals
+    the eager step bit for bit."""
+    chain, dt = _build(name)
+    _set_biases(chain, dt)
+    bufs = lambda: ([chain.loss, chain.output] + list(chain.acts[1:]) + list(chain.grads[1:])
+                    + [t for pair in chain.wgrads for t in pair])
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        chain.step()
+    torch.cuda.synchronize()
+    ref = [b.clone() for b in bufs()]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        chain.step()
+    torch.cuda.synchronize()
+    for rep in range(2):
+        for b in bufs():
+            b.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (b, r) in enumerate(zip(bufs(), ref)):
+            assert torch.equal(b, r), f"{name} replay {rep}: buffer {i} differs from the eager step"
+        chain.convs[-1].forward(chain.acts[-2])  # eager library work on the default stream between replays
+        torch.cuda.synchronize()

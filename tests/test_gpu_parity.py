@@ -115,6 +115,39 @@ def test_matmul_family(mkn, dt):
     check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), dt, "dB", k=m)
 
 
+# m, k or n = 1: the 2-D forms of the reference's mat-vec, vec-mat and dot products
+MM_EDGE = [(1, 5, 7), (6, 1, 9), (4, 8, 1), (1, 1, 1), (1, 64, 1), (300, 1, 2), (1, 300, 130), (130, 300, 1)]
+
+
+@pytest.mark.parametrize("mkn", MM_EDGE)
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_matmul_family_unit_dims(mkn, dt):
+    m, k, n = mkn
+    g = rng(m * 13 + k * 5 + n)
+    a, at = prep(g.standard_normal((m, k)), dt)
+    b, bt = prep(g.standard_normal((k, n)), dt)
+    gr, grt = prep(g.standard_normal((m, n)), dt)
+    check(ops.gpu_matmul(at, bt, m, k, n), oracle.matmul, (a, b), dt, "matmul", k=k)
+    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), dt, "dA", k=n)
+    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), dt, "dB", k=m)
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+def test_matmul_vector_known_answers(dt):
+    """lib.rs:4559-4605 as 2-D products: (3,2)@(2,1) = [-1,-1,-1]; (1,3)@(3,2) =
+    [4,5]; (1,3)@(3,1) = 8 -- exact in both dtypes (small integers)."""
+    def mm(a, b):
+        a = np.asarray(a, np.float32)
+        b = np.asarray(b, np.float32)
+        m, k = a.shape
+        n = b.shape[1]
+        return host(ops.gpu_matmul(torch.from_numpy(a).to(DEV, DTYPES[dt]), torch.from_numpy(b).to(DEV, DTYPES[dt]),
+                                   m, k, n))
+    assert np.array_equal(mm([[1, 2], [3, 4], [5, 6]], [[1], [-1]]), np.array([[-1], [-1], [-1]], np.float32))
+    assert np.array_equal(mm([[1, 2, 3]], [[1, 0], [0, 1], [1, 1]]), np.array([[4, 5]], np.float32))
+    assert np.array_equal(mm([[1, 2, 3]], [[4], [-1], [2]]), np.array([[8]], np.float32))
+
+
 @pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (1, 7, 5)])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_linear_fwd_bwd(shape, dt):

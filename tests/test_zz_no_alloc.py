@@ -51,6 +51,10 @@ CASES = [
     ("f32", _lib.ALGO_IGEMM, (8, 64, 32, 28, 28, 3, 1, 1), (2, 16, 8, 9, 9, 3, 1, 1)),            # generic split-K
     ("f32", _lib.ALGO_IM2COL, (8, 16, 32, 20, 20, 3, 1, 1), (2, 16, 32, 9, 9, 3, 1, 1)),
     ("bf16", _lib.ALGO_DIRECT, (4, 8, 16, 12, 12, 3, 1, 1), (1, 8, 16, 7, 7, 3, 1, 1)),
+    # at most 4 input channels at a large batch: the input gradient needs no workspace and
+    # the weight gradient only the few-channel kernel's partials (what the sizing must report)
+    ("bf16", _lib.ALGO_IGEMM, (256, 3, 64, 64, 64, 5, 1, 2), (4, 3, 64, 16, 16, 5, 1, 2)),
+    ("f32", _lib.ALGO_IGEMM, (512, 4, 32, 28, 28, 3, 1, 1), (2, 4, 32, 9, 9, 3, 1, 1)),
 ]
 
 

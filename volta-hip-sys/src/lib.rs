@@ -6,10 +6,14 @@
 //! the header.  Device pointers are `*const c_void` / `*mut c_void`, sizes
 //! `i64`, streams `*mut c_void` (a `hipStream_t`; null = default stream), and
 //! every function returns a status (`VH_OK` = 0).  The safe layer Volta calls
-//! from `src/ops/gpu_ops.rs` is [`check`] plus the `gpu_*` bodies shown in
-//! INTEGRATION.md: a non-zero status becomes `None`, keeping the CPU fallback.
+//! from `src/ops/gpu_ops.rs` is the [`gpu_ops`] module: an owned device buffer
+//! and one `gpu_*` function per conv / matmul entry of the reference's
+//! `gpu_ops.rs`, where a non-zero status becomes `None`, keeping the CPU
+//! fallback.
 #![allow(non_camel_case_types)]
 use std::ffi::{c_char, c_int, c_void, CStr};
+
+pub mod gpu_ops;
 
 pub const VH_OK: c_int = 0;
 pub const VH_ERR_NO_DEVICE: c_int = 1;
@@ -47,6 +51,7 @@ extern "C" {
     pub fn vh_download(dst_host: *mut c_void, src_dev: *const c_void, bytes: usize, stream: *mut c_void) -> c_int;
     pub fn vh_stream_sync(stream: *mut c_void) -> c_int;
     pub fn vh_release_cache() -> c_int;
+    pub fn vh_workspace_info(stream: *mut c_void, ptr: *mut *mut c_void, bytes: *mut usize, retired: *mut usize) -> c_int;
     pub fn vh_set_kernel_policy(policy: c_int) -> c_int;
     pub fn vh_matmul(dtype: c_int, a: *const c_void, b: *const c_void, c: *mut c_void, m: i64, k: i64, n: i64, stream: *mut c_void) -> c_int;
     pub fn vh_matmul_backward_a(dtype: c_int, grad: *const c_void, b: *const c_void, grad_a: *mut c_void, m: i64, k: i64, n: i64, stream: *mut c_void) -> c_int;

@@ -57,6 +57,7 @@ SIGNATURES = {
     "vh_download": [_P, _P, _SZ, _P],
     "vh_stream_sync": [_P],
     "vh_release_cache": [],
+    "vh_workspace_info": [_P, _PP, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)],
     "vh_set_kernel_policy": [_INT],
     "vh_matmul": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],
     "vh_matmul_backward_a": [_INT, _P, _P, _P, _I64, _I64, _I64, _P],

@@ -78,17 +78,20 @@ static size_t round_bytes(size_t b) { return (b + 255) & ~size_t(255); }
 
 // ------------------------------------------------------------------ per-stream workspace
 // One grow-only device buffer per HIP stream; stream order makes its reuse by
-// consecutive calls on that stream safe.  A buffer that a later call outgrows
-// is retired, never freed on the spot: a HIP graph captured earlier on the
-// stream still holds its address (and kernels queued on the stream may still
-// use it).  Retired buffers are freed only by vh_release_cache(), which is why
-// a release invalidates every graph captured from library calls.  While the
-// stream is being captured the workspace never grows (that would allocate, and
+// consecutive calls on that stream safe.  A HIP graph captured on the stream
+// records the buffer's address, so its replays use the capture stream's
+// buffer wherever they run.  A buffer that a later call outgrows is therefore
+// freed (after the stream's queued work, which may still use it) only when no
+// call was captured while it was current; a buffer that a capture referenced is
+// retired instead and freed only by vh_release_cache(), which is why a release
+// invalidates every graph captured from library calls.  While the stream is
+// being captured the workspace never grows (that would allocate, and
 // synchronise nothing, in the middle of a capture): the call fails with
 // VH_ERR_CAPTURE and the caller runs it once eagerly before capturing.
 struct Ws {
   void* ptr = nullptr;
   size_t bytes = 0;
+  bool captured = false;  // a call captured into a graph used this buffer
 };
 static std::mutex g_ws_mu;
 static std::unordered_map<hipStream_t, Ws> g_ws;
@@ -118,24 +121,45 @@ static int ws_get(hipStream_t st, size_t bytes, void** out) {
   }
   std::lock_guard<std::mutex> lk(g_ws_mu);
   Ws& w = g_ws[st];
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  VH_HIP_CHECK(hipStreamIsCapturing(st, &cs));
+  const bool capturing = cs != hipStreamCaptureStatusNone;
   const size_t nb = ws_grow_to(w.bytes, bytes);
   if (nb) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    VH_HIP_CHECK(hipStreamIsCapturing(st, &cs));
-    if (cs != hipStreamCaptureStatusNone)
+    if (capturing)
       return set_error(VH_ERR_CAPTURE,
                        "workspace of this stream (%zu bytes) must grow to %zu while the stream is captured: "
                        "run the call once eagerly on the stream before capturing",
                        w.bytes, bytes);
+    if (w.ptr) {
+      void* old = w.ptr;
+      const bool keep = w.captured;
+      w.ptr = nullptr;
+      w.bytes = 0;
+      w.captured = false;
+      if (keep) {
+        g_ws_retired.push_back(old);  // a graph holds its address: freed by vh_release_cache only
+      } else {
+        // only this stream's queued calls can still use it
+        const hipError_t e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+          g_ws_retired.push_back(old);
+          return set_error(VH_ERR_LAUNCH, "hipStreamSynchronize before a workspace grows failed: %s",
+                           hipGetErrorString(e));
+        }
+        VH_HIP_CHECK(hipFree(old));
+      }
+    }
     void* p = nullptr;
     if (hipMalloc(&p, nb) != hipSuccess) {
       (void)hipGetLastError();
       return set_error(VH_ERR_OOM, "workspace allocation of %zu bytes failed", nb);
     }
-    if (w.ptr) g_ws_retired.push_back(w.ptr);  // may still be referenced: freed by vh_release_cache only
     w.ptr = p;
     w.bytes = nb;
+    w.captured = false;
   }
+  if (capturing) w.captured = true;
   *out = w.ptr;
   return VH_OK;
 }
@@ -469,6 +493,11 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   Carve cv;
   size_t o_w = cv.take(wbytes), o_g = cv.take(ws_gemm);
   if (need) {
+    // at most 4 input channels: the one-lane-per-position kernel, no workspace
+    if (g_fast_paths && dgrad_smallc_ok(g)) {
+      *need = 0;
+      return VH_OK;
+    }
     // the larger of this pass's request and the stride-phase path's
     size_t n = cv.off, np = 0;
     if ((d.SH > 1 || d.SW > 1) && g_fast_paths && dgrad_phases(dt, dy, w, nullptr, dx, d, st, mask, &np) == VH_OK)
@@ -513,12 +542,15 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
 static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db, bool* db_done,
                        const ConvDims& d, hipStream_t st, size_t* need = nullptr) {
   if (db_done) *db_done = false;
-  size_t most = 0;  // sizing mode: the largest request of every path that may run
+  size_t most = 0;  // sizing mode: the largest request of the paths that run
   if (dt == VH_BF16 && d.SH == 1 && d.SW == 1 && g_fast_paths) {
     size_t nb = wgrad_rows_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH, (int)d.KW,
                               (int)d.PH, (int)d.PW, db != nullptr);
-    most = std::max(most, nb);
-    if (nb && !need) {
+    if (nb && need) {  // the row kernel runs whenever it plans a workspace
+      *need = nb;
+      return VH_OK;
+    }
+    if (nb) {
       void* ws;
       VH_TRY(ws_get(st, nb, &ws));
       int r = wgrad_rows_bf16(dy, x, dw, db, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.KH,
@@ -531,7 +563,11 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   }
   if (dt == VH_BF16 && is_strided_pointwise(d) && g_fast_paths) {
     size_t nb = pw_conv_bf16_wgrad_ws((int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH);
-    most = std::max(most, nb);
+    if (nb && need && aligned16(x) && aligned16(dy)) {  // the pointwise kernel runs
+      *need = nb;
+      return VH_OK;
+    }
+    most = std::max(most, nb);  // requested, then unsupported for unaligned operands
     if (nb && !need) {
       void* ws;
       VH_TRY(ws_get(st, nb, &ws));
@@ -870,6 +906,15 @@ int vh_release_cache(void) {
   g_ws.clear();
   for (void* p : g_ws_retired) (void)hipFree(p);
   g_ws_retired.clear();
+  return VH_OK;
+}
+
+int vh_workspace_info(void* stream, void** ptr, size_t* bytes, size_t* retired) {
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  auto it = g_ws.find(S(stream));
+  if (ptr) *ptr = it == g_ws.end() ? nullptr : it->second.ptr;
+  if (bytes) *bytes = it == g_ws.end() ? 0 : it->second.bytes;
+  if (retired) *retired = g_ws_retired.size();
   return VH_OK;
 }
 

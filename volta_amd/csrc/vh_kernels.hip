@@ -1129,7 +1129,7 @@ __global__ __launch_bounds__(256) void pixel_shuffle_vec_kernel(const typename E
   // with R instructions of 64 consecutive chunks each, exchanging chunks
   // through LDS (chunk u of the span is chunk u % R of item u / R), instead of
   // R instructions whose lanes are R chunks apart (configs[4], r = 3: 22.1 ->
-  // 18.3 us).  LDS work of one wave only, in program order: no barrier.
+  // 18.3 us).  LDS work of one wave only: a wave barrier after its stores.
   __shared__ u32x4w xs[4][64 * R];
   const int lane = threadIdx.x & 63, wv4 = threadIdx.x >> 6;
   const bool whole = item - lane + 64 <= items;  // wave-uniform
@@ -1143,7 +1143,9 @@ __global__ __launch_bounds__(256) void pixel_shuffle_vec_kernel(const typename E
     if (whole) {
 #pragma unroll
       for (int j = 0; j < R; ++j) xs[wv4][R * lane + j] = *reinterpret_cast<const u32x4w*>(run + j * VE);
-      asm volatile("" ::: "memory");
+      // every lane's LDS stores complete before any lane reads another lane's slot
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int j = 0; j < R; ++j)
         *reinterpret_cast<u32x4w*>(out + span0 + (long)(64 * j + lane) * VE) = xs[wv4][64 * j + lane];
