@@ -99,6 +99,9 @@ def parse():
     ap.add_argument("--one-stream", action="store_true",
                     help="issue the whole step on one stream (default: each layer's weight gradient on a "
                          "second stream next to the input-gradient chain)")
+    ap.add_argument("--profile-step", action="store_true",
+                    help="run only the headline training step, eagerly, --warmup then --steps times (for kernel "
+                         "traces of the two-stream schedule); prints the measured ms per step")
     ap.add_argument("--profile-op", default=None,
                     help="run only these passes (e.g. '3x3 256->256 @14 wgrad', several separated by ';', "
                          "or 'headline' for all twelve) --steps times each, then a 256 MiB device copy, for "
@@ -687,6 +690,10 @@ def main():
 
     if args.profile_op:
         profile_op(torch, vnn, dev, layers, args.profile_op, args.steps)
+        return
+    if args.profile_step:
+        step = make_train_step(torch, layers, None if args.one_stream else torch.cuda.Stream())
+        print("headline step ms:", round(time_eager_fn(torch, step, args.steps, args.warmup), 4), flush=True)
         return
 
     # headline: the training step (forward, then dX and dW in reverse layer

@@ -593,6 +593,13 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   p.args.d = dw;
   p.args.a = Operand{dy, 0, (int)d.O, aligned16(dy)};
   p.args.b = Operand{x, 0, p.args.N, 0};
+  if (db && p.args.N % 64 != 0) {
+    // the bias gradient (row sums of dY) as one more column -- a B row of ones --
+    // where it falls into the padding of the last column tile (no extra tile)
+    p.args.N += 1;
+    p.args.b = Operand{x, 1, p.args.N, 0};
+    p.args.dbias = db;
+  }
   p.wide = 1;
   p.splits = pick_splits(p.args.M, p.args.N, p.args.K, dt, p.wide);
   size_t ws_gemm = igemm_prepare(p);
@@ -602,7 +609,9 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
   }
   void* ws;
   VH_TRY(ws_get(st, ws_gemm, &ws));
-  return run_igemm(p, (float*)ws, st);
+  const int r = run_igemm(p, (float*)ws, st);
+  if (r == VH_OK && p.args.dbias && db_done) *db_done = true;
+  return r;
 }
 
 static int bias_grad_nchw(int dt, const void* dy, void* db, long B, long C, long HW, hipStream_t st,

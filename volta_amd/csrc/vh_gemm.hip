@@ -67,7 +67,7 @@ int launch_tile(IgemmPlan& p, float* ws, hipStream_t st) {
     VH_LAUNCH_CHECK();
     // few splits of a large weight gradient: the coalesced OIHW reduction
     if (OUT == OK_WGRAD_OIHW && a.bias_mode == 0 && a.act == 0 && a.wg_rs <= 64 && p.splits <= 8 &&
-        (long)a.wg_c * a.wg_rs == a.N) {
+        (long)a.wg_c * a.wg_rs + (a.dbias ? 1 : 0) == a.N) {
       splitk_reduce_oihw_kernel<T><<<dim3((unsigned)a.M, (unsigned)((a.wg_c + 63) / 64)), 256,
                                      (size_t)a.wg_rs * 65 * sizeof(float), st>>>(a, ws, p.splits);
     } else {

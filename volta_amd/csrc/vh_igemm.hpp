@@ -74,6 +74,7 @@ struct IgemmArgs {
   FastDiv f_wsub;    // OK_NCHW_SUB: divide by the phase's width
   int act;           // epilogue: 0 none, 1 ReLU, 2 zero where mask <= 0 (mask laid out like d)
   const void* mask;
+  void* dbias;       // OK_WGRAD_OIHW: column wg_c*wg_rs (a B row of ones) is the bias gradient -> dbias[row]
   ConvGeom g;
   int nphase;        // > 1: blockIdx.y selects ph[blockIdx.y] (same M, N, K for every phase)
   PhaseArg ph[4];
@@ -91,14 +92,16 @@ struct Loader {
   // per-unit row state
   int row;
   bool valid;
+  bool ones;       // KD_CONV_WGRAD_X with op.ld == 1: the last row is all ones (bias column)
   int s0, s1, s2;  // kind-specific precomputed quantities
   const S* base;
 
   __device__ __forceinline__ void init(const Operand& op, const ConvGeom& g, int r) {
     row = r;
     valid = r < op.rows;
+    ones = KIND == KD_CONV_WGRAD_X && op.ld == 1 && r == op.rows - 1;
     base = reinterpret_cast<const S*>(op.p);
-    if (!valid) return;
+    if (!valid || ones) return;
     if (KIND == KD_CONV_FWD_X) {
       uint32_t n, pq, p, q;
       g.fPQ.divmod((uint32_t)r, n, pq);
@@ -131,6 +134,11 @@ struct Loader {
 #pragma unroll
     for (int j = 0; j < VEC; ++j) out[j] = S(0);
     if (!valid || k0 >= K) return;
+    if (KIND == KD_CONV_WGRAD_X && ones) {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) out[j] = k0 + j < K ? Elem<T>::from_f32(1.f) : S(0);
+      return;
+    }
     if (KIND == KD_DENSE_K) {
       const S* src = base + (long)row * op.ld + k0;
       if (op.vec_ok && k0 + VEC <= K) {
@@ -335,6 +343,10 @@ __device__ __forceinline__ void store_out(const IgemmArgs& args, int row, int co
   if (OUT == OK_PARTIAL) {
     float* ws = reinterpret_cast<float*>(args.d);
     ws[((long)blockIdx.z * args.M + row) * args.N + col] = v;
+    return;
+  }
+  if (OUT == OK_WGRAD_OIHW && args.dbias && col == args.wg_c * args.wg_rs) {
+    reinterpret_cast<S*>(args.dbias)[row] = Elem<T>::from_f32(v);
     return;
   }
   if (args.bias_mode == 1) v += Elem<T>::to_f32(reinterpret_cast<const S*>(args.bias)[row]);
@@ -572,6 +584,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_oihw_kernel(IgemmArgs args,
   for (int i = threadIdx.x; i < nc * RS; i += 256) {
     const int cl = i / RS, rs = i - cl * RS;
     d[i] = Elem<T>::from_f32(tile[rs * 65 + cl]);
+  }
+  // the bias column (a B row of ones): the same split order
+  if (args.dbias && blockIdx.y == 0 && threadIdx.x == 0) {
+    const float* p = ws + (long)o * args.N + (long)RS * C;
+    float s = 0.f;
+    for (int z = 0; z < splits; ++z) s += p[z * MN];
+    reinterpret_cast<S*>(args.dbias)[o] = Elem<T>::from_f32(s);
   }
 }
 

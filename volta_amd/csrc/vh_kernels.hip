@@ -58,6 +58,74 @@ __global__ __launch_bounds__(256) void direct_fwd_kernel(const typename Elem<T>:
   }
 }
 
+// Direct forward for a few products per output (C*R*S <= 128, R x S of 1x1, 3x3
+// or 5x5: a first layer on 1-4 channels).  Block (image n, OB output channels,
+// chunk of 256 output positions): one position per lane, whose C*R*S input taps are
+// read once and multiplied with the OB channels' weights (staged in LDS as
+// fp32), so x is read once per OB outputs instead of once per output, and the
+// index math is 32-bit.  Every output is summed exactly as direct_fwd_kernel
+// sums it (c -> r -> s, out-of-range taps skipped, separate multiply and add,
+// bias in fp32 before the one rounding, ReLU of the rounded value): the
+// results are bit-identical, i.e. equal to Volta's CPU Direct loop in f32.
+template <typename T, int R, int S, int OB>
+__global__ __launch_bounds__(256) void direct_fwd_small_kernel(const typename Elem<T>::storage* __restrict__ x,
+                                                               const typename Elem<T>::storage* __restrict__ w,
+                                                               const typename Elem<T>::storage* __restrict__ bias,
+                                                               typename Elem<T>::storage* __restrict__ y,
+                                                               ConvGeom g, int act) {
+#pragma clang fp contract(off)
+  constexpr int RS = R * S;
+  __shared__ float wl[OB][128];
+  const int n = blockIdx.x, o0 = blockIdx.y * OB;
+  const int CRS = g.C * RS;
+  for (int i = threadIdx.x; i < OB * CRS; i += 256) {
+    const int o = i / CRS, k = i - o * CRS;
+    wl[o][k] = o0 + o < g.O ? Elem<T>::to_f32(w[(long)(o0 + o) * CRS + k]) : 0.f;
+  }
+  float bv[OB];
+#pragma unroll
+  for (int o = 0; o < OB; ++o) bv[o] = bias && o0 + o < g.O ? Elem<T>::to_f32(bias[o0 + o]) : 0.f;
+  __syncthreads();
+  const int PQ = g.P * g.Q, HW = g.H * g.W;
+  const auto* xn = x + (long)n * g.C * HW;
+  auto* yn = y + ((long)n * g.O + o0) * PQ;
+  for (int pq = blockIdx.z * 256 + threadIdx.x; pq < PQ; pq += gridDim.z * 256) {
+    uint32_t p, q;
+    g.fQ.divmod((uint32_t)pq, p, q);
+    const int h0 = (int)p * g.sh - g.ph, w0 = (int)q * g.sw - g.pw;
+    float sacc[OB];
+#pragma unroll
+    for (int o = 0; o < OB; ++o) sacc[o] = 0.f;
+    for (int c = 0; c < g.C; ++c) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int h = h0 + r;
+        if (h < 0 || h >= g.H) continue;
+#pragma unroll
+        for (int k = 0; k < S; ++k) {
+          const int ww = w0 + k;
+          if (ww < 0 || ww >= g.W) continue;
+          const float xv = Elem<T>::to_f32(xn[c * HW + h * g.W + ww]);
+#pragma unroll
+          for (int o = 0; o < OB; ++o) {
+            const float prod = xv * wl[o][(c * R + r) * S + k];
+            sacc[o] += prod;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < OB; ++o) {
+      if (o0 + o >= g.O) break;
+      float sv = sacc[o];
+      if (bias) sv += bv[o];
+      auto v = Elem<T>::from_f32(sv);
+      if (act == 1 && !(Elem<T>::to_f32(v) > 0.f)) v = Elem<T>::from_f32(0.f);
+      yn[(long)o * PQ + pq] = v;
+    }
+  }
+}
+
 // Input gradient, one input element per lane (conv_backward_input.wgsl:26-89).
 // Terms are visited in the reference's order oc -> oh -> ow (conv.rs:458-505),
 // skipping the output positions whose receptive field misses the element, with
@@ -651,6 +719,101 @@ __global__ __launch_bounds__(256) void direct_wgrad_taps_kernel(const typename E
     if ((threadIdx.x & 63) == 0) bred[threadIdx.x >> 6] = v;
     __syncthreads();
     if (threadIdx.x == 0) bpart[(long)blockIdx.y * g.O + o] = (bred[0] + bred[1]) + (bred[2] + bred[3]);
+  }
+}
+
+// Weight (and bias) gradient of the Direct algorithm for 1x1 and 3x3 windows,
+// OB output channels per block: block (o-group, input channel c, slice of IT*256 output positions) reads
+// each position's OB dY values and its R x S x values once and keeps OB x R*S
+// accumulators (+ OB bias sums in the blocks of c = 0) per lane, i.e. x is read
+// once per OB output channels.  The lanes' sums are combined through LDS in a
+// fixed order (wave, then lane) into one partial per slice: [slice][o][c][r][s]
+// and [slice][o], reduced by direct_wgrad_reduce_kernel.
+template <typename T, int R, int S, int OB, int IT>
+__global__ __launch_bounds__(256) void direct_wgrad_ob_kernel(const typename Elem<T>::storage* __restrict__ dy,
+                                                              const typename Elem<T>::storage* __restrict__ x,
+                                                              float* __restrict__ part, ConvGeom g,
+                                                              float* __restrict__ bpart) {
+  constexpr int RS = R * S, NV = OB * RS + OB;  // accumulators per lane
+  __shared__ float red[4][NV][64];
+  const int o0 = blockIdx.x * OB, c = blockIdx.y, slice = blockIdx.z;
+  const int npos = g.N * g.P * g.Q, HW = g.H * g.W, PQ = g.P * g.Q;
+  float acc[OB][RS], bs[OB];
+#pragma unroll
+  for (int o = 0; o < OB; ++o) {
+    bs[o] = 0.f;
+#pragma unroll
+    for (int t = 0; t < RS; ++t) acc[o][t] = 0.f;
+  }
+  float gv[IT][OB], xv[IT][RS];
+  // every load of the lane's IT positions first (out-of-range ones read a
+  // clamped address and are zeroed), then the products
+#pragma unroll
+  for (int u = 0; u < IT; ++u) {
+    const int i = (slice * IT + u) * 256 + threadIdx.x;
+    const bool ok = i < npos;
+    uint32_t n, pq, p, q;
+    g.fPQ.divmod((uint32_t)(ok ? i : 0), n, pq);
+    g.fQ.divmod(pq, p, q);
+    const long db_ = ((long)n * g.O + o0) * PQ + pq;
+#pragma unroll
+    for (int o = 0; o < OB; ++o) {
+      const bool oo = ok && o0 + o < g.O;
+      const float v = Elem<T>::to_f32(dy[oo ? db_ + (long)o * PQ : 0]);
+      gv[u][o] = oo ? v : 0.f;
+    }
+    const long xb = ((long)n * g.C + c) * HW;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int h = (int)p * g.sh + r - g.ph;
+#pragma unroll
+      for (int k = 0; k < S; ++k) {
+        const int w = (int)q * g.sw + k - g.pw;
+        const bool in = ok && h >= 0 && h < g.H && w >= 0 && w < g.W;
+        const float v = Elem<T>::to_f32(x[in ? xb + h * g.W + w : 0]);
+        xv[u][r * S + k] = in ? v : 0.f;
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < IT; ++u)
+#pragma unroll
+    for (int o = 0; o < OB; ++o) {
+      bs[o] += gv[u][o];
+#pragma unroll
+      for (int t = 0; t < RS; ++t) acc[o][t] += xv[u][t] * gv[u][o];
+    }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 0; o < OB; ++o) {
+#pragma unroll
+    for (int t = 0; t < RS; ++t) red[wave][o * RS + t][lane] = acc[o][t];
+    red[wave][OB * RS + o][lane] = bs[o];
+  }
+  __syncthreads();
+  // each wave's 64 lanes per value (all threads), then the four waves in order
+  __shared__ float red2[4][NV];
+  for (int idx = threadIdx.x; idx < 4 * NV; idx += 256) {
+    const int wv = idx / NV, v = idx - wv * NV;
+    const float4* row = reinterpret_cast<const float4*>(red[wv][v]);
+    float sum = 0.f;
+#pragma unroll
+    for (int l4 = 0; l4 < 16; ++l4) {
+      const float4 f = row[l4];
+      sum += ((f.x + f.y) + (f.z + f.w));
+    }
+    red2[wv][v] = sum;
+  }
+  __syncthreads();
+  for (int v = threadIdx.x; v < NV; v += 256) {
+    const float sum = ((red2[0][v] + red2[1][v]) + red2[2][v]) + red2[3][v];
+    if (v < OB * RS) {
+      const int o = v / RS, t = v - o * RS;
+      if (o0 + o < g.O) part[(long)slice * g.O * g.C * RS + ((long)(o0 + o) * g.C + c) * RS + t] = sum;
+    } else if (bpart && c == 0) {
+      const int o = v - OB * RS;
+      if (o0 + o < g.O) bpart[(long)slice * g.O + o0 + o] = sum;
+    }
   }
 }
 
@@ -1337,6 +1500,20 @@ int run_direct_fwd(const void* x, const void* w, const void* bias, void* y, cons
                    int act) {
   long total = (long)g.N * g.O * g.P * g.Q;
   using S = typename Elem<T>::storage;
+  // few products per output: the block-per-(image, 8 channels) kernel (same sums, same bits)
+  const bool rs_ok = g.R == g.S && (g.R == 1 || g.R == 3 || g.R == 5);
+  if (rs_ok && (long)g.C * g.R * g.S <= 128 && g.N <= 65535 && (long)g.P * g.Q < (1L << 31) &&
+      (long)g.C * g.H * g.W < (1L << 31)) {
+    dim3 grid((unsigned)g.N, (unsigned)((g.O + 7) / 8), (unsigned)std::min<long>(((long)g.P * g.Q + 255) / 256, 64));
+    if (g.R == 3)
+      direct_fwd_small_kernel<T, 3, 3, 8><<<grid, 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, act);
+    else if (g.R == 5)
+      direct_fwd_small_kernel<T, 5, 5, 8><<<grid, 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, act);
+    else
+      direct_fwd_small_kernel<T, 1, 1, 8><<<grid, 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, act);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   direct_fwd_kernel<T><<<grid_for(total), 256, 0, st>>>((const S*)x, (const S*)w, (const S*)bias, (S*)y, g, total,
                                                         act);
   VH_LAUNCH_CHECK();
@@ -1554,10 +1731,22 @@ int run_channel_bias_add(void* y, const void* bias, long N, int C, long HW, hipS
   return VH_OK;
 }
 
+// direct_wgrad_ob_kernel: positions per lane and slices
+constexpr int kWgradObIt = 4;
+static bool direct_wgrad_ob_ok(const ConvGeom& g) {
+  return direct_wgrad_taps_ok(g) && g.R <= 3 && g.O >= 8 && g.C <= 65535 &&
+         ((long)g.N * g.P * g.Q + 256 * kWgradObIt - 1) / (256 * kWgradObIt) <= 65535;
+}
+
 template <typename T>
 size_t direct_wgrad_ws(const ConvGeom& g, int* slices, int* slice_len) {
   long npos = (long)g.N * g.P * g.Q;
   long nw = (long)g.O * g.C * g.R * g.S;
+  if (direct_wgrad_ob_ok(g)) {
+    *slice_len = 256 * kWgradObIt;
+    *slices = (int)((npos + *slice_len - 1) / *slice_len);
+    return (size_t)(*slices) * (nw + g.O) * sizeof(float);
+  }
   if (direct_wgrad_taps_ok(g)) {
     const int sl = direct_wgrad_taps_slices(g);
     *slice_len = (int)((npos + sl - 1) / sl);
@@ -1578,6 +1767,20 @@ int run_direct_wgrad(const void* dy, const void* x, void* dw, const ConvGeom& g,
   using S = typename Elem<T>::storage;
   long nw = (long)g.O * g.C * g.R * g.S;
   if (db_done) *db_done = false;
+  if (direct_wgrad_ob_ok(g)) {
+    if (db_done) *db_done = db != nullptr;
+    float* bp = db ? ws + (long)slices * nw : nullptr;
+    dim3 grid((unsigned)((g.O + 7) / 8), (unsigned)g.C, (unsigned)slices);
+    if (g.R == 3)
+      direct_wgrad_ob_kernel<T, 3, 3, 8, kWgradObIt><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, bp);
+    else
+      direct_wgrad_ob_kernel<T, 1, 1, 8, kWgradObIt><<<grid, 256, 0, st>>>((const S*)dy, (const S*)x, ws, g, bp);
+    VH_LAUNCH_CHECK();
+    const int nbw = reduce_splits_grid(nw), nbb = db ? reduce_splits_grid(g.O) : 0;
+    direct_wgrad_reduce_kernel<T><<<nbw + nbb, 256, 0, st>>>(ws, slices, nw, g.O, (S*)dw, (S*)db, nbw);
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   if (direct_wgrad_taps_ok(g)) {
     if (db_done) *db_done = db != nullptr;
     // the bias partials ride along (dB of the same pass, one reduction launch)
