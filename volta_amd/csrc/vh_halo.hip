@@ -72,10 +72,12 @@ struct HaloArgs {
   FastDiv fStrips;              // nstrips
 };
 
-template <int R, int S, int WM, int XI>
+// FMT: 32-row fragments per wave along the output channels (2: 64 o per wave;
+// 1: 32, the tile for layers with at most 32 output channels)
+template <int R, int S, int WM, int XI, int FMT = 2>
 struct HaloCfg {
   static constexpr int RS = R * S;
-  static constexpr int FM = 2, FN = 2;            // 32x32 tiles per wave
+  static constexpr int FM = FMT, FN = 2;          // 32x32 tiles per wave
   static constexpr int WN = 4 / WM;               // waves along positions
   static constexpr int BM = WM * FM * 32;
   static constexpr int BN = WN * FN * 32;
@@ -136,11 +138,13 @@ constexpr int kFusedStageUnits = 2432;
 // EPI selects the epilogue at compile time (0 per-element stores, 1 vector
 // stores through LDS, 2 lane pairs), so each instance carries the registers of
 // one epilogue only.
-template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false, bool PC = false, int EPI = 0>
+template <int R, int S, int WM, int XI, int WPE, bool FUSED = false, bool WD = false, bool PC = false, int EPI = 0,
+          int FMT = 2>
 __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(WPE, WPE))) void conv_halo_bf16_kernel(HaloArgs a) {
-  using Cfg = HaloCfg<R, S, WM, XI>;
+  using Cfg = HaloCfg<R, S, WM, XI, FMT>;
   static_assert(!PC || FUSED, "producer / consumer split: fused form only");
-  static_assert(!WD || (R == 3 && S == 3 && WM == 1), "direct weight staging: 3x3, 64-channel tiles");
+  static_assert(!WD || (R == 3 && S == 3 && WM == 1 && FMT == 2), "direct weight staging: 3x3, 64-channel tiles");
+  static_assert(FMT == 2 || (!FUSED && WM == 1), "32-row tiles: one wave row, not the fused form");
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int SU = FUSED ? kFusedStageUnits : 1;
   __shared__ __attribute__((aligned(16))) u32x4 lds0[SU];
@@ -683,7 +687,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
     return;
   }
   if constexpr (EPI == 1) {
-    // Vector epilogue.  Each wave writes its 64 o x 64 position tile, bias added
+    // Vector epilogue.  Each wave writes its FM*32 o x 64 position tile, bias added
     // and rounded once to bf16 (ReLU applied in fp32 first), into its own LDS
     // region [o][position] (pitch 72 elements: the two half-waves, 4 rows
     // apart, fall on disjoint banks), then stores runs of 8 consecutive
@@ -716,11 +720,12 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
     uint32_t n_e, pq_e;
     a.fPQ.divmod((uint32_t)min(m, a.M - 1), n_e, pq_e);
     const long ybase = (long)n_e * a.O * PQ + pq_e;
-    uint4 ev[8];
+    uint4 ev[FM * 4];
 #pragma unroll
-    for (int it = 0; it < 8; ++it) ev[it] = *reinterpret_cast<const uint4*>(eb + (it * 8 + (lane >> 3)) * EP + k8 * 8);
+    for (int it = 0; it < FM * 4; ++it)
+      ev[it] = *reinterpret_cast<const uint4*>(eb + (it * 8 + (lane >> 3)) * EP + k8 * 8);
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
+    for (int it = 0; it < FM * 4; ++it) {
       const int row = it * 8 + (lane >> 3);
       const int o = o0 + wm + row;
       if (o < a.O && m < a.M) {
@@ -813,12 +818,13 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
 // ---------------------------------------------------------------- host side
 namespace {
 
-template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false, bool PC = false>
+template <int R, int S, int WM, int XI, int WPE = 2, bool FUSED = false, bool WD = false, bool PC = false,
+          int FMT = 2>
 int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
-  using Cfg = HaloCfg<R, S, WM, XI>;
-  auto k0 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 0>;
-  auto k1 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 1>;
-  auto k2 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 2>;
+  using Cfg = HaloCfg<R, S, WM, XI, FMT>;
+  auto k0 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 0, FMT>;
+  auto k1 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 1, FMT>;
+  auto k2 = conv_halo_bf16_kernel<R, S, WM, XI, WPE, FUSED, WD, PC, 2, FMT>;
   // the fused form's stages are static (2 x 38.9 KB): no dynamic LDS
   if (!FUSED) {
     VH_LDS_LIMIT_ONCE(k0);
@@ -837,18 +843,21 @@ int launch_halo(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
 // x load items per thread: an even count, half of them per half-plane
 int halo_xi(const HaloArgs& a) { return 2 * ((a.rows_max * a.npairs + 255) / 256); }
 
-template <int R, int S, int WM>
+template <int R, int S, int WM, int FMT = 2>
 int pick_xi(const HaloArgs& a, size_t lds_bytes, hipStream_t st) {
   const int xi = halo_xi(a);
-  if (xi <= 2) return launch_halo<R, S, WM, 2>(a, lds_bytes, st);
-  if (xi <= 4) return launch_halo<R, S, WM, 4>(a, lds_bytes, st);
-  if (xi <= 6) return launch_halo<R, S, WM, 6>(a, lds_bytes, st);
-  return launch_halo<R, S, WM, 8>(a, lds_bytes, st);
+  if (xi <= 2) return launch_halo<R, S, WM, 2, 2, false, false, false, FMT>(a, lds_bytes, st);
+  if (xi <= 4) return launch_halo<R, S, WM, 4, 2, false, false, false, FMT>(a, lds_bytes, st);
+  if (xi <= 6) return launch_halo<R, S, WM, 6, 2, false, false, false, FMT>(a, lds_bytes, st);
+  return launch_halo<R, S, WM, 8, 2, false, false, false, FMT>(a, lds_bytes, st);
 }
 
 // three blocks per CU: the 3x3 load widths that fit 168 VGPRs without spills
-int pick_xi_wpe3(const HaloArgs& a, int WM, size_t lds_bytes, hipStream_t st) {
+int pick_xi_wpe3(const HaloArgs& a, int WM, int FM, size_t lds_bytes, hipStream_t st) {
   const int xi = halo_xi(a);
+  if (FM == 1)
+    return xi <= 2 ? launch_halo<3, 3, 1, 2, 3, false, false, false, 1>(a, lds_bytes, st)
+                   : launch_halo<3, 3, 1, 4, 3, false, false, false, 1>(a, lds_bytes, st);
   if (WM == 2) return launch_halo<3, 3, 2, 2, 3>(a, lds_bytes, st);
   return xi <= 2 ? launch_halo<3, 3, 1, 2, 3>(a, lds_bytes, st) : launch_halo<3, 3, 1, 4, 3>(a, lds_bytes, st);
 }
@@ -940,8 +949,11 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     size_t lds;
     long cols;  // virtual columns per row: nstrips * TW
   };
+  // 3x3 layers with at most 32 output channels take 32-row tiles (one wave row
+  // of 32 x 64 wave tiles): a 64-row tile would leave half its MFMA work empty
+  const int fm = R == 3 && S == 3 && O <= 32 ? 1 : 2;
   auto eval = [&](int TW, int WM, Cand& c) {
-    const int BN = (4 / WM) * 64, BM = WM * 64;
+    const int BN = (4 / WM) * 64, BM = WM * fm * 32;
     const int nstrips = (Q + TW - 1) / TW;
     const long Mv = (long)N * nstrips * P * TW;
     if (Mv >= (1L << 31)) return false;
@@ -983,7 +995,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // larger stage keeps every decision the base pitch led to (blocks per CU,
   // fused form's static stage size).
   {
-    const int WMb = best.WM, BMb = WMb * 64;
+    const int WMb = best.WM, BMb = WMb * fm * 32;
     auto units = [&](int wp) { return BMb * (2 * R * S + 1) + 2 * best.rows_max * wp + 2; };
     const bool two = best.lds <= 80 * 1024;
     const bool fused_base = units(best.Wp) <= kFusedStageUnits;
@@ -1023,8 +1035,9 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   a.pair_epi = (!a.vec_epi && Q % 2 == 0 && a.TW % 2 == 0 && ((uintptr_t)y & 3) == 0 &&
                 (act != 2 || ((uintptr_t)mask & 3) == 0))
                    ? 1 : 0;
-  const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + WM * 64 - 1) / (WM * 64));
-  const int stage_units = WM * 64 * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
+  const int BMt = WM * fm * 32;
+  const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + BMt - 1) / BMt);
+  const int stage_units = BMt * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
   const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= VH_HALO_WPE3_MIN_TILES && halo_xi(a) <= (WM == 1 ? 4 : 2);
@@ -1034,7 +1047,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // Fused form (two register sets, whole channel groups, stages and the
   // vector epilogue within the static stage size): 3x3, 64 x 256 tiles with
   // at most 4 x items per thread.
-  const bool fused = !wpe3 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
+  const bool fused = !wpe3 && fm == 2 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
                      stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16);
   // The fused forward reads W [O][C][3][3] directly (no relayout launch).  Each
   // block then repacks its weights itself: free in the fused form (128@28 and
@@ -1048,7 +1061,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   } else {
     VH_TRY_HALO(run_relayout_grouped(w, ws, O, C, R * S, w_mode, st));
   }
-  if (wpe3) return pick_xi_wpe3(a, WM, lds, st);
+  if (wpe3) return pick_xi_wpe3(a, WM, fm, lds, st);
   if (fused) {
     if (wd)
       return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, VH_HALO_FUSED_WPE, true, true, VH_HALO_PC>(a, lds, st)
@@ -1056,6 +1069,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     return halo_xi(a) <= 2 ? launch_halo<3, 3, 1, 2, VH_HALO_FUSED_WPE, true, false, VH_HALO_PC>(a, lds, st)
                            : launch_halo<3, 3, 1, 4, VH_HALO_FUSED_WPE, true, false, VH_HALO_PC>(a, lds, st);
   }
+  if (fm == 1) return pick_xi<3, 3, 1, 1>(a, lds, st);
 #define VH_HALO(RR, SS)                                           \
   if (R == RR && S == SS) {                                       \
     return WM == 2 ? pick_xi<RR, SS, 2>(a, lds, st) : pick_xi<RR, SS, 1>(a, lds, st); \
