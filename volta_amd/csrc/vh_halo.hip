@@ -907,13 +907,15 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   if (C < 1 || (W % 2) != 0 || ph > R - 1 || pw > S - 1) return VH_ERR_UNSUPPORTED;
   const int nk = (C + 15) / 16;  // channel groups; the grouped weights are padded with zeros to whole groups
   if (!((R == 3 && S == 3) || (R == 5 && S == 5) || (R == 1 && S == 1))) return VH_ERR_UNSUPPORTED;
-  // 3x3 with at most 64 input and output channels: the resident-weight kernel
-  // (vh_wres.hip) for the masked input gradient (act 2), where it measured
-  // faster; VOLTA_HIP_WRES=1 sends every shape in its envelope there, 0 none.
+  // 3x3 with at most 64 input and 33-64 output channels: the resident-weight
+  // kernel (vh_wres.hip) for the masked input gradient (act 2), where it
+  // measured faster; VOLTA_HIP_WRES=1 sends every shape in its envelope there, 0 none.
   if (R == 3 && S == 3 && C <= 64 && O <= 64) {
     const char* e = getenv("VOLTA_HIP_WRES");
     const int mode = e && *e ? (*e == '0' ? 0 : 1) : -1;
-    if (mode == 1 || (mode == -1 && act == 2)) {
+    // (at most 32 output channels: the 32-row halo tiles measured faster, 68.2 -> 49.6 us for
+    // configs[4]'s 32 -> 27 input gradient)
+    if (mode == 1 || (mode == -1 && act == 2 && O > 32)) {
       const int r = wres_conv_bf16(x, w, w_mode, ws, bias, y, N, C, H, W, O, ph, pw, st, act, mask);
       if (r != VH_ERR_UNSUPPORTED) return r;
     }
