@@ -735,7 +735,10 @@ __global__ __launch_bounds__(256) void direct_wgrad_ob_kernel(const typename Ele
                                                               float* __restrict__ part, ConvGeom g,
                                                               float* __restrict__ bpart) {
   constexpr int RS = R * S, NV = OB * RS + OB;  // accumulators per lane
-  __shared__ float red[4][NV][64];
+  // rows of 64 lanes at a pitch of 68 floats: the 16-byte row reads of
+  // neighbouring threads start on different banks
+  constexpr int RP = 68;
+  __shared__ float red[4][NV][RP];
   const int o0 = blockIdx.x * OB, c = blockIdx.y, slice = blockIdx.z;
   const int npos = g.N * g.P * g.Q, HW = g.H * g.W, PQ = g.P * g.Q;
   float acc[OB][RS], bs[OB];
