@@ -238,8 +238,8 @@ def profile_op(torch, vnn, dev, layers, names, reps):
         elif ":" in name:
             cfg, pname = name.split(":", 1)
             works = works or build_workloads(torch, vnn, dev, layers)
-            w = next(w for w in works if w.name.startswith(cfg) and pname in w.passes)
-            todo.append((name, w.passes[pname][0]))
+            w = next(w for w in works if w.name.startswith(cfg) and (pname in w.passes or pname in w.combined))
+            todo.append((name, {**w.passes, **w.combined}[pname][0]))
         else:
             layer, op = name.rsplit(" ", 1)
             L = next(L for L in layers if L["name"] == layer)
@@ -283,10 +283,13 @@ def roofline_of(flops, byts, ms, dt):
 class Workload:
     """One BASELINE config at its full size: `step` (one fwd+bwd step), the
     passes it is made of (name -> (fn, flops, bytes)), its dtype and the CPU
-    baseline function (seconds per step of Volta's CPU path, extrapolated)."""
+    baseline function (seconds per step of Volta's CPU path, extrapolated).
+    `combined`: calls that run several of the passes at once (same form),
+    timed and listed but not counted in the step's FLOPs or pass sum."""
 
-    def __init__(self, name, dt, step, passes, cpu, note=""):
+    def __init__(self, name, dt, step, passes, cpu, note="", combined=None):
         self.name, self.dt, self.step, self.passes, self.cpu, self.note = name, dt, step, passes, cpu, note
+        self.combined = combined or {}
 
 
 def chain_passes(chain, es):
@@ -336,11 +339,15 @@ def build_workloads(torch, vnn, dev, c3_layers):
             "dW (+db)": (lambda lin=lin, x=x, dy=dy, o=outs: lin.backward(dy, x, input_grad=False,
                                                                          outs=(None, o[1], o[2])), fl, by),
         }
+        # the step's backward: one call (bf16: dX and dW in one launch)
+        combined = {"dX + dW (+db)": (lambda lin=lin, x=x, dy=dy, o=outs: lin.backward(dy, x, outs=o), 2 * fl,
+                                      es * (4096 * 4096 + 2 * 4096 * 1024 + 2 * 1024 * 4096))}
 
         def step(lin=lin, x=x, y=y, dy=dy, o=outs):
             lin.forward(x, out=y)
             lin.backward(dy, x, outs=o)
-        wl.append(Workload(f"configs[1] Linear 4096x1024->4096 fwd+bwd {dt}", dt, step, passes, cpu_config1_linear))
+        wl.append(Workload(f"configs[1] Linear 4096x1024->4096 fwd+bwd {dt}", dt, step, passes, cpu_config1_linear,
+                           combined=combined))
     import volta_amd
     lib = volta_amd.lib()
     n = 8192
@@ -423,6 +430,11 @@ def measure_workload(torch, w, steps, warmup, step_ms=None, pass_ms=None):
         ms = pass_ms[name] if pass_ms and name in pass_ms else time_op_graph(torch, fn, reps=10, replays=3)
         passes[name] = dict(ms=round(ms, 4), tflops=round(fl / (ms * 1e-3) / 1e12, 2) if fl else 0.0,
                             gbs=round(by / (ms * 1e-3) / 1e9, 1))
+    combined = {}
+    for name, (fn, fl, by) in w.combined.items():
+        ms = time_op_graph(torch, fn, reps=10, replays=3)
+        combined[name] = dict(ms=round(ms, 4), tflops=round(fl / (ms * 1e-3) / 1e12, 2),
+                              gbs=round(by / (ms * 1e-3) / 1e9, 1))
     fl = sum(f for _, f, _ in w.passes.values() if f > 1e6)  # conv / GEMM FLOPs (not the loss adds)
     dom = max(w.passes, key=lambda n: passes[n]["ms"])
     _, dfl, dby = w.passes[dom]
@@ -434,7 +446,8 @@ def measure_workload(torch, w, steps, warmup, step_ms=None, pass_ms=None):
     return dict(dtype=w.dt, ms_per_step=round(step_ms, 4), **times, gflop_per_step=round(fl / 1e9, 3),
                 tflops=round(tf, 2),
                 pct_peak=round(100 * tf / PEAK_TFLOPS[w.dt], 2), roofline=roof,
-                sum_of_passes_ms=round(sum(p["ms"] for p in passes.values()), 4), passes=passes)
+                sum_of_passes_ms=round(sum(p["ms"] for p in passes.values()), 4), passes=passes,
+                **(dict(combined_calls=combined) if combined else {}))
 
 
 C4_BATCH = 128

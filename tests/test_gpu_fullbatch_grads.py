@@ -6,6 +6,11 @@ are zero there.  Here every image contributes: dY is dense ~N(0,1) over the
 whole batch and dW / db are compared with the oracle's sum over all images
 (evaluated over image chunks in a thread pool, `tests/oracle_pool.py`).
 
+configs[1]'s Linear layer (4096 rows, and a ragged 4104 x 1032 -> 4104) is
+checked the same way, and its combined backward (in bf16 one launch for dX and
+dW, with db as column sums inside the dW tiles) against the separate dX-only
+and dW-only calls: dX and dW bit for bit, db against the oracle.
+
 configs[2] is also run exactly as bench.py calls it: Conv2d without a bias,
 so the forward gets a NULL bias and the weight gradient a NULL db (a separate
 runtime path and workspace size in the weight-gradient kernel), next to the
@@ -153,3 +158,37 @@ def test_config1_dense_wgrad(C, O):
     assert_parity(host(dw), ref, sc, "f32", "dw over the whole batch")
     ref, sc = oracle_bgrad(dy)
     assert_parity(host(db), ref, sc, "f32", "db over the whole batch")
+
+
+# ------------------------------------------------------------------ configs[1] Linear, 4096 rows
+@pytest.mark.parametrize("dt,shape", [("f32", (4096, 1024, 4096)), ("bf16", (4096, 1024, 4096)),
+                                      ("bf16", (4104, 1032, 4104))], ids=["f32", "bf16", "bf16-ragged"])
+def test_config2_linear_dense_grads(dt, shape):
+    M, IN, OUT = shape
+    print(f"configs[1] Linear {dt} {shape}: dense dY over {M} rows", flush=True)
+    g = np.random.default_rng(5000)
+    x, xt = prep(g.standard_normal((M, IN)), dt)
+    bound = np.sqrt(6.0 / (IN + OUT))
+    w, wt = prep(g.uniform(-bound, bound, (IN, OUT)), dt)
+    dy, dyt = prep(g.standard_normal((M, OUT)), dt)
+    lin = vnn.Linear(IN, OUT, device=DEV, dtype=DT[dt])
+    lin.weight = wt
+    dxt, dwt, dbt = lin.backward(dyt, xt)
+    dx, dw, db = host(dxt), host(dwt), host(dbt)
+    both = lambda r: np.concatenate([r[1].ravel(), r[2]])  # dW and db of one chunk
+    ref, sc = batch_sum(oracle.linear_backward, (dy, x), (w,), pick=both)
+    n = IN * OUT
+    assert_parity(dw, ref[:n].reshape(IN, OUT), sc[:n].reshape(IN, OUT), dt, "dw over all rows", k=M)
+    ref_db, sc_db = ref[n:], sc[n:]
+    assert_parity(db, ref_db, sc_db, dt, "db over all rows", k=M)
+    rows = [0, 1, M // 2, M - 1]
+    ref = oracle.linear_backward(dy[rows], x[rows], w)[0]
+    sc = oracle.linear_backward(np.abs(dy[rows]), np.abs(x[rows]), np.abs(w))[0]
+    assert_parity(dx[rows], ref, sc, dt, "dx rows", k=OUT)
+    # the combined call equals the separate ones (dX, dW: the same MFMA order
+    # per element whatever the tiling); the dW-only call's db is its own sum
+    dx1 = host(lin.backward(dyt, xt, input_grad=True, weight_grad=False)[0])
+    _, dw2, db2 = lin.backward(dyt, xt, input_grad=False, weight_grad=True)
+    assert np.array_equal(dx, dx1), "dX of the combined backward differs from the dX-only call"
+    assert np.array_equal(dw, host(dw2)), "dW of the combined backward differs from the dW-only call"
+    assert_parity(host(db2), ref_db, sc_db, dt, "db of the dW-only call", k=M)

@@ -148,7 +148,7 @@ def test_matmul_vector_known_answers(dt):
     assert np.array_equal(mm([[1, 2, 3]], [[4], [-1], [2]]), np.array([[8]], np.float32))
 
 
-@pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (1, 7, 5)])
+@pytest.mark.parametrize("shape", [(9, 6, 4), (64, 100, 48), (256, 1024, 512), (200, 136, 264), (1, 7, 5)])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 def test_linear_fwd_bwd(shape, dt):
     m, i, o = shape

@@ -772,12 +772,25 @@ static int direct_wgrad(int dt, const void* dy, const void* x, void* dw, const C
 // (KD_DENSE_MN: stored [K][rows], read by transposing LDS reads).  Returns
 // VH_ERR_UNSUPPORTED when the shapes or alignments do not fit.
 static int dense_bf16(int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc, long M,
-                      long N, long K, const void* bias, hipStream_t st) {
+                      long N, long K, const void* bias, hipStream_t st, void* colsum = nullptr) {
   const bool at = ak == KD_DENSE_MN, bt = bk == KD_DENSE_MN;
   if (!dense_bf16_ok(M, N, K, at, lda, bt, ldb, ldc, a, b, c)) return VH_ERR_UNSUPPORTED;
   // a grid of few tiles over a long K: the split-K implicit GEMM fills the chip instead
   if (((M + 127) / 128) * ((N + 127) / 128) < 64 && K > 2048) return VH_ERR_UNSUPPORTED;
-  return dense_bf16_gemm(a, lda, at, b, ldb, bt, c, ldc, (int)M, (int)N, (int)K, bias, st);
+  return dense_bf16_gemm(a, lda, at, b, ldb, bt, c, ldc, (int)M, (int)N, (int)K, bias, st, colsum);
+}
+
+// Linear's dX and dW (K-major x K-major, MN-major x MN-major) as one launch of
+// the dense kernel when both take its 128 x 128 tiles: each grid alone would
+// hold one block per CU.  VH_ERR_UNSUPPORTED: run them separately.
+static int dense_bf16_pair(const DenseProblem& p0, const DenseProblem& p1, hipStream_t st) {
+  for (const DenseProblem* p : {&p0, &p1}) {
+    if (std::max({(long)p->M * p->K, (long)p->K * p->N, (long)p->M * p->N}) > kMaxElems) return VH_ERR_UNSUPPORTED;
+    if (!dense_bf16_ok(p->M, p->N, p->K, p->at, p->lda, p->bt, p->ldb, p->ldc, p->a, p->b, p->c))
+      return VH_ERR_UNSUPPORTED;
+    if (((p->M + 127L) / 128) * ((p->N + 127L) / 128) < 64 && p->K > 2048) return VH_ERR_UNSUPPORTED;
+  }
+  return dense_bf16_gemm_pair(p0, p1, st);
 }
 
 static int dense_f32(int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc, long M,
@@ -1445,9 +1458,27 @@ int vh_linear_backward(int dtype, const void* out_grad, const void* x, const voi
   if (m < 0 || in_features < 0 || out_features < 0) return set_error(VH_ERR_BAD_SHAPE, "negative dimension");
   if (!out_grad || (grad_x && !weight) || (grad_weight && !x)) return set_error(VH_ERR_BAD_ARG, "null pointer");
   hipStream_t st = S(stream);
+  if (dtype == VH_BF16 && g_fast_paths && grad_x && grad_weight && m * in_features * out_features &&
+      std::max({m, in_features, out_features}) < (1L << 31)) {
+    // db as the column sums of dY inside the dW tiles
+    const DenseProblem dx{out_grad, (int)out_features, false, weight, (int)out_features, false,
+                          grad_x, (int)in_features, (int)m, (int)in_features, (int)out_features, nullptr};
+    const DenseProblem dw{x, (int)in_features, true, out_grad, (int)out_features, true,
+                          grad_weight, (int)out_features, (int)in_features, (int)out_features, (int)m, grad_bias};
+    const int r = dense_bf16_pair(dx, dw, st);
+    if (r != VH_OK && r != VH_ERR_UNSUPPORTED) return r;
+    if (r == VH_OK) grad_x = grad_weight = grad_bias = nullptr;  // all done
+  }
   if (grad_x && m * in_features)
     VH_TRY(gemm(dtype, KD_DENSE_K, KD_DENSE_K, out_grad, (int)out_features, weight, (int)out_features, grad_x,
                 (int)in_features, m, in_features, out_features, nullptr, 0, st));
+  if (grad_weight && grad_bias && dtype == VH_BF16 && g_fast_paths && m * in_features * out_features &&
+      std::max({m * in_features, m * out_features, in_features * out_features}) <= kMaxElems) {
+    const int r = dense_bf16(KD_DENSE_MN, KD_DENSE_MN, x, (int)in_features, out_grad, (int)out_features,
+                             grad_weight, (int)out_features, in_features, out_features, m, nullptr, st, grad_bias);
+    if (r != VH_OK && r != VH_ERR_UNSUPPORTED) return r;
+    if (r == VH_OK) grad_weight = grad_bias = nullptr;  // dW and db done
+  }
   if (grad_weight && in_features * out_features)
     VH_TRY(gemm(dtype, KD_DENSE_MN, KD_DENSE_MN, x, (int)in_features, out_grad, (int)out_features, grad_weight,
                 (int)out_features, in_features, out_features, m, nullptr, 0, st));

@@ -78,12 +78,14 @@ struct FastDiv {
 // to the 8 XCDs (each with its own L2) round robin by block id.  Logical
 // block L = xcd * (nb / 8) + slot puts consecutive logical blocks -- which
 // the callers arrange to share input data -- on the same XCD.  Identity when
-// nb is not a multiple of 8.
-__device__ __forceinline__ int xcd_block(int nb) {
-  const int h = blockIdx.x;
+// nb is not a multiple of 8.  xcd_map applies the same order to block h of a
+// group of nb blocks inside a larger grid (the group starting at a multiple of
+// 8, so that h & 7 is still the XCD).
+__device__ __forceinline__ int xcd_map(int h, int nb) {
   if (nb & 7) return h;
   return (h & 7) * (nb >> 3) + (h >> 3);
 }
+__device__ __forceinline__ int xcd_block(int nb) { return xcd_map(blockIdx.x, nb); }
 
 // Deterministic reduction of split-K partial sums part[z][i] (z < splits,
 // i < total) by a 256-thread block: 64 consecutive outputs per pass, wave w

@@ -25,6 +25,7 @@
 namespace vh {
 
 typedef unsigned int u32x4d __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2d __attribute__((ext_vector_type(2)));
 
 namespace {
 
@@ -39,6 +40,8 @@ struct DenseArgs {
   const uint16_t* b;     // [N][ldb] (K-major) or [K][ldb] (MN-major)
   uint16_t* c;           // [M][ldc]
   const uint16_t* bias;  // [N] or nullptr (added to every row)
+  uint16_t* colsum;      // [N] or nullptr: column sums of an MN-major B over K (128 x 128 tiles only)
+  int cs_shift;          // columns per block of the column sums: 4 << cs_shift (set at launch)
   int M, N, K, lda, ldb, ldc;
   int a_bytes, b_bytes, c_bytes;
   int tiles_m, tiles_n;
@@ -57,6 +60,11 @@ struct DenseCfg {
   static constexpr int A_UNITS = AT ? BK * mn_pitch(BM) : BM * PU;
   static constexpr int B_UNITS = BT ? BK * mn_pitch(BN) : BN * PU;
   static constexpr int STAGE = A_UNITS + B_UNITS;  // units per LDS stage
+  // producer / consumer tiles with an MN-major B: room after the two stages
+  // for the producers' column-sum exchange (256 / (BN / 8) k-row groups x at
+  // most BN columns, fp32)
+  static constexpr int CS_BYTES = BT ? 256 / (BN / 8) * BN * 4 : 0;
+  static constexpr size_t lds_bytes(bool pc) { return (size_t)2 * STAGE * 16 + (pc ? CS_BYTES : 0); }
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes) {
@@ -68,9 +76,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, int bytes)
 // other LDS buffer (producers, threads 256-511 serving the load map of threads
 // 0-255).  Neither role holds the other's registers, so two waves run per SIMD
 // and the loads leave the multiplying waves' instruction stream.
-template <int BM, int BN, bool BIAS, bool PC = false, bool AT = false, bool BT = false>
-__global__ __launch_bounds__(PC ? 512 : 256)
-void gemm_bf16_kernel(DenseArgs g) {
+// One block's tile: logical block lb of the grid order below.
+template <int BM, int BN, bool BIAS, bool PC, bool AT, bool BT>
+__device__ __forceinline__ void gemm_bf16_tile(const DenseArgs& g, const int lb) {
   using Cfg = DenseCfg<BM, BN, AT, BT>;
   constexpr int FM = Cfg::FM, FN = Cfg::FN, PU = Cfg::PU, STAGE = Cfg::STAGE;
   constexpr int APU = Cfg::mn_pitch(BM), BPU = Cfg::mn_pitch(BN);  // MN-major LDS pitches (units)
@@ -83,7 +91,6 @@ void gemm_bf16_kernel(DenseArgs g) {
   // blocks (the ones resident on one XCD at a time) walk 8 m-tiles, then the
   // next n-tile, so they share both A and B slices in that XCD's L2 (32 of them
   // cover 8 x 4 tiles instead of 1 x 32)
-  const int lb = xcd_block(g.tiles_m * g.tiles_n);
   const int grp = lb / (kGroupM * g.tiles_n), first_m = grp * kGroupM;
   const int gm = min(g.tiles_m - first_m, kGroupM);
   const int in_grp = lb - grp * kGroupM * g.tiles_n;
@@ -142,6 +149,37 @@ void gemm_bf16_kernel(DenseArgs g) {
       breg[s][it] = __builtin_bit_cast(
           u32x4d, __builtin_amdgcn_raw_buffer_load_b128(br, k0 + b_kr[it] < g.K ? b_off[it] : kOOR, bsk, 0));
   };
+  // Column sums of B over K (a Linear weight gradient's bias gradient, B = dY
+  // stored [K][N]).  The tiling's tiles_m blocks of a column tile each own
+  // 4 << cs_shift of its columns (block of m-tile mt: columns mt * width ..
+  // + width - 1), so every column is summed by exactly one block, over all K.
+  //  * 4-wave blocks: from the staged LDS tile -- a thread adds 4 consecutive
+  //    owned columns of the k rows tid >> cs_shift (+ 256 >> cs_shift ...) of
+  //    each stage, in stage order; the thread sums are added in k-row order.
+  //  * producer / consumer blocks: the producers add the owned B units they
+  //    hold in registers before storing them (a thread's units all cover the
+  //    same 8 columns: unit tid + 256 it has row unit tid % (BN / 8)), stage by
+  //    stage; the 256 / (BN / 8) k-row group sums are added in group order.
+  constexpr bool CS = BT;
+  constexpr int RU = BN / 8;  // row units per k row of the B tile
+  static_assert(256 % RU == 0, "a thread's B units must share their columns");
+  const int cs_w = 4 << g.cs_shift, cs_c0 = (m0 / BM) * cs_w;
+  const bool cs_on = CS && g.colsum != nullptr;  // block-uniform
+  const bool cs_blk = cs_on && cs_c0 < BN;
+  const int cs_g = tid & ((1 << g.cs_shift) - 1), cs_k0 = tid >> g.cs_shift;
+  const int cs_ru = tid % RU;
+  const bool cs_own = cs_blk && cs_ru * 8 >= cs_c0 && cs_ru * 8 < cs_c0 + cs_w;
+  float csum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  auto colsum_stage = [&](int st) {
+    const char* bt = reinterpret_cast<const char*>(lds + st * STAGE + Cfg::A_UNITS);
+    for (int k = cs_k0; k < Cfg::BK; k += 256 >> g.cs_shift) {
+      const u32x2d v = *reinterpret_cast<const u32x2d*>(bt + k * BPU * 16 + (cs_c0 + cs_g * 4) * 2);
+      csum[0] += __builtin_bit_cast(float, v[0] << 16);
+      csum[1] += __builtin_bit_cast(float, v[0] & 0xffff0000u);
+      csum[2] += __builtin_bit_cast(float, v[1] << 16);
+      csum[3] += __builtin_bit_cast(float, v[1] & 0xffff0000u);
+    }
+  };
   auto sstore = [&](auto SET, int st) {
     constexpr int s = decltype(SET)::value;
     u32x4d* base = lds + st * STAGE;
@@ -149,6 +187,18 @@ void gemm_bf16_kernel(DenseArgs g) {
     for (int it = 0; it < Cfg::AIT; ++it) base[a_l[it]] = areg[s][it];
 #pragma unroll
     for (int it = 0; it < Cfg::BIT; ++it) base[b_l[it]] = breg[s][it];
+    if constexpr (CS && PC) {
+      if (cs_own) {
+#pragma unroll
+        for (int it = 0; it < Cfg::BIT; ++it)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const unsigned w = breg[s][it][e];
+            csum[2 * e] += __builtin_bit_cast(float, w << 16);
+            csum[2 * e + 1] += __builtin_bit_cast(float, w & 0xffff0000u);
+          }
+      }
+    }
   };
 
   f32x16 acc[FM][FN];
@@ -195,6 +245,9 @@ void gemm_bf16_kernel(DenseArgs g) {
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
     }
+    if constexpr (CS && !PC) {  // after the stage's MFMAs are issued: the adds overlap their execution
+      if (cs_blk) colsum_stage(st);
+    }
   };
 
   using I0 = std::integral_constant<int, 0>;
@@ -220,6 +273,22 @@ void gemm_bf16_kernel(DenseArgs g) {
         if (kt + 4 < nk) gload(I0{}, (kt + 4) * Cfg::BK);
         __syncthreads();
       }
+      if constexpr (CS) {
+        if (cs_on) {
+          float* red = reinterpret_cast<float*>(lds + 2 * STAGE);  // [256 / RU][cs_w]
+          if (cs_own) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[(tid / RU) * cs_w + cs_ru * 8 - cs_c0 + e] = csum[e];
+          }
+          __syncthreads();  // matched by the consumers after their last stage
+          const int n = n0 + cs_c0 + tid;
+          if (cs_blk && tid < cs_w && n < g.N) {
+            float t = 0.f;
+            for (int j = 0; j < 256 / RU; ++j) t += red[j * cs_w + tid];
+            g.colsum[n] = f32_to_bf16(t);
+          }
+        }
+      }
       return;
     }
     zero_acc();
@@ -227,6 +296,9 @@ void gemm_bf16_kernel(DenseArgs g) {
     for (int kt = 0; kt < nk; ++kt) {
       compute(kt & 1);
       __syncthreads();
+    }
+    if constexpr (CS) {
+      if (cs_on) __syncthreads();  // the producers' column-sum exchange
     }
   } else {
   // invariant at an even stage k: LDS buffer 0 holds stage k, register set 1
@@ -267,6 +339,23 @@ void gemm_bf16_kernel(DenseArgs g) {
   }
   }
 
+  if constexpr (CS && !PC) {
+    if (cs_blk) {  // per owned column: the 256 >> cs_shift k-row sums, added in k-row order
+      static_assert(256 * 4 * 4 <= 2 * STAGE * 16, "column-sum exchange exceeds the LDS stages");
+      __syncthreads();  // every wave is done reading the last stage
+      float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[cs_k0 * cs_w + cs_g * 4 + e] = csum[e];
+      __syncthreads();
+      const int n = n0 + cs_c0 + tid;
+      if (tid < cs_w && n < g.N) {
+        float t = 0.f;
+        for (int j = 0; j < 256 >> g.cs_shift; ++j) t += red[j * cs_w + tid];
+        g.colsum[n] = f32_to_bf16(t);
+      }
+    }
+  }
+
   // epilogue: fp32 (+ bias), one rounding, row-major stores (lanes walk columns)
   const __amdgpu_buffer_rsrc_t cr = rsrc(g.c, g.c_bytes);
 #pragma unroll
@@ -287,17 +376,49 @@ void gemm_bf16_kernel(DenseArgs g) {
   }
 }
 
+template <int BM, int BN, bool BIAS, bool PC = false, bool AT = false, bool BT = false>
+__global__ __launch_bounds__(PC ? 512 : 256)
+void gemm_bf16_kernel(DenseArgs g) {
+  gemm_bf16_tile<BM, BN, BIAS, PC, AT, BT>(g, xcd_block(g.tiles_m * g.tiles_n));
+}
+
+// Two independent products in one launch: blocks 0 .. T0-1 take the first
+// product's tiles, the rest the second's.  Meant for pairs whose grids would
+// each leave half the chip idle (a Linear layer's dX and dW): together they
+// fill it -- 128 x 256 producer / consumer tiles, one block per CU, when the
+// two grids reach a block per CU, else 128 x 128 tiles at two blocks per CU.
+template <int BN, bool PC, bool AT0, bool BT0, bool AT1, bool BT1>
+__global__ __launch_bounds__(PC ? 512 : 256)
+void gemm_bf16_pair_kernel(DenseArgs g0, DenseArgs g1) {
+  const int t0 = g0.tiles_m * g0.tiles_n, h = blockIdx.x;
+  if (h < t0)
+    gemm_bf16_tile<128, BN, false, PC, AT0, BT0>(g0, xcd_map(h, t0));
+  else
+    gemm_bf16_tile<128, BN, false, PC, AT1, BT1>(g1, xcd_map(h - t0, g1.tiles_m * g1.tiles_n));
+}
+
+// Column-sum ownership on BN-column tiles: 2^cs_shift groups of 4 columns per
+// block, the smallest power-of-2 width >= BN / tiles_m (at least 16 columns).
+int colsum_shift(int tiles_m, int BN) {
+  int w = 16;
+  while (w < BN && w * tiles_m < BN) w <<= 1;
+  int sh = 0;
+  while ((4 << sh) < w) ++sh;
+  return sh;
+}
+
 bool fits(long bytes) { return bytes >= 0 && bytes < (1L << 31) - 64; }
 
 template <int BM, int BN, bool BIAS, bool PC, bool AT, bool BT>
 int launch_gemm(const DenseArgs& a0, hipStream_t st) {
   using Cfg = DenseCfg<BM, BN, AT, BT>;
   auto kern = gemm_bf16_kernel<BM, BN, BIAS, PC, AT, BT>;
-  const size_t lds = (size_t)2 * Cfg::STAGE * 16;
+  const size_t lds = Cfg::lds_bytes(PC);
   VH_LDS_LIMIT_ONCE(kern);
   DenseArgs a = a0;
   a.tiles_m = (a.M + BM - 1) / BM;
   a.tiles_n = (a.N + BN - 1) / BN;
+  a.cs_shift = colsum_shift(a.tiles_m, BN);
   kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), PC ? 512 : 256, lds, st>>>(a);
   VH_LAUNCH_CHECK();
   return VH_OK;
@@ -324,9 +445,11 @@ bool dense_bf16_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb,
   return fits((at ? K : M) * lda * 2) && fits((bt ? K : N) * ldb * 2) && fits(M * ldc * 2);
 }
 
-int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
-                    int N, int K, const void* bias, hipStream_t st) {
+namespace {
+DenseArgs dense_args(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
+                     int N, int K, const void* bias, void* colsum) {
   DenseArgs g{};
+  g.colsum = (uint16_t*)colsum;
   g.a = (const uint16_t*)a;
   g.b = (const uint16_t*)b;
   g.c = (uint16_t*)c;
@@ -340,9 +463,49 @@ int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, boo
   g.a_bytes = (int)((long)(at ? K : M) * lda * 2);
   g.b_bytes = (int)((long)(bt ? K : N) * ldb * 2);
   g.c_bytes = (int)((long)M * ldc * 2);
-  const bool big = (long)((M + 127) / 128) * ((N + 255) / 256) >= 256;
+  return g;
+}
+
+// 128 x 256 tiles when they still give at least one block per CU
+bool dense_big(int M, int N) { return (long)((M + 127) / 128) * ((N + 255) / 256) >= 256; }
+}  // namespace
+
+int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
+                    int N, int K, const void* bias, hipStream_t st, void* colsum) {
+  const bool big = dense_big(M, N);
+  if (colsum && (!bt || bias)) return VH_ERR_UNSUPPORTED;
+  const DenseArgs g = dense_args(a, lda, at, b, ldb, bt, c, ldc, M, N, K, bias, colsum);
   if (at) return bt ? launch_layout<true, true>(g, big, st) : launch_layout<true, false>(g, big, st);
   return bt ? launch_layout<false, true>(g, big, st) : launch_layout<false, false>(g, big, st);
+}
+
+namespace {
+template <int BN, bool PC>
+int launch_pair(DenseArgs a0, DenseArgs a1, hipStream_t st) {
+  for (DenseArgs* a : {&a0, &a1}) {
+    a->tiles_m = (a->M + 127) / 128;
+    a->tiles_n = (a->N + BN - 1) / BN;
+    a->cs_shift = colsum_shift(a->tiles_m, BN);
+  }
+  auto kern = gemm_bf16_pair_kernel<BN, PC, false, false, true, true>;
+  const size_t lds = std::max(DenseCfg<128, BN, false, false>::lds_bytes(PC), DenseCfg<128, BN, true, true>::lds_bytes(PC));
+  VH_LDS_LIMIT_ONCE(kern);
+  kern<<<dim3((unsigned)(a0.tiles_m * a0.tiles_n + a1.tiles_m * a1.tiles_n)), PC ? 512 : 256, lds, st>>>(a0, a1);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+}  // namespace
+
+int dense_bf16_gemm_pair(const DenseProblem& p0, const DenseProblem& p1, hipStream_t st) {
+  // the pair form serves a K-major x K-major product next to an MN-major x
+  // MN-major one (Linear's dX and dW)
+  if (p0.at || p0.bt || !p1.at || !p1.bt || p0.colsum) return VH_ERR_UNSUPPORTED;
+  const DenseArgs a0 = dense_args(p0.a, p0.lda, p0.at, p0.b, p0.ldb, p0.bt, p0.c, p0.ldc, p0.M, p0.N, p0.K, nullptr,
+                                  nullptr);
+  const DenseArgs a1 = dense_args(p1.a, p1.lda, p1.at, p1.b, p1.ldb, p1.bt, p1.c, p1.ldc, p1.M, p1.N, p1.K, nullptr,
+                                  p1.colsum);
+  const long t256 = (long)((p0.M + 127) / 128) * ((p0.N + 255) / 256) + (long)((p1.M + 127) / 128) * ((p1.N + 255) / 256);
+  return t256 >= 256 ? launch_pair<256, true>(a0, a1, st) : launch_pair<128, false>(a0, a1, st);
 }
 
 }  // namespace vh

@@ -156,8 +156,27 @@ int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, in
 // [N][ldb] or, with bt, [K][ldb].
 bool dense_bf16_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, long ldc, const void* a,
                    const void* b, const void* c);
+// colsum (bf16 [N], optional): also the column sums of B over K, for an
+// MN-major B on 128 x 128 tiles without bias (VH_ERR_UNSUPPORTED otherwise,
+// before anything is queued).
 int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
-                    int N, int K, const void* bias, hipStream_t st);
+                    int N, int K, const void* bias, hipStream_t st, void* colsum = nullptr);
+// Two bias-free products in one launch (each checked by dense_bf16_ok): a
+// K-major A and B next to an MN-major A and B (with optional column sums of
+// that B), when both run 128 x 128 tiles; VH_ERR_UNSUPPORTED otherwise (the
+// caller then runs them one after the other).
+struct DenseProblem {
+  const void* a;
+  int lda;
+  bool at;
+  const void* b;
+  int ldb;
+  bool bt;
+  void* c;
+  int ldc, M, N, K;
+  void* colsum;
+};
+int dense_bf16_gemm_pair(const DenseProblem& p0, const DenseProblem& p1, hipStream_t st);
 // The same in fp32 (vh_dense_f32.hip): K % 4 == 0, 16-byte aligned A and B.
 bool dense_f32_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, long ldc, const void* a,
                   const void* b, const void* c);
