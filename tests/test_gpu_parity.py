@@ -187,6 +187,7 @@ CONV_CASES = [
     (1, 4, 6, 16, 17, 4, 2, 1),      # the same with 4 input channels, odd width (a cell past the last dY column)
     (2, 16, 128, 12, 12, 3, 1, 1),   # fp32 weight gradient on 128 x 128 tiles with split K (O and C*R*S >= 128)
     (2, 3, 16, 64, 64, 4, 2, 1),     # 4x4 stride 2 from 3 channels, 32-column output rows: fp32 cell forward
+    (2, 64, 32, 15, 20, 3, 1, 1),    # fp32 halo kernel from 64 channels (K split over waves), a partial row band
 ]
 
 
@@ -511,6 +512,8 @@ RELU_CASES = [
     (2, 1, 32, 12, 12, 3, 1, 1),     # one input channel (MI355X selector: direct)
     (2, 3, 16, 16, 17, 4, 2, 1),     # k4 s2 p1, 3 input channels: masked cell-wise input gradient
     (1, 2, 8, 16, 64, 4, 2, 1),      # k4 s2 p1 to 32-column rows: fp32 cell forward with the ReLU fused
+    (2, 32, 64, 9, 12, 3, 1, 1),     # fp32 halo kernel: ReLU forward, masked dX through the K-split form
+    (1, 64, 32, 8, 4, 3, 1, 1),      # fp32 halo kernel, 4-column rows
 ]
 
 

@@ -294,6 +294,10 @@ static int mask_after(int dt, const void* mask, void* grad, long n, hipStream_t 
   return VH_DISPATCH(dt, run_relu, mask, grad, grad, n, st);
 }
 
+static bool is_3x3_s1_p1(const ConvDims& d) {
+  return d.KH == 3 && d.KW == 3 && d.SH == 1 && d.SW == 1 && d.PH == 1 && d.PW == 1;
+}
+
 // act: 1 = ReLU on the output (fused into the epilogue where the kernel has it).
 static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, void* y, const ConvDims& d,
                      hipStream_t st, int act = 0) {
@@ -307,6 +311,10 @@ static int igemm_fwd(int dt, const void* x, const void* w, const void* bias, voi
     // 4x4 stride 2 from a few channels (the up-sampling layer's input gradient)
     int r = cell_fwd_f32(x, w, bias, y, g, act, st);
     if (r != VH_ERR_UNSUPPORTED) return r;
+    if (is_3x3_s1_p1(d)) {  // narrow images: the fp32 halo kernel
+      r = halo_conv3x3_f32(x, w, 0, bias, nullptr, y, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, act, st);
+      if (r != VH_ERR_UNSUPPORTED) return r;
+    }
   }
   // weight staging: the generic layout, or the halo kernel's channel-grouped one (padded to 16 channels)
   const size_t wbytes = std::max((size_t)d.O * d.C * RS * elem_size(dt),
@@ -492,9 +500,12 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   size_t ws_gemm = igemm_prepare(p);
   Carve cv;
   size_t o_w = cv.take(wbytes), o_g = cv.take(ws_gemm);
+  const bool halo_f32 = dt == VH_F32 && g_fast_paths && is_3x3_s1_p1(d) &&
+                        halo_conv3x3_f32_ok(dy, w, (int)d.B, (int)d.O, (int)d.H, (int)d.W, (int)d.C);
   if (need) {
-    // at most 4 input channels: the one-lane-per-position kernel, no workspace
-    if (g_fast_paths && dgrad_smallc_ok(g)) {
+    // at most 4 input channels: the one-lane-per-position kernel; fp32 3x3 of
+    // narrow images: the halo kernel -- neither takes workspace
+    if (g_fast_paths && (dgrad_smallc_ok(g) || halo_f32)) {
       *need = 0;
       return VH_OK;
     }
@@ -507,6 +518,8 @@ static int igemm_dgrad(int dt, const void* dy, const void* w, void* dx, const Co
   }
   // at most 4 input channels: one lane per input position, no workspace
   if (g_fast_paths && dgrad_smallc_ok(g)) return VH_DISPATCH(dt, run_dgrad_smallc, dy, w, nullptr, mask, dx, g, st);
+  if (halo_f32)  // dX = conv(dY, W rotated, O and C swapped), the ReLU mask in the epilogue
+    return halo_conv3x3_f32(dy, w, 1, nullptr, mask, dx, (int)d.B, (int)d.O, (int)d.H, (int)d.W, (int)d.C, 0, st);
   void* ws;
   VH_TRY(ws_get(st, cv.off, &ws));
   void* wd = at(ws, o_w);
@@ -574,6 +587,23 @@ static int igemm_wgrad(int dt, const void* dy, const void* x, void* dw, void* db
       int r = pw_conv_bf16_wgrad(dy, x, dw, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (int)d.SH,
                                  (float*)ws, nb, st);
       if (r != VH_ERR_UNSUPPORTED) return r;
+    }
+  }
+  if (dt == VH_F32 && g_fast_paths && is_3x3_s1_p1(d)) {
+    // fp32 3x3 of narrow images: the halo weight gradient (bias gradient included)
+    const size_t nb = halo_wgrad3x3_f32_ws(dy, x, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O);
+    if (nb && need) {
+      *need = nb;
+      return VH_OK;
+    }
+    if (nb) {
+      void* ws;
+      VH_TRY(ws_get(st, nb, &ws));
+      int r = halo_wgrad3x3_f32(dy, x, dw, db, (int)d.B, (int)d.C, (int)d.H, (int)d.W, (int)d.O, (float*)ws, nb, st);
+      if (r != VH_ERR_UNSUPPORTED) {
+        if (r == VH_OK && db_done) *db_done = db != nullptr;
+        return r;
+      }
     }
   }
   ConvGeom g = geom_of(d);

@@ -150,6 +150,22 @@ size_t wgrad_rows_ws(int N, int C, int H, int W, int O, int R, int S, int ph, in
 int wgrad_rows_bf16(const void* dy, const void* x, void* dw, void* db, int N, int C, int H, int W, int O, int R,
                     int S, int ph, int pw, float* ws, size_t ws_bytes, hipStream_t st);
 
+// ---- fp32 3x3 stride-1 pad-1 convolutions of narrow images (vh_halo_f32.hip) ----
+// Forward (dgrad = 0: w [O][C][3][3], + bias, act 1 = ReLU) or the input
+// gradient as a forward conv over dY (dgrad = 1: C = the layer's O, O = the
+// layer's C, w the layer's [C][O][3][3] read rotated and transposed), output
+// * 1[mask > 0] when mask is given.  W % 4 == 0, W <= 28, (C, O) = (32, 64) or
+// (64, 32), 16-byte aligned x and w; no workspace.
+bool halo_conv3x3_f32_ok(const void* x, const void* w, int N, int C, int H, int W, int O);
+int halo_conv3x3_f32(const void* x, const void* w, int dgrad, const void* bias, const void* mask, void* y, int N,
+                     int C, int H, int W, int O, int act, hipStream_t st);
+// Weight gradient of the same layers (dw [O][C][3][3], db [O] optional): the
+// workspace bytes it needs (0: unsupported shape), and the pass (partials per
+// (image, 7-row band) added in a fixed order by a second kernel).
+size_t halo_wgrad3x3_f32_ws(const void* dy, const void* x, int N, int C, int H, int W, int O);
+int halo_wgrad3x3_f32(const void* dy, const void* x, void* dw, void* db, int N, int C, int H, int W, int O,
+                      float* ws, size_t ws_bytes, hipStream_t st);
+
 // ---- dense bf16 products (vh_dense.hip) ----
 // C[M][N] = A . B (+ bias[N] per column), bf16 in and out.  A is stored
 // [M][lda] (K contiguous) or, with at, [K][lda] (M contiguous); B is stored
