@@ -10,15 +10,16 @@
 // rows x 32 columns of one image (a row's columns q >= W are computed and
 // dropped), K = (c, r, s) in the weight's own order.  A block stages the whole
 // weight matrix and the 9 input rows its outputs read in LDS:
-//   weights  wl[kq][k'][o]        k = kq * K/4 + k'  (the MFMA's four k lanes each walk one quarter of K)
+//   weights  wl[kq][o][k']        k = kq * K/4 + k'  (the MFMA's four k lanes each walk one quarter of K)
 //   input    xs[kq][c'][row][36]  channel kq * C/4 + c'; image column w at 4 + w, zeros at 3 and past W
 // so every tap (r, s) is an address shift, and a B fragment is one ds_read_b32
-// per lane (16 consecutive columns).  The quarter strides are 16 mod 64 floats:
-// the four k lanes of a read hit disjoint banks.
-// Waves: (o-tile of 16, column half of 16, K split); each holds the 16 x 16
-// tiles of the 7 rows (28 accumulators) and reads one A and 7 B fragments per
-// k step.  With a K split (O <= 32) the later waves' sums are handed over
-// through LDS and added after the first wave's, in split order.
+// per lane (16 consecutive columns).  The quarter strides are 16 mod 64 floats
+// and the weight rows have an odd pitch (K/4 + 1): the 16 rows x four k lanes of
+// a fragment read hit disjoint banks, and the staging writes of a row's
+// consecutive k are consecutive words.
+// Waves: (o-tile of 16, column half of 16, row group); with 64 output channels
+// a wave takes all 7 rows (one A and 7 B fragments per k step), with 32 two
+// waves on one SIMD take rows 0-3 and 4-6.
 //
 // Weight gradient: dw[o][c][r][s] = sum_{n,p,q} dy[n][o][p][q] x[n][c][p+r-1][q+s-1]
 // (and db[o] = sum dy).  GEMM view of a block (image, band of 7 output rows):
@@ -30,6 +31,8 @@
 // (36 accumulators): per k step one dY and 9 shifted x fragments.  Each block
 // writes its partial sums ([tap][O][C], then [O] for the bias) to the
 // workspace; a second kernel adds the blocks' partials in block order.
+#include <type_traits>
+
 #include "vh_kernels.hpp"
 
 namespace vh {
@@ -55,21 +58,21 @@ constexpr int quarter_stride(int n) { return n + ((16 - n % 64) % 64 + 64) % 64;
 template <int C, int O>
 struct HfCfg {
   static constexpr int K = 9 * C, KQ = K / 4, CQ = C / 4;
-  static constexpr int OT = O / 16, KS = 8 / (2 * OT);  // o-tiles, K splits
-  static constexpr int KQW = KQ / KS;                   // k steps per wave
-  static constexpr int WQS = quarter_stride(KQ * O);
+  static constexpr int OT = O / 16, RG = 8 / (2 * OT);  // o-tiles, row groups (rows 0-3 / 4-6)
+  static constexpr int WP = KQ + 1;  // weight row pitch (odd)
+  static constexpr int WQS = quarter_stride(WP * O);
   static constexpr int XQS = quarter_stride(CQ * kHfRows * kHfXP);
   static constexpr int LDS_FLOATS = 4 * WQS + 4 * XQS + 64;  // + tail read by dropped columns
-  static_assert(C % 4 == 0 && O % 16 == 0 && O <= 64 && KS * 2 * OT == 8, "shape");
-  static_assert(KQW % 9 == 0, "a wave's K range must hold whole channels");
+  static_assert(C % 4 == 0 && O % 16 == 0 && O <= 64 && RG * 2 * OT == 8 && RG <= 2, "shape");
+  static_assert(kHfRB == 7, "row groups of 4 and 3");
   static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
 };
 
 template <int C, int O, bool DG>
 __global__ __launch_bounds__(512) void halo_f32_kernel(HaloF32Args a) {
   using Cfg = HfCfg<C, O>;
-  constexpr int K = Cfg::K, KQ = Cfg::KQ, CQ = Cfg::CQ, OT = Cfg::OT, KS = Cfg::KS, KQW = Cfg::KQW;
-  constexpr int WQS = Cfg::WQS, XQS = Cfg::XQS;
+  constexpr int K = Cfg::K, KQ = Cfg::KQ, CQ = Cfg::CQ, OT = Cfg::OT, RG = Cfg::RG;
+  constexpr int WQS = Cfg::WQS, XQS = Cfg::XQS, WP = Cfg::WP;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float* wl = lds;
   float* xs = lds + 4 * WQS;
@@ -118,7 +121,7 @@ __global__ __launch_bounds__(512) void halo_f32_kernel(HaloF32Args a) {
           i = f / K;
           k = f % K;
         }
-        wl[(k / KQ) * WQS + (k % KQ) * O + i] = v[e];
+        wl[(k / KQ) * WQS + i * WP + k % KQ] = v[e];
       }
     }
   }
@@ -133,64 +136,49 @@ __global__ __launch_bounds__(512) void halo_f32_kernel(HaloF32Args a) {
   }
   __syncthreads();
 
-  // ---- multiply: wave = (o-tile, column half, K split)
-  const int ot = wave % OT, half = (wave / OT) & 1, kspl = wave / (2 * OT);
+  // ---- multiply and store: wave = (o-tile, column half, row group)
+  const int ot = wave % OT, half = (wave / OT) & 1, rg = wave / (2 * OT);
   const int kq = lane >> 4, j = lane & 15;
-  const float* ap = wl + kq * WQS + (kspl * KQW) * O + ot * 16 + j;
-  const float* bp = xs + kq * XQS + (kspl * (KQW / 9)) * kHfRows * kHfXP + half * 16 + j + 3;
-  f32x4 acc[kHfRB];
+  const float* ap = wl + kq * WQS + (ot * 16 + j) * WP;
+  const float* bp = xs + kq * XQS + half * 16 + j + 3;
+  const int q = half * 16 + j;
+  auto phase = [&](auto NRV, int t0) {
+    constexpr int NR = decltype(NRV)::value;
+    f32x4 acc[NR];
 #pragma unroll
-  for (int t = 0; t < kHfRB; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NR; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < KQW; ++ks) {
-    const int cc = ks / 9, r = (ks % 9) / 3, s = ks % 3;
-    const float av = ap[ks * O];
+    for (int ks = 0; ks < KQ; ++ks) {
+      const int cc = ks / 9, r = (ks % 9) / 3, s = ks % 3;
+      const float av = ap[ks];
 #pragma unroll
-    for (int t = 0; t < kHfRB; ++t)
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bp[(cc * kHfRows + t + r) * kHfXP + s], acc[t], 0, 0, 0);
-  }
-
-  // ---- K split: later waves hand their sums to the first, added in split order
-  if constexpr (KS > 1) {
-    __syncthreads();  // every wave is done reading the staged operands
-    float* hand = lds + ((wave % (2 * OT)) * (KS - 1) + (kspl > 0 ? kspl - 1 : 0)) * kHfRB * 4 * 64;
-    if (kspl > 0) {
-#pragma unroll
-      for (int t = 0; t < kHfRB; ++t)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) hand[(t * 4 + v) * 64 + lane] = acc[t][v];
+      for (int t = 0; t < NR; ++t)
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bp[(cc * kHfRows + t0 + t + r) * kHfXP + s], acc[t], 0,
+                                                      0, 0);
     }
-    __syncthreads();
-    if (kspl == 0) {
-#pragma unroll 1
-      for (int q = 1; q < KS; ++q) {
-        const float* h2 = hand + (q - 1) * kHfRB * 4 * 64;
+    // 16 consecutive columns of 4 output channels per store
+    if (q >= W) return;
 #pragma unroll
-        for (int t = 0; t < kHfRB; ++t)
+    for (int v = 0; v < 4; ++v) {
+      const int o = ot * 16 + kq * 4 + v;
+      const float b = a.bias ? a.bias[o] : 0.f;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[t][v] += h2[(t * 4 + v) * 64 + lane];
+      for (int t = 0; t < NR; ++t) {
+        const int p = p0 + t0 + t;
+        if (p >= H) break;
+        const long off = (((long)n * O + o) * H + p) * W + q;
+        float val = acc[t][v] + b;
+        if (a.act == 1) val = fmaxf(val, 0.f);
+        if (a.mask) val = a.mask[off] > 0.f ? val : 0.f;
+        a.y[off] = val;
       }
     }
-  }
-  if (kspl != 0) return;
-
-  // ---- epilogue: 16 consecutive columns of 4 output channels per store
-  const int q = half * 16 + j;
-  if (q >= W) return;
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int o = ot * 16 + kq * 4 + v;
-    const float b = a.bias ? a.bias[o] : 0.f;
-#pragma unroll
-    for (int t = 0; t < kHfRB; ++t) {
-      const int p = p0 + t;
-      if (p >= H) break;
-      const long off = (((long)n * O + o) * H + p) * W + q;
-      float val = acc[t][v] + b;
-      if (a.act == 1) val = fmaxf(val, 0.f);
-      if (a.mask) val = a.mask[off] > 0.f ? val : 0.f;
-      a.y[off] = val;
-    }
+  };
+  if constexpr (RG == 1) {
+    phase(std::integral_constant<int, kHfRB>(), 0);
+  } else {
+    if (rg == 0) phase(std::integral_constant<int, 4>(), 0);
+    else phase(std::integral_constant<int, 3>(), 4);
   }
 }
 
