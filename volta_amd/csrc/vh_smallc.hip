@@ -312,10 +312,12 @@ int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, in
   if (lds > 64 * 1024) return VH_ERR_UNSUPPORTED;
   a.tiles_m = (a.M + 255) / 256;
   a.tiles_o = (O + 63) / 64;
-  // position tiles per block (at most 8): one round of three blocks per CU on
-  // 256 CUs (the weights are loaded once per block)
+  // position tiles per block (at most 8): one round of two blocks per CU on
+  // 256 CUs -- the kernel holds ~255 registers per lane, two waves per SIMD
+  // (the weights are loaded once per block).  Sized for three blocks per CU,
+  // configs[4]'s 4096 tiles made 683 blocks: 1.33 rounds of 512 slots.
   const long tiles = (long)a.tiles_m * a.tiles_o;
-  a.tpb = (int)std::max<long>(1, std::min<long>(8, (tiles + 767) / 768));
+  a.tpb = (int)std::max<long>(1, std::min<long>(8, (tiles + 511) / 512));
   a.fPQ = FastDiv((uint32_t)(P * Q));
   a.fQ = FastDiv((uint32_t)Q);
   a.fHp = FastDiv((uint32_t)a.Hp);
