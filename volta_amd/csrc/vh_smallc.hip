@@ -45,8 +45,13 @@ struct SmallcArgs {
 
 constexpr int kEP = 72;  // epilogue LDS pitch (elements) of a wave's 64 x 64 tile
 
-template <int KP>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_smallc_fwd_bf16_kernel(SmallcArgs a) {
+// VEC: the 16-byte halo loads and the 16-byte epilogue (the configs' shapes),
+// compiled without the element-wise paths: 157 registers, three waves per SIMD
+// (with the element-wise paths in the same instance: 255, two).
+template <int KP, bool VEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(VEC ? 3 : 2))) void conv_smallc_fwd_bf16_kernel(
+    SmallcArgs a) {
+  const bool vec_halo = VEC || a.vec_halo, vec_epi = VEC || a.vec_epi;
   constexpr int WPITCH = KP + 8;  // weight row pitch (elements): 16-byte aligned rows, shifted banks
   extern __shared__ __attribute__((aligned(16))) uint16_t sm[];
   uint16_t* wl = sm;                                              // [64][WPITCH]
@@ -129,9 +134,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
   for (int tm = tm0; tm < tm_end; ++tm) {
   const int m0 = tm * 256;
   const int e_start = first_row(tm);
-  if (a.vec_halo) hload(e_start);  // issued before the barrier: the loads overlap the other waves' epilogue
+  if (vec_halo) hload(e_start);  // issued before the barrier: the loads overlap the other waves' epilogue
   if (tm != tm0) __syncthreads();  // the previous tile's epilogue is done with the LDS
-  if (a.vec_halo) {
+  if (vec_halo) {
 #pragma unroll
     for (int u = 0; u < kHU; ++u)
       if (hoff[u] >= 0) *reinterpret_cast<uint4*>(xl + hoff[u]) = hreg[u];
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     if (a.act == 1) r = fmaxf(r, 0.f);
     return __builtin_bit_cast(uint16_t, (__bf16)r);
   };
-  if (a.vec_epi) {
+  if (vec_epi) {
     __syncthreads();  // every wave is done with the halo and the weights
     // each wave's 64 x 64 tile goes through its own LDS region past the weights
     // and offsets, then out as 16-byte runs of 8 positions
@@ -312,12 +317,13 @@ int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, in
   if (lds > 64 * 1024) return VH_ERR_UNSUPPORTED;
   a.tiles_m = (a.M + 255) / 256;
   a.tiles_o = (O + 63) / 64;
-  // position tiles per block (at most 8): one round of two blocks per CU on
-  // 256 CUs -- the kernel holds ~255 registers per lane, two waves per SIMD
-  // (the weights are loaded once per block).  Sized for three blocks per CU,
-  // configs[4]'s 4096 tiles made 683 blocks: 1.33 rounds of 512 slots.
+  // position tiles per block (at most 8): one round of the blocks per CU the
+  // instance's registers allow on 256 CUs -- three for the vector instance, two
+  // for the generic one (the weights are loaded once per block)
+  const bool vec = a.vec_halo && a.vec_epi;
+  const long slots = vec ? 768 : 512;
   const long tiles = (long)a.tiles_m * a.tiles_o;
-  a.tpb = (int)std::max<long>(1, std::min<long>(8, (tiles + 511) / 512));
+  a.tpb = (int)std::max<long>(1, std::min<long>(8, (tiles + slots - 1) / slots));
   a.fPQ = FastDiv((uint32_t)(P * Q));
   a.fQ = FastDiv((uint32_t)Q);
   a.fHp = FastDiv((uint32_t)a.Hp);
@@ -329,9 +335,15 @@ int smallc_conv_bf16(const void* x, const void* w, const void* bias, void* y, in
   const dim3 grid((unsigned)((a.tiles_m + a.tpb - 1) / a.tpb * a.tiles_o));
 #define VH_SMALLC_FWD(KPV)                                                    \
   if (KP == KPV) {                                                            \
-    auto kern = conv_smallc_fwd_bf16_kernel<KPV>;                             \
-    VH_LDS_LIMIT_ONCE(kern);                                                  \
-    kern<<<grid, 256, lds, st>>>(a);                                          \
+    if (vec) {                                                                \
+      auto kern = conv_smallc_fwd_bf16_kernel<KPV, true>;                     \
+      VH_LDS_LIMIT_ONCE(kern);                                                \
+      kern<<<grid, 256, lds, st>>>(a);                                        \
+    } else {                                                                  \
+      auto kern = conv_smallc_fwd_bf16_kernel<KPV, false>;                    \
+      VH_LDS_LIMIT_ONCE(kern);                                                \
+      kern<<<grid, 256, lds, st>>>(a);                                        \
+    }                                                                         \
     VH_LAUNCH_CHECK();                                                        \
     return VH_OK;                                                             \
   }
