@@ -187,7 +187,9 @@ CONV_CASES = [
     (1, 4, 6, 16, 17, 4, 2, 1),      # the same with 4 input channels, odd width (a cell past the last dY column)
     (2, 16, 128, 12, 12, 3, 1, 1),   # fp32 weight gradient on 128 x 128 tiles with split K (O and C*R*S >= 128)
     (2, 3, 16, 64, 64, 4, 2, 1),     # 4x4 stride 2 from 3 channels, 32-column output rows: fp32 cell forward
-    (2, 64, 32, 15, 20, 3, 1, 1),    # fp32 halo kernel from 64 channels (K split over waves), a partial row band
+    (2, 64, 32, 15, 20, 3, 1, 1),    # fp32 halo kernel from 64 channels (rows split over wave pairs), a partial band
+    (3, 32, 64, 1, 8, 3, 1, 1),      # fp32 halo kernels, one-row images (the band's other rows are padding)
+    (2, 32, 64, 7, 28, 3, 1, 1),     # fp32 halo kernels, exactly one 7-row band
 ]
 
 
@@ -377,6 +379,7 @@ CT_CASES = [
     (2, 16, 3, 4, 32, 4, 2, 1),      # the same kernel, 4 input rows
     (1, 64, 4, 2, 64, 4, 2, 1),      # two 32-position segments per input row, 4 output channels
     (2, 8, 1, 3, 32, 4, 2, 1),       # 1 output channel, odd input height
+    (2, 512, 128, 3, 4, 4, 2, 1),    # 512 x 128 weight rows: the row-wise stride-phase weight relayout
 ]
 
 
