@@ -190,6 +190,7 @@ CONV_CASES = [
     (2, 64, 32, 15, 20, 3, 1, 1),    # fp32 halo kernel from 64 channels (rows split over wave pairs), a partial band
     (3, 32, 64, 1, 8, 3, 1, 1),      # fp32 halo kernels, one-row images (the band's other rows are padding)
     (2, 32, 64, 7, 28, 3, 1, 1),     # fp32 halo kernels, exactly one 7-row band
+    (2, 4, 24, 10, 16, 3, 1, 1),     # bf16 few-channel 3x3 weight gradient, (channel, tap) MFMA columns (C*S = 12)
 ]
 
 

@@ -850,6 +850,176 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// The same weight gradient for C * S <= 16 (an RGB 5x5 or a few-channel 3x3
+// layer) with the MFMA's 16 B columns holding (c, s) = c * S + s instead of the
+// channels alone: per row r one v_mfma_f32_16x16x32_bf16 covers every
+// (channel, column tap) -- R MFMAs per K step instead of R * S with 13 of 16
+// columns empty.  Operands: A = the lane's aligned 8-column dY chunk (o = lane %
+// 16, columns v .. v+7 of the step's output row; no shifted windows, so no
+// neighbour chunks of dY); B = for column j = (c, s) the 8 x values of channel c,
+// input row p - ph + r, starting at column v + s - PW: a lane window taken at a
+// lane-dependent offset (8 + s - PW elements) out of its channel's chunks v - 8,
+// v, v + 8 (the outer ones from the lanes 16 below / above, or one more load at
+// the wave's edges).  Rows walk as in wgrad_smallc_bf16_kernel (p fastest): a
+// step computes the window of its one new x row and keeps the other R - 1.
+// Partials: the same [split][tap][O][C] and [split][O] as that kernel.
+template <int R, int S, int PW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 4))) void wgrad_smallc_cs_bf16_kernel(
+    SmallcArgs a) {
+  static_assert(PW <= 2 && S - 1 - PW <= 2, "x windows reach at most 2 columns either side");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tile_o = blockIdx.x % a.tiles_o, split = blockIdx.x / a.tiles_o;
+  const int ob = tile_o * 64 + wave * 16;  // the wave's first o
+  const int kg = lane >> 4, li = lane & 15;
+  const int o = ob + li;                   // A row of this lane
+  const int c = li / S, s = li - (li / S) * S;  // B column (c, s) of this lane
+  const bool o_ok = o < a.O, c_ok = li < a.C * S;
+  const int PQ = a.P * a.Q, HW = a.H * a.W;
+  const __amdgpu_buffer_rsrc_t dyr = __builtin_amdgcn_make_buffer_rsrc((void*)a.dy, (short)0, a.dy_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xrr = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, a.x_bytes, 0x00020000);
+  const int OOR = (int)0x80000000u;
+  // window start (elements) in the lane's 24 x columns v - 8 .. v + 15: the
+  // window's dwords start at dword 3 + t (t = e / 2 - 3 in 0..3), shifted by a
+  // half dword when e is odd; selections as bit masks (branch-free: the lanes
+  // of a wave take different t)
+  const int e = 8 + s - PW, t3 = (e >> 1) - 3;
+  const uint32_t m1 = (t3 & 1) ? ~0u : 0u, m2 = (t3 & 2) ? ~0u : 0u, modd = (e & 1) ? ~0u : 0u;
+
+  const int step_b = split * a.steps_per_split;
+  const int step_e = min(a.total_steps, step_b + a.steps_per_split);
+  const int nsteps = step_e - step_b;  // >= 1 (splits are sized so)
+
+  // operands of a step: the dY chunk, and the x chunk (+ the wave-edge chunk)
+  // of each x row it has to load (all R at a chunk's first row, else the last)
+  struct Ops {
+    u32x4w dz, xz[R], xe[R];
+  };
+  int n, p, qc;
+  {
+    const int PN = a.P * a.nq;
+    n = step_b / PN;
+    const int rem = step_b - n * PN;
+    qc = rem / a.P;
+    p = rem - qc * a.P;
+  }
+  auto xrow_ld = [&](Ops& f, int r, int slot) {
+    const int v = qc * 32 + kg * 8, ve = kg == 0 ? v - 8 : v + 8;
+    const bool edge = kg == 0 || kg == 3;
+    const int h = p - a.ph + r;
+    const bool hok = c_ok && h >= 0 && h < a.H;
+    const int rb = ((n * a.C + c) * HW + h * a.W) * 2;
+    f.xz[slot] = BufLoad<8>::ld(xrr, hok && v < a.W ? rb + v * 2 : OOR, 0);
+    f.xe[slot] = BufLoad<8>::ld(xrr, hok && edge && ve >= 0 && ve < a.W ? rb + ve * 2 : OOR, 0);
+  };
+  // all: load every x row (a chunk's first row, or a split's first step)
+  auto load = [&](Ops& f, bool all) {
+    const int v = qc * 32 + kg * 8;
+    f.dz = BufLoad<8>::ld(dyr, o_ok && v < a.Q ? ((n * a.O + o) * PQ + p * a.Q + v) * 2 : OOR, 0);
+    if (all) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) xrow_ld(f, r, r);
+    } else {
+      xrow_ld(f, R - 1, R - 1);
+    }
+  };
+  auto advance = [&]() {
+    ++p;
+    const int w1 = p == a.P;
+    p = w1 ? 0 : p;
+    qc += w1;
+    const int w2 = qc == a.nq;
+    qc = w2 ? 0 : qc;
+    n += w2;
+  };
+  // the lane's window of one x row: 8 elements from offset e of (xm, xz, xp)
+  auto window = [&](const u32x4w& xz, const u32x4w& xe) {
+    uint32_t w[12];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (uint32_t)__shfl((int)xz[i], lane - 16, 64);
+      const uint32_t hi = (uint32_t)__shfl((int)xz[i], lane + 16, 64);
+      w[i] = kg == 0 ? xe[i] : lo;
+      w[4 + i] = xz[i];
+      w[8 + i] = kg == 3 ? xe[i] : hi;
+    }
+    auto pick = [](uint32_t m, uint32_t a, uint32_t b) { return (a & m) | (b & ~m); };  // m ? a : b
+    u32x4w out;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // dwords 3 + t3 + i and 4 + t3 + i
+      const uint32_t d0 = pick(m2, pick(m1, w[6 + i], w[5 + i]), pick(m1, w[4 + i], w[3 + i]));
+      const uint32_t d1 = pick(m2, pick(m1, w[7 + i], w[6 + i]), pick(m1, w[5 + i], w[4 + i]));
+      out[i] = pick(modd, __builtin_amdgcn_alignbyte(d1, d0, 2), d0);
+    }
+    return out;
+  };
+
+  f32x4 acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float bsum = 0.f;
+  const bool do_bias = a.dbias_part != nullptr;
+  u32x4w win[R];  // the windows of the step's R x rows (rows 0 .. R-2 carried over)
+
+  // all: the step loaded every x row (all R windows new)
+  auto compute = [&](const Ops& f, bool all) {
+    if (all) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) win[r] = window(f.xz[r], f.xe[r]);
+    } else {
+#pragma unroll
+      for (int r = 0; r + 1 < R; ++r) win[r] = win[r + 1];
+      win[R - 1] = window(f.xz[R - 1], f.xe[R - 1]);
+    }
+    const bf16x8 ad = __builtin_bit_cast(bf16x8, f.dz);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ad, __builtin_bit_cast(bf16x8, win[r]), acc[r], 0, 0, 0);
+    if (do_bias) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        bsum += __uint_as_float(f.dz[i] << 16) + __uint_as_float(f.dz[i] & 0xffff0000u);
+    }
+  };
+
+  // two operand sets: the loads of step k+1 are issued before the MFMAs of
+  // step k; the last prefetch re-reads the final step (always in range)
+  Ops fa, fb;
+  bool all_a = true, all_b;  // the split's first step has no carried windows
+  load(fa, true);
+  int k = 0;
+  for (; k + 2 <= nsteps; k += 2) {
+    advance();
+    all_b = p == 0;
+    load(fb, all_b);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fa, all_a);
+    __builtin_amdgcn_sched_barrier(0);
+    if (k + 2 < nsteps) advance();
+    all_a = p == 0;
+    load(fa, all_a);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(fb, all_b);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (k < nsteps) compute(fa, all_a);
+
+  // partials: lane holds D[o = ob + 4*kg + j][column li = (c, s)] for each row r
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int oo = ob + kg * 4 + j;
+      if (oo < a.O && c_ok) a.part[(((long)split * R * S + r * S + s) * a.O + oo) * a.C + c] = acc[r][j];
+    }
+  if (do_bias) {
+    bsum += __shfl_xor(bsum, 16, 64);
+    bsum += __shfl_xor(bsum, 32, 64);
+    if (kg == 0 && o_ok) a.dbias_part[(long)split * a.O + o] = bsum;
+  }
+}
+
 namespace {
 
 struct WgradPlan {
@@ -964,7 +1134,9 @@ bool plan_smallc(SmallcArgs& a, int N, int C, int H, int W, int O, int R, int S,
   a.nq = (std::max(W, Q) + 31) / 32;
   a.total_steps = N * P * a.nq;
   a.tiles_o = (O + 63) / 64;
-  // about two blocks per CU (about 190 VGPRs per lane: two waves per SIMD)
+  // about two blocks per CU (the per-channel kernel: ~190 VGPRs, two waves
+  // per SIMD; the (channel, tap) kernel fits three, but 768 blocks measured
+  // equal in its loop and 3 us slower in the reduction of their partials)
   const int splits = std::max(1, std::min(a.total_steps, (512 + a.tiles_o - 1) / a.tiles_o));
   a.steps_per_split = (a.total_steps + splits - 1) / splits;
   a.dy_bytes = (int)dyb;
@@ -976,6 +1148,19 @@ int smallc_splits(const SmallcArgs& a) { return (a.total_steps + a.steps_per_spl
 
 int launch_smallc(const SmallcArgs& a, int R, int S, int pw, hipStream_t st) {
   const dim3 grid((unsigned)(a.tiles_o * smallc_splits(a)));
+  if (a.C * S <= 16) {  // (channel, column tap) in the MFMA columns
+    if (R == 5) {
+      wgrad_smallc_cs_bf16_kernel<5, 5, 2><<<grid, 256, 0, st>>>(a);
+    } else if (pw == 0) {
+      wgrad_smallc_cs_bf16_kernel<3, 3, 0><<<grid, 256, 0, st>>>(a);
+    } else if (pw == 1) {
+      wgrad_smallc_cs_bf16_kernel<3, 3, 1><<<grid, 256, 0, st>>>(a);
+    } else {
+      wgrad_smallc_cs_bf16_kernel<3, 3, 2><<<grid, 256, 0, st>>>(a);
+    }
+    VH_LAUNCH_CHECK();
+    return VH_OK;
+  }
   if (R == 5) {
     wgrad_smallc_bf16_kernel<5, 5, 2><<<grid, 256, 0, st>>>(a);
   } else if (pw == 0) {
