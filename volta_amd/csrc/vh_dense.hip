@@ -42,6 +42,7 @@ struct DenseArgs {
   const uint16_t* bias;  // [N] or nullptr (added to every row)
   uint16_t* colsum;      // [N] or nullptr: column sums of an MN-major B over K (128 x 128 tiles only)
   int cs_shift;          // columns per block of the column sums: 4 << cs_shift (set at launch)
+  int vec_epi;           // C 16-byte aligned, ldc and N multiples of 8: 16-byte stores through LDS
   int M, N, K, lda, ldb, ldc;
   int a_bytes, b_bytes, c_bytes;
   int tiles_m, tiles_n;
@@ -356,8 +357,38 @@ __device__ __forceinline__ void gemm_bf16_tile(const DenseArgs& g, const int lb)
     }
   }
 
-  // epilogue: fp32 (+ bias), one rounding, row-major stores (lanes walk columns)
   const __amdgpu_buffer_rsrc_t cr = rsrc(g.c, g.c_bytes);
+  if (g.vec_epi) {
+    // epilogue: fp32 (+ bias), one rounding, the wave's tile through its own LDS
+    // region (pitch WN + 8 elements), then out as 16-byte runs of 8 columns: 16
+    // (8) stores per lane instead of 128 (64) two-byte ones
+    constexpr int WMR = FM * 32, WN = FN * 32, EP = WN + 8, CPR = WN / 8, RPI = 64 / CPR;
+    static_assert(4 * WMR * EP * 2 <= 2 * STAGE * 16, "epilogue tiles exceed the LDS stages");
+    if constexpr (!PC) __syncthreads();  // PC: the consumers' last stage barrier already passed
+    uint16_t* eb = reinterpret_cast<uint16_t*>(lds) + wave * WMR * EP;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int cw = j * 32 + row_l, col = n0 + wn + cw;
+      const float bv = (BIAS && col < g.N) ? bf16_to_f32(g.bias[col]) : 0.f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          eb[(i * 32 + (v >> 2) * 8 + half_l * 4 + (v & 3)) * EP + cw] =
+              __builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][v] + bv));
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the wave's LDS writes are done
+    __builtin_amdgcn_wave_barrier();
+    const int ch = lane % CPR, col = n0 + wn + ch * 8;
+#pragma unroll
+    for (int it = 0; it < WMR / RPI; ++it) {
+      const int rw = it * RPI + lane / CPR, row = m0 + wm + rw;
+      const u32x4d v = *reinterpret_cast<const u32x4d*>(eb + rw * EP + ch * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(v, cr, row < g.M && col < g.N ? (row * g.ldc + col) * 2 : kOOR, 0, 0);
+    }
+    return;
+  }
+  // epilogue: fp32 (+ bias), one rounding, row-major stores (lanes walk columns)
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     const int col = n0 + wn + j * 32 + row_l;
@@ -450,6 +481,7 @@ DenseArgs dense_args(const void* a, int lda, bool at, const void* b, int ldb, bo
                      int N, int K, const void* bias, void* colsum) {
   DenseArgs g{};
   g.colsum = (uint16_t*)colsum;
+  g.vec_epi = ((uintptr_t)c & 15) == 0 && ldc % 8 == 0 && N % 8 == 0;
   g.a = (const uint16_t*)a;
   g.b = (const uint16_t*)b;
   g.c = (uint16_t*)c;
