@@ -1,0 +1,76 @@
+"""GPU parity of the 256 x 256 bf16 product tiles (operands copied straight
+into LDS, swizzled layouts): whole outputs of every operand layout they serve
+-- matmul (K-major x MN-major), its dA (K-major x K-major) and dB (MN-major x
+MN-major), and the Linear forward with its bias -- at shapes that take them
+(M and N multiples of 256 with at least 256 tiles, K a multiple of 128: one
+and three turns of the four-stage loop), against the CPU oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from volta_amd import nn as vnn
+from volta_amd import ops
+from tests.parity import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def prep(a):
+    r = oracle.round_bf16(np.ascontiguousarray(a, np.float32))
+    return r, torch.from_numpy(r).to(DEV, torch.bfloat16)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.float().cpu().numpy()
+
+
+def check(got, fn, args, what, k, extra=None):
+    ref = fn(*args)
+    scale = fn(*[np.abs(a) for a in args])
+    if extra is not None:
+        ref = ref + extra
+        scale = scale + np.abs(extra)
+    assert_parity(host(got), ref, scale, "bf16", what, k=k)
+
+
+@pytest.mark.parametrize("kk", [128, 384])
+def test_matmul_256_tiles(kk):
+    m, n = 4096, 4096
+    g = np.random.default_rng(kk + 1)
+    a, at = prep(g.standard_normal((m, kk)))
+    b, bt = prep(g.standard_normal((kk, n)))
+    check(ops.gpu_matmul(at, bt, m, kk, n), oracle.matmul, (a, b), f"C = A.B, K = {kk}", k=kk)
+
+
+def test_matmul_backward_a_256_tiles():
+    # dA[m][k] = G[m][n] . B[k][n]^T: M = m, N = k, contraction n
+    m, k, n = 4096, 4096, 128
+    g = np.random.default_rng(21)
+    gr, grt = prep(g.standard_normal((m, n)))
+    b, bt = prep(g.standard_normal((k, n)))
+    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), "dA", k=n)
+
+
+def test_matmul_backward_b_256_tiles():
+    # dB[k][n] = A[m][k]^T . G[m][n]: M = k, N = n, contraction m
+    m, k, n = 128, 4096, 4096
+    g = np.random.default_rng(22)
+    a, at = prep(g.standard_normal((m, k)))
+    gr, grt = prep(g.standard_normal((m, n)))
+    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), "dB", k=m)
+
+
+def test_linear_forward_256_tiles():
+    m, i, o = 4096, 128, 4096
+    g = np.random.default_rng(23)
+    x, xt = prep(g.standard_normal((m, i)))
+    w, wt = prep(g.uniform(-0.5, 0.5, (i, o)))
+    b, bt = prep(g.uniform(-1, 1, (o,)))
+    lin = vnn.Linear(i, o, device=DEV, dtype=torch.bfloat16)
+    lin.weight, lin.bias = wt, bt
+    check(lin.forward(xt), oracle.matmul, (x, w), "Linear y = x.W + b", k=i + 1, extra=b[None, :])

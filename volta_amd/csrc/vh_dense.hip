@@ -428,6 +428,250 @@ void gemm_bf16_pair_kernel(DenseArgs g0, DenseArgs g1) {
     gemm_bf16_tile<128, BN, false, PC, AT1, BT1>(g1, xcd_map(h - t0, g1.tiles_m * g1.tiles_n));
 }
 
+// ---------------------------------------------------------------- 256 x 256 tiles, direct-to-LDS loads
+// For products whose M and N are multiples of 256 and K a multiple of 128 (the
+// square product and its gradients, a Linear forward over whole 256-row
+// tiles).  The operands are copied from global memory straight into LDS by
+// buffer_load_dwordx4 ... lds (no registers and no LDS store instructions on
+// the way), four LDS stages of 32 k, the copies of stage s+3 issued while
+// stage s is multiplied.  NW waves split the tile 2 (m) x NW/2 (n): NW = 8
+// gives 128 x 64 per wave (128 accumulator registers, two waves per SIMD, so
+// one wave's copy issue and barrier waits are covered by the other's MFMAs);
+// NW = 4 gives 128 x 128 (256 accumulator registers, one wave per SIMD).
+// LDS DMA writes a wave's 64 16-byte units contiguously (lane l at unit l of
+// the instruction's base), so a tile's layout is set by which global unit each
+// lane fetches; an XOR swizzle of the unit index keeps the fragment reads
+// free of bank conflicts (16 consecutive lanes on 16 distinct 16-byte bank
+// groups; measured: 0.8 % conflict cycles):
+//  * K-major tile (256 rows x 32 k, 4 units per row, row r at units 4r ..
+//    4r+3): slot t of row r holds k unit t ^ ((r >> 2) & 3).  Copy
+//    instruction c (0 .. 15) covers rows 16c .. 16c+15.
+//  * MN-major tile (32 k rows x 256, 32 units per k row): slot t of k row kr
+//    holds row unit t ^ (4 (kr & 3)).  Instruction c covers k rows 2c, 2c+1.
+// The copies are issued as inline assembly, so the compiler's wait-count pass
+// does not see them (it would otherwise order fragment reads after all copies
+// in flight): the waits are explicit -- vmcnt(N) for the thread's own copies
+// of the next stage (the later stages stay in flight), lgkmcnt(0) for its
+// fragment reads -- in one statement with the s_barrier, which clobbers memory
+// so that no LDS read moves across it.  The four stages are separate static
+// arrays and the main loop is unrolled by four.
+constexpr int kD2lBK = 32;       // k per stage
+constexpr int kD2lUnits = 1024;  // 16-byte units per operand tile per stage
+#ifndef VH_D2L_WAVES
+#define VH_D2L_WAVES 8
+#endif
+
+template <int B>
+__device__ __forceinline__ u32x4d* d2l_stage(u32x4d* s0, u32x4d* s1, u32x4d* s2, u32x4d* s3) {
+  return B == 0 ? s0 : B == 1 ? s1 : B == 2 ? s2 : s3;
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes (voff + soff) land at LDS
+// byte la + 16 l; M0 holds la (the s_nop covers the M0 -> LDS DMA hazard).
+__device__ __forceinline__ void d2l_copy(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t la) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "s"(la)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0), then the block barrier
+template <int N>
+__device__ __forceinline__ void d2l_sync() {
+  static_assert(N == 0 || N == 4 || N == 8 || N == 16, "vmcnt");
+  if constexpr (N == 16)
+    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 8)
+    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else if constexpr (N == 4)
+    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const u32x4d* p) {
+  return __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) u32x4d*)p);
+}
+
+template <bool AT, bool BT, bool BIAS, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+void gemm_bf16_d2l_kernel(DenseArgs g) {
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  constexpr int WNW = NW / 2;        // waves along n
+  constexpr int FN = 8 / WNW;        // 32-column fragments per wave (FM = 4 rows of 32)
+  constexpr int CPW = 16 / NW;       // copy instructions per wave and operand per stage
+  constexpr int VM1 = 2 * CPW;       // copies per thread per stage
+  __shared__ __attribute__((aligned(16))) u32x4d S0[2 * kD2lUnits];
+  __shared__ __attribute__((aligned(16))) u32x4d S1[2 * kD2lUnits];
+  __shared__ __attribute__((aligned(16))) u32x4d S2[2 * kD2lUnits];
+  __shared__ __attribute__((aligned(16))) u32x4d S3[2 * kD2lUnits];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave / WNW) * 128, wn = (wave % WNW) * (FN * 32);
+  const int lb = xcd_block(g.tiles_m * g.tiles_n);
+  const int grp = lb / (kGroupM * g.tiles_n), first_m = grp * kGroupM;
+  const int gm = min(g.tiles_m - first_m, kGroupM);
+  const int in_grp = lb - grp * kGroupM * g.tiles_n;
+  const int m0 = (first_m + in_grp % gm) * 256, n0 = (in_grp / gm) * 256;
+
+  // the thread's load units per operand (k0 = 0; the stage's k0 is a scalar
+  // offset), instruction c = CPW * wave + i
+  auto unit_off = [&](bool mn, int rc0, int ld, int i) {
+    const int c = CPW * wave + i;
+    if (!mn) {
+      const int r = 16 * c + (lane >> 2), u = (lane & 3) ^ ((lane >> 4) & 3);
+      return ((rc0 + r) * ld + 8 * u) * 2;
+    }
+    const int kr = 2 * c + (lane >> 5), mu = (lane & 31) ^ (4 * (kr & 3));
+    return (kr * ld + rc0 + 8 * mu) * 2;
+  };
+  int aoff[CPW], boff[CPW];
+#pragma unroll
+  for (int i = 0; i < CPW; ++i) {
+    aoff[i] = unit_off(AT, m0, g.lda, i);
+    boff[i] = unit_off(BT, n0, g.ldb, i);
+  }
+  const __amdgpu_buffer_rsrc_t ar = rsrc(g.a, g.a_bytes), br = rsrc(g.b, g.b_bytes);
+  auto issue = [&](u32x4d* st, int k0) {
+    const int ask = __builtin_amdgcn_readfirstlane(AT ? k0 * g.lda * 2 : k0 * 2);
+    const int bsk = __builtin_amdgcn_readfirstlane(BT ? k0 * g.ldb * 2 : k0 * 2);
+    const uint32_t la = lds_addr(st) + wave * CPW * 64 * 16;
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) d2l_copy(ar, aoff[i], ask, la + i * 64 * 16);
+#pragma unroll
+    for (int i = 0; i < CPW; ++i) d2l_copy(br, boff[i], bsk, la + (kD2lUnits + i * 64) * 16);
+  };
+
+  // fragment addresses (bytes from the operand tile's start) of k step kk (0, 1)
+  const int row_l = lane & 31, half_l = lane >> 5;
+  // K-major: row = base + row_l, k unit 2 kk + half_l
+  int kfrag[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) kfrag[kk] = (4 * row_l + ((2 * kk + half_l) ^ ((lane >> 2) & 3))) * 16;
+  // MN-major (transposing reads): k row 16 kk + 8 half_l + (lane & 15) / 4
+  // (+4 for the second read), columns 16 ((lane >> 4) & 1) + 4 (lane & 3) .. +3
+  const int tr_row = 8 * half_l + ((lane & 15) >> 2), x4 = 4 * ((lane >> 2) & 3);
+  const int tr_lo = tr_row * 32 * 16 + (2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) * 16 + 8 * (lane & 1);
+  auto mn_unit0 = [&](int col0) { return ((col0 >> 3) ^ x4) * 16; };
+  int amn[4], bmn[FN];
+#pragma unroll
+  for (int f = 0; f < 4; ++f) amn[f] = tr_lo + mn_unit0(wm + 32 * f);
+#pragma unroll
+  for (int f = 0; f < FN; ++f) bmn[f] = tr_lo + mn_unit0(wn + 32 * f);
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  typedef short v8i16 __attribute__((ext_vector_type(8)));
+  auto read_tr = [&](const u32x4d* tile, int byte) {
+    const __attribute__((address_space(3))) char* p = (const __attribute__((address_space(3))) char*)tile + byte;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)p);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p + 4 * 32 * 16));
+    const v8i16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8, v);
+  };
+  struct Frags {
+    bf16x8 a[4], b[FN];
+  };
+  auto read = [&](const u32x4d* st, int kk, Frags& f) {
+    const u32x4d* at = st;
+    const u32x4d* bt = st + kD2lUnits;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      f.a[i] = AT ? read_tr(at, amn[i] + kk * 16 * 32 * 16)
+                  : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
+                                                   reinterpret_cast<const char*>(at) + (wm + 32 * i) * 64 + kfrag[kk]));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      f.b[j] = BT ? read_tr(bt, bmn[j] + kk * 16 * 32 * 16)
+                  : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
+                                                   reinterpret_cast<const char*>(bt) + (wn + 32 * j) * 64 + kfrag[kk]));
+  };
+  f32x16 acc[4][FN];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+  };
+
+  const int nst = g.K / kD2lBK;  // a multiple of 4 (>= 4)
+  issue(S0, 0);
+  issue(S1, kD2lBK);
+  issue(S2, 2 * kD2lBK);
+  d2l_sync<2 * VM1>();
+  Frags f0, f1;
+  read(S0, 0, f0);
+  // stage s sits in buffer s % 4; f0 holds its first k step on entry
+  auto body = [&](auto BUF, int s) {
+    constexpr int B = decltype(BUF)::value;
+    u32x4d* cur = d2l_stage<B>(S0, S1, S2, S3);
+    // buffer (s + 3) % 4 held stage s - 1, which every wave finished reading
+    // before the last barrier
+    if (s + 3 < nst) issue(d2l_stage<(B + 3) & 3>(S0, S1, S2, S3), (s + 3) * kD2lBK);
+    read(cur, 1, f1);
+    mma(f0);
+    if (s + 1 < nst) {
+      // the thread's copies of stage s+1 have landed (stages s+2, s+3 may
+      // still be in flight) and its fragment reads of stage s are done; after
+      // the barrier every wave's are
+      if (s + 3 < nst) d2l_sync<2 * VM1>(); else if (s + 2 < nst) d2l_sync<VM1>(); else d2l_sync<0>();
+      read(d2l_stage<(B + 1) & 3>(S0, S1, S2, S3), 0, f0);
+    }
+    mma(f1);
+  };
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C3 = std::integral_constant<int, 3>;
+  for (int s = 0; s < nst; s += 4) {
+    body(C0{}, s);
+    body(C1{}, s + 1);
+    body(C2{}, s + 2);
+    body(C3{}, s + 3);
+  }
+
+  // epilogue: fp32 (+ bias), one rounding, through LDS in two halves of the
+  // wave's 128 rows (pitch FN * 32 + 8 elements), out as 16-byte runs.  Wave
+  // w's region: stage array w (NW = 4: 17 KB) or half of array w / 2 (NW = 8:
+  // 9 KB each).
+  __syncthreads();  // every wave is done reading the stages
+  constexpr int WN = FN * 32, EP = WN + 8, CPR = WN / 8, RPI = 64 / CPR;
+  static_assert(64 * EP * 2 * (NW / 4) <= 2 * kD2lUnits * 16, "epilogue regions exceed a stage array");
+  const int ea = NW == 4 ? wave : wave >> 1;
+  u32x4d* const earr = ea == 0 ? S0 : ea == 1 ? S1 : ea == 2 ? S2 : S3;
+  uint16_t* eb = reinterpret_cast<uint16_t*>(earr) + (NW == 4 ? 0 : (wave & 1) * 64 * EP);
+  const __amdgpu_buffer_rsrc_t cr = rsrc(g.c, g.c_bytes);
+  float bv[FN];
+#pragma unroll
+  for (int j = 0; j < FN; ++j) bv[j] = BIAS ? bf16_to_f32(g.bias[n0 + wn + j * 32 + row_l]) : 0.f;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          eb[(ii * 32 + (v >> 2) * 8 + half_l * 4 + (v & 3)) * EP + j * 32 + row_l] =
+              __builtin_bit_cast(uint16_t, (__bf16)(acc[2 * h + ii][j][v] + bv[j]));
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+    const int ch = lane % CPR, col = n0 + wn + ch * 8;
+#pragma unroll
+    for (int it = 0; it < 64 / RPI; ++it) {
+      const int rw = it * RPI + lane / CPR, row = m0 + wm + h * 64 + rw;
+      const u32x4d v = *reinterpret_cast<const u32x4d*>(eb + rw * EP + ch * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * g.ldc + col) * 2, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
 // Column-sum ownership on BN-column tiles: 2^cs_shift groups of 4 columns per
 // block, the smallest power-of-2 width >= BN / tiles_m (at least 16 columns).
 int colsum_shift(int tiles_m, int BN) {
@@ -500,6 +744,26 @@ DenseArgs dense_args(const void* a, int lda, bool at, const void* b, int ldb, bo
 
 // 128 x 256 tiles when they still give at least one block per CU
 bool dense_big(int M, int N) { return (long)((M + 127) / 128) * ((N + 255) / 256) >= 256; }
+
+// The 256 x 256 direct-to-LDS kernel: whole tiles only (no bounds checks in
+// its loads or stores), K in whole stages, 16-byte aligned rows of every
+// operand, and a grid of at least one block per CU.
+bool dense_d2l(const DenseArgs& g, bool colsum) {
+  return !colsum && g.M % 256 == 0 && g.N % 256 == 0 && g.K % (4 * kD2lBK) == 0 && g.vec_epi &&
+         (long)(g.M / 256) * (g.N / 256) >= 256;
+}
+
+template <bool AT, bool BT>
+int launch_d2l(const DenseArgs& a0, hipStream_t st) {
+  DenseArgs a = a0;
+  a.tiles_m = a.M / 256;
+  a.tiles_n = a.N / 256;
+  constexpr int NW = VH_D2L_WAVES;
+  auto kern = a.bias ? gemm_bf16_d2l_kernel<AT, BT, true, NW> : gemm_bf16_d2l_kernel<AT, BT, false, NW>;
+  kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), NW * 64, 0, st>>>(a);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
 }  // namespace
 
 int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
@@ -507,6 +771,10 @@ int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, boo
   const bool big = dense_big(M, N);
   if (colsum && (!bt || bias)) return VH_ERR_UNSUPPORTED;
   const DenseArgs g = dense_args(a, lda, at, b, ldb, bt, c, ldc, M, N, K, bias, colsum);
+  if (dense_d2l(g, colsum != nullptr)) {
+    if (at) return bt ? launch_d2l<true, true>(g, st) : launch_d2l<true, false>(g, st);
+    return bt ? launch_d2l<false, true>(g, st) : launch_d2l<false, false>(g, st);
+  }
   if (at) return bt ? launch_layout<true, true>(g, big, st) : launch_layout<true, false>(g, big, st);
   return bt ? launch_layout<false, true>(g, big, st) : launch_layout<false, false>(g, big, st);
 }
