@@ -433,38 +433,36 @@ void gemm_bf16_pair_kernel(DenseArgs g0, DenseArgs g1) {
 // square product and its gradients, a Linear forward over whole 256-row
 // tiles).  The operands are copied from global memory straight into LDS by
 // buffer_load_dwordx4 ... lds (no registers and no LDS store instructions on
-// the way), four LDS stages of 32 k, the copies of stage s+3 issued while
-// stage s is multiplied.  NW waves split the tile 2 (m) x NW/2 (n): NW = 8
-// gives 128 x 64 per wave (128 accumulator registers, two waves per SIMD, so
+// the way), two LDS stages of 64 k (64 KB each), the copies of stage s+1
+// issued when stage s starts.  NW waves split the tile 2 (m) x NW/2 (n): NW =
+// 8 gives 128 x 64 per wave (128 accumulator registers, two waves per SIMD, so
 // one wave's copy issue and barrier waits are covered by the other's MFMAs);
 // NW = 4 gives 128 x 128 (256 accumulator registers, one wave per SIMD).
+// Measured on 8192^3 (one box): eight waves 5-15 % faster than four; 64-k
+// stages 2-5 % faster than four stages of 32 k (whole 128-byte lines of the
+// K-major rows, half the barriers).
 // LDS DMA writes a wave's 64 16-byte units contiguously (lane l at unit l of
 // the instruction's base), so a tile's layout is set by which global unit each
 // lane fetches; an XOR swizzle of the unit index keeps the fragment reads
 // free of bank conflicts (16 consecutive lanes on 16 distinct 16-byte bank
 // groups; measured: 0.8 % conflict cycles):
-//  * K-major tile (256 rows x 32 k, 4 units per row, row r at units 4r ..
-//    4r+3): slot t of row r holds k unit t ^ ((r >> 2) & 3).  Copy
-//    instruction c (0 .. 15) covers rows 16c .. 16c+15.
-//  * MN-major tile (32 k rows x 256, 32 units per k row): slot t of k row kr
+//  * K-major tile (256 rows x 64 k, 8 units per row, row r at units 8r ..
+//    8r+7): slot t of row r holds k unit t ^ ((r >> 1) & 7).  Copy
+//    instruction c (0 .. 31) covers rows 8c .. 8c+7.
+//  * MN-major tile (64 k rows x 256, 32 units per k row): slot t of k row kr
 //    holds row unit t ^ (4 (kr & 3)).  Instruction c covers k rows 2c, 2c+1.
 // The copies are issued as inline assembly, so the compiler's wait-count pass
 // does not see them (it would otherwise order fragment reads after all copies
-// in flight): the waits are explicit -- vmcnt(N) for the thread's own copies
-// of the next stage (the later stages stay in flight), lgkmcnt(0) for its
-// fragment reads -- in one statement with the s_barrier, which clobbers memory
-// so that no LDS read moves across it.  The four stages are separate static
-// arrays and the main loop is unrolled by four.
-constexpr int kD2lBK = 32;       // k per stage
-constexpr int kD2lUnits = 1024;  // 16-byte units per operand tile per stage
+// in flight): the waits are explicit -- vmcnt(0) for the thread's own copies
+// of the next stage, lgkmcnt(0) for its fragment reads -- in one statement
+// with the s_barrier, which clobbers memory so that no LDS read moves across
+// it.  The two stages are separate static arrays and the main loop is
+// unrolled by two.
+constexpr int kD2lBK = 64;       // k per stage
+constexpr int kD2lUnits = 2048;  // 16-byte units per operand tile per stage
 #ifndef VH_D2L_WAVES
 #define VH_D2L_WAVES 8
 #endif
-
-template <int B>
-__device__ __forceinline__ u32x4d* d2l_stage(u32x4d* s0, u32x4d* s1, u32x4d* s2, u32x4d* s3) {
-  return B == 0 ? s0 : B == 1 ? s1 : B == 2 ? s2 : s3;
-}
 
 // buffer_load_dwordx4 ... lds: lane l's 16 bytes (voff + soff) land at LDS
 // byte la + 16 l; M0 holds la (the s_nop covers the M0 -> LDS DMA hazard).
@@ -475,19 +473,8 @@ __device__ __forceinline__ void d2l_copy(__amdgpu_buffer_rsrc_t r, int voff, int
                : "memory", "m0");
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0), then the block barrier
-template <int N>
-__device__ __forceinline__ void d2l_sync() {
-  static_assert(N == 0 || N == 4 || N == 8 || N == 16, "vmcnt");
-  if constexpr (N == 16)
-    asm volatile("s_waitcnt vmcnt(16) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 8)
-    asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else if constexpr (N == 4)
-    asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  else
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
+// s_waitcnt vmcnt(0) lgkmcnt(0), then the block barrier
+__device__ __forceinline__ void d2l_sync() { asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ uint32_t lds_addr(const u32x4d* p) {
   return __builtin_amdgcn_readfirstlane(
@@ -497,15 +484,12 @@ __device__ __forceinline__ uint32_t lds_addr(const u32x4d* p) {
 template <bool AT, bool BT, bool BIAS, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
 void gemm_bf16_d2l_kernel(DenseArgs g) {
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
-  constexpr int WNW = NW / 2;        // waves along n
-  constexpr int FN = 8 / WNW;        // 32-column fragments per wave (FM = 4 rows of 32)
-  constexpr int CPW = 16 / NW;       // copy instructions per wave and operand per stage
-  constexpr int VM1 = 2 * CPW;       // copies per thread per stage
-  __shared__ __attribute__((aligned(16))) u32x4d S0[2 * kD2lUnits];
-  __shared__ __attribute__((aligned(16))) u32x4d S1[2 * kD2lUnits];
-  __shared__ __attribute__((aligned(16))) u32x4d S2[2 * kD2lUnits];
-  __shared__ __attribute__((aligned(16))) u32x4d S3[2 * kD2lUnits];
+  constexpr int BKX = kD2lBK, UNITS = kD2lUnits;
+  constexpr int WNW = NW / 2;   // waves along n
+  constexpr int FN = 8 / WNW;   // 32-column fragments per wave (FM = 4 rows of 32)
+  constexpr int CPW = 32 / NW;  // copy instructions per wave and operand per stage
+  __shared__ __attribute__((aligned(16))) u32x4d S0[2 * UNITS];
+  __shared__ __attribute__((aligned(16))) u32x4d S1[2 * UNITS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = (wave / WNW) * 128, wn = (wave % WNW) * (FN * 32);
@@ -514,13 +498,12 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
   const int gm = min(g.tiles_m - first_m, kGroupM);
   const int in_grp = lb - grp * kGroupM * g.tiles_n;
   const int m0 = (first_m + in_grp % gm) * 256, n0 = (in_grp / gm) * 256;
-
   // the thread's load units per operand (k0 = 0; the stage's k0 is a scalar
-  // offset), instruction c = CPW * wave + i
+  // offset), copy instruction c = CPW * wave + i
   auto unit_off = [&](bool mn, int rc0, int ld, int i) {
     const int c = CPW * wave + i;
     if (!mn) {
-      const int r = 16 * c + (lane >> 2), u = (lane & 3) ^ ((lane >> 4) & 3);
+      const int r = 8 * c + (lane >> 3), u = (lane & 7) ^ ((r >> 1) & 7);
       return ((rc0 + r) * ld + 8 * u) * 2;
     }
     const int kr = 2 * c + (lane >> 5), mu = (lane & 31) ^ (4 * (kr & 3));
@@ -540,15 +523,14 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
 #pragma unroll
     for (int i = 0; i < CPW; ++i) d2l_copy(ar, aoff[i], ask, la + i * 64 * 16);
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) d2l_copy(br, boff[i], bsk, la + (kD2lUnits + i * 64) * 16);
+    for (int i = 0; i < CPW; ++i) d2l_copy(br, boff[i], bsk, la + (UNITS + i * 64) * 16);
   };
-
-  // fragment addresses (bytes from the operand tile's start) of k step kk (0, 1)
+  // fragment addresses (bytes from the operand tile's start) of k step kk (0 .. 3)
   const int row_l = lane & 31, half_l = lane >> 5;
-  // K-major: row = base + row_l, k unit 2 kk + half_l
-  int kfrag[2];
+  // K-major: row = base + row_l (base a multiple of 32), k unit 2 kk + half_l
+  int kfrag[4];
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) kfrag[kk] = (4 * row_l + ((2 * kk + half_l) ^ ((lane >> 2) & 3))) * 16;
+  for (int kk = 0; kk < 4; ++kk) kfrag[kk] = (8 * row_l + ((2 * kk + half_l) ^ ((row_l >> 1) & 7))) * 16;
   // MN-major (transposing reads): k row 16 kk + 8 half_l + (lane & 15) / 4
   // (+4 for the second read), columns 16 ((lane >> 4) & 1) + 4 (lane & 3) .. +3
   const int tr_row = 8 * half_l + ((lane & 15) >> 2), x4 = 4 * ((lane >> 2) & 3);
@@ -573,17 +555,17 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
   };
   auto read = [&](const u32x4d* st, int kk, Frags& f) {
     const u32x4d* at = st;
-    const u32x4d* bt = st + kD2lUnits;
+    const u32x4d* bt = st + UNITS;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       f.a[i] = AT ? read_tr(at, amn[i] + kk * 16 * 32 * 16)
                   : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
-                                                   reinterpret_cast<const char*>(at) + (wm + 32 * i) * 64 + kfrag[kk]));
+                                                   reinterpret_cast<const char*>(at) + (wm + 32 * i) * 128 + kfrag[kk]));
 #pragma unroll
     for (int j = 0; j < FN; ++j)
       f.b[j] = BT ? read_tr(bt, bmn[j] + kk * 16 * 32 * 16)
                   : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
-                                                   reinterpret_cast<const char*>(bt) + (wn + 32 * j) * 64 + kfrag[kk]));
+                                                   reinterpret_cast<const char*>(bt) + (wn + 32 * j) * 128 + kfrag[kk]));
   };
   f32x16 acc[4][FN];
 #pragma unroll
@@ -597,53 +579,48 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
       for (int j = 0; j < FN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
   };
-
-  const int nst = g.K / kD2lBK;  // a multiple of 4 (>= 4)
+  const int nst = g.K / BKX;  // even (K % 128 == 0)
   issue(S0, 0);
-  issue(S1, kD2lBK);
-  issue(S2, 2 * kD2lBK);
-  d2l_sync<2 * VM1>();
-  Frags f0, f1;
-  read(S0, 0, f0);
-  // stage s sits in buffer s % 4; f0 holds its first k step on entry
+  d2l_sync();
+  Frags fa, fb;
+  read(S0, 0, fa);
+  // stage s sits in buffer s % 2; fa holds its first k step on entry.  The
+  // copies of stage s+1 go into the other buffer, whose stage s-1 every wave
+  // finished reading before the last barrier; the fragment reads of step
+  // kk+1 are issued ahead of the MFMAs of step kk.
   auto body = [&](auto BUF, int s) {
     constexpr int B = decltype(BUF)::value;
-    u32x4d* cur = d2l_stage<B>(S0, S1, S2, S3);
-    // buffer (s + 3) % 4 held stage s - 1, which every wave finished reading
-    // before the last barrier
-    if (s + 3 < nst) issue(d2l_stage<(B + 3) & 3>(S0, S1, S2, S3), (s + 3) * kD2lBK);
-    read(cur, 1, f1);
-    mma(f0);
+    u32x4d* cur = B == 0 ? S0 : S1;
+    u32x4d* nxt = B == 0 ? S1 : S0;
+    if (s + 1 < nst) issue(nxt, (s + 1) * BKX);
+    read(cur, 1, fb);
+    mma(fa);
+    read(cur, 2, fa);
+    mma(fb);
+    read(cur, 3, fb);
+    mma(fa);
     if (s + 1 < nst) {
-      // the thread's copies of stage s+1 have landed (stages s+2, s+3 may
-      // still be in flight) and its fragment reads of stage s are done; after
-      // the barrier every wave's are
-      if (s + 3 < nst) d2l_sync<2 * VM1>(); else if (s + 2 < nst) d2l_sync<VM1>(); else d2l_sync<0>();
-      read(d2l_stage<(B + 1) & 3>(S0, S1, S2, S3), 0, f0);
+      // the thread's copies of stage s+1 have landed and its reads of stage s
+      // are done; after the barrier every wave's are
+      d2l_sync();
+      read(nxt, 0, fa);
     }
-    mma(f1);
+    mma(fb);
   };
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
-  using C2 = std::integral_constant<int, 2>;
-  using C3 = std::integral_constant<int, 3>;
-  for (int s = 0; s < nst; s += 4) {
+  for (int s = 0; s < nst; s += 2) {
     body(C0{}, s);
     body(C1{}, s + 1);
-    body(C2{}, s + 2);
-    body(C3{}, s + 3);
   }
-
   // epilogue: fp32 (+ bias), one rounding, through LDS in two halves of the
-  // wave's 128 rows (pitch FN * 32 + 8 elements), out as 16-byte runs.  Wave
-  // w's region: stage array w (NW = 4: 17 KB) or half of array w / 2 (NW = 8:
-  // 9 KB each).
+  // wave's 128 rows (pitch FN * 32 + 8 elements), out as 16-byte runs; waves
+  // 0 .. NW/2-1 stage in S0, the others in S1
   __syncthreads();  // every wave is done reading the stages
   constexpr int WN = FN * 32, EP = WN + 8, CPR = WN / 8, RPI = 64 / CPR;
-  static_assert(64 * EP * 2 * (NW / 4) <= 2 * kD2lUnits * 16, "epilogue regions exceed a stage array");
-  const int ea = NW == 4 ? wave : wave >> 1;
-  u32x4d* const earr = ea == 0 ? S0 : ea == 1 ? S1 : ea == 2 ? S2 : S3;
-  uint16_t* eb = reinterpret_cast<uint16_t*>(earr) + (NW == 4 ? 0 : (wave & 1) * 64 * EP);
+  static_assert(NW / 2 * 64 * EP * 2 <= 2 * UNITS * 16, "epilogue regions exceed a stage array");
+  u32x4d* const earr = wave < NW / 2 ? S0 : S1;
+  uint16_t* eb = reinterpret_cast<uint16_t*>(earr) + (wave % (NW / 2)) * 64 * EP;
   const __amdgpu_buffer_rsrc_t cr = rsrc(g.c, g.c_bytes);
   float bv[FN];
 #pragma unroll
@@ -658,7 +635,7 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
         for (int v = 0; v < 16; ++v)
           eb[(ii * 32 + (v >> 2) * 8 + half_l * 4 + (v & 3)) * EP + j * 32 + row_l] =
               __builtin_bit_cast(uint16_t, (__bf16)(acc[2 * h + ii][j][v] + bv[j]));
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
     const int ch = lane % CPR, col = n0 + wn + ch * 8;
 #pragma unroll
@@ -749,7 +726,7 @@ bool dense_big(int M, int N) { return (long)((M + 127) / 128) * ((N + 255) / 256
 // its loads or stores), K in whole stages, 16-byte aligned rows of every
 // operand, and a grid of at least one block per CU.
 bool dense_d2l(const DenseArgs& g, bool colsum) {
-  return !colsum && g.M % 256 == 0 && g.N % 256 == 0 && g.K % (4 * kD2lBK) == 0 && g.vec_epi &&
+  return !colsum && g.M % 256 == 0 && g.N % 256 == 0 && g.K % (2 * kD2lBK) == 0 && g.vec_epi &&
          (long)(g.M / 256) * (g.N / 256) >= 256;
 }
 

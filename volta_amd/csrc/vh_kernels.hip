@@ -1023,28 +1023,38 @@ __global__ __launch_bounds__(256) void relayout_kernel(const typename Elem<T>::s
 // group and a range of rows is one contiguous run that lands in LDS unchanged.
 // mode 0: M = O, K = C, from W[m][k][tap] (forward); mode 1: M = C, K = O, from
 // W[k][m][tap] with the taps rotated 180 degrees (input gradient as a forward
-// convolution).  Walks dst in order.
+// convolution).  One thread per 16-byte unit of dst: its eight elements are
+// eight independent gathers (all in flight at once -- the pass is a single
+// memory round trip, latency-bound) and one 16-byte store.
 __global__ __launch_bounds__(256) void relayout_grouped_kernel(const uint16_t* __restrict__ src,
                                                                uint16_t* __restrict__ dst, int M, int K, int RS,
                                                                int mode, FastDiv fU, FastDiv fM) {
   // K is padded to whole groups of 16; the padding channels are zero
   const uint32_t U = 2u * (uint32_t)RS + 1u;  // units per row
-  const uint32_t total = (uint32_t)M * (uint32_t)((K + 15) / 16) * U * 8u;
-  for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < total; d += gridDim.x * 256u) {
-    const uint32_t i8 = d & 7u;
+  const uint32_t units = (uint32_t)M * (uint32_t)((K + 15) / 16) * U;
+  for (uint32_t d = blockIdx.x * 256u + threadIdx.x; d < units; d += gridDim.x * 256u) {
     uint32_t t2, unit, kg, m;
-    fU.divmod(d >> 3, t2, unit);
+    fU.divmod(d, t2, unit);
     fM.divmod(t2, kg, m);
-    const uint32_t tap = unit >> 1, k = kg * 16u + (unit & 1u) * 8u + i8;
-    uint16_t v = 0;
-    if (unit + 1u < U && k < (uint32_t)K)
-      v = src[mode == 0 ? (m * (uint32_t)K + k) * RS + tap : (k * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap)];
-    dst[d] = v;
+    const uint32_t tap = unit >> 1, k0 = kg * 16u + (unit & 1u) * 8u;
+    // element i: channel k0 + i (src stride RS along k for mode 0, M * RS for mode 1)
+    const uint32_t base = mode == 0 ? (m * (uint32_t)K + k0) * RS + tap : (k0 * (uint32_t)M + m) * RS + ((uint32_t)RS - 1u - tap);
+    const uint32_t step = mode == 0 ? (uint32_t)RS : (uint32_t)M * RS;
+    const bool row_ok = unit + 1u < U;
+    uint16_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = row_ok && k0 + i < (uint32_t)K ? src[base + i * step] : (uint16_t)0;
+    uint4 o;
+    o.x = v[0] | ((uint32_t)v[1] << 16);
+    o.y = v[2] | ((uint32_t)v[3] << 16);
+    o.z = v[4] | ((uint32_t)v[5] << 16);
+    o.w = v[6] | ((uint32_t)v[7] << 16);
+    reinterpret_cast<uint4*>(dst)[d] = o;
   }
 }
 
 int run_relayout_grouped(const void* w, void* dst, int M, int K, int RS, int mode, hipStream_t st) {
-  relayout_grouped_kernel<<<grid_for((long)M * ((K + 15) / 16) * (2 * RS + 1) * 8), 256, 0, st>>>(
+  relayout_grouped_kernel<<<grid_for((long)M * ((K + 15) / 16) * (2 * RS + 1)), 256, 0, st>>>(
       (const uint16_t*)w, (uint16_t*)dst, M, K, RS, mode, FastDiv((uint32_t)(2 * RS + 1)), FastDiv((uint32_t)M));
   VH_LAUNCH_CHECK();
   return VH_OK;
