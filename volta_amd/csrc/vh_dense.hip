@@ -428,29 +428,29 @@ void gemm_bf16_pair_kernel(DenseArgs g0, DenseArgs g1) {
     gemm_bf16_tile<128, BN, false, PC, AT1, BT1>(g1, xcd_map(h - t0, g1.tiles_m * g1.tiles_n));
 }
 
-// ---------------------------------------------------------------- 256 x 256 tiles, direct-to-LDS loads
-// For products whose M and N are multiples of 256 and K a multiple of 128 (the
-// square product and its gradients, a Linear forward over whole 256-row
-// tiles).  The operands are copied from global memory straight into LDS by
+// ---------------------------------------------------------------- BM x 256 tiles, direct-to-LDS loads
+// For products whose tiles are whole (M a multiple of BM, N of 256, K of 128):
+// the square product and its gradients and a Linear forward on 256 x 256
+// tiles, a Linear layer's dX and dW as one launch on 128 x 256 tiles.  The
+// operands are copied from global memory straight into LDS by
 // buffer_load_dwordx4 ... lds (no registers and no LDS store instructions on
-// the way), two LDS stages of 64 k (64 KB each), the copies of stage s+1
-// issued when stage s starts.  NW waves split the tile 2 (m) x NW/2 (n): NW =
-// 8 gives 128 x 64 per wave (128 accumulator registers, two waves per SIMD, so
-// one wave's copy issue and barrier waits are covered by the other's MFMAs);
-// NW = 4 gives 128 x 128 (256 accumulator registers, one wave per SIMD).
-// Measured on 8192^3 (one box): eight waves 5-15 % faster than four; 64-k
-// stages 2-5 % faster than four stages of 32 k (whole 128-byte lines of the
-// K-major rows, half the barriers).
+// the way), two LDS stages of 64 k, the copies of stage s+1 issued when stage
+// s starts.  Eight waves split the tile 2 (m) x 4 (n): BM/2 x 64 per wave
+// (256 x 256: 128 accumulator registers, two waves per SIMD, so one wave's
+// copy issue and barrier waits are covered by the other's MFMAs).  Measured on
+// 8192^3 (one box): eight waves 5-15 % faster than four waves of 128 x 128;
+// 64-k stages 2-5 % faster than four stages of 32 k (whole 128-byte lines of
+// the K-major rows, half the barriers).
 // LDS DMA writes a wave's 64 16-byte units contiguously (lane l at unit l of
 // the instruction's base), so a tile's layout is set by which global unit each
 // lane fetches; an XOR swizzle of the unit index keeps the fragment reads
 // free of bank conflicts (16 consecutive lanes on 16 distinct 16-byte bank
 // groups; measured: 0.8 % conflict cycles):
-//  * K-major tile (256 rows x 64 k, 8 units per row, row r at units 8r ..
+//  * K-major tile (R rows x 64 k, 8 units per row, row r at units 8r ..
 //    8r+7): slot t of row r holds k unit t ^ ((r >> 1) & 7).  Copy
-//    instruction c (0 .. 31) covers rows 8c .. 8c+7.
-//  * MN-major tile (64 k rows x 256, 32 units per k row): slot t of k row kr
-//    holds row unit t ^ (4 (kr & 3)).  Instruction c covers k rows 2c, 2c+1.
+//    instruction c covers rows 8c .. 8c+7.
+//  * MN-major tile (64 k rows x R, UR = R/8 units per k row): slot t of k row
+//    kr holds row unit t ^ (4 (kr & 3)).  Instruction c covers 64/UR k rows.
 // The copies are issued as inline assembly, so the compiler's wait-count pass
 // does not see them (it would otherwise order fragment reads after all copies
 // in flight): the waits are explicit -- vmcnt(0) for the thread's own copies
@@ -458,11 +458,7 @@ void gemm_bf16_pair_kernel(DenseArgs g0, DenseArgs g1) {
 // with the s_barrier, which clobbers memory so that no LDS read moves across
 // it.  The two stages are separate static arrays and the main loop is
 // unrolled by two.
-constexpr int kD2lBK = 64;       // k per stage
-constexpr int kD2lUnits = 2048;  // 16-byte units per operand tile per stage
-#ifndef VH_D2L_WAVES
-#define VH_D2L_WAVES 8
-#endif
+constexpr int kD2lBK = 64;  // k per stage
 
 // buffer_load_dwordx4 ... lds: lane l's 16 bytes (voff + soff) land at LDS
 // byte la + 16 l; M0 holds la (the s_nop covers the M0 -> LDS DMA hazard).
@@ -481,104 +477,142 @@ __device__ __forceinline__ uint32_t lds_addr(const u32x4d* p) {
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) u32x4d*)p);
 }
 
-template <bool AT, bool BT, bool BIAS, int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
-void gemm_bf16_d2l_kernel(DenseArgs g) {
-  constexpr int BKX = kD2lBK, UNITS = kD2lUnits;
-  constexpr int WNW = NW / 2;   // waves along n
-  constexpr int FN = 8 / WNW;   // 32-column fragments per wave (FM = 4 rows of 32)
-  constexpr int CPW = 32 / NW;  // copy instructions per wave and operand per stage
-  __shared__ __attribute__((aligned(16))) u32x4d S0[2 * UNITS];
-  __shared__ __attribute__((aligned(16))) u32x4d S1[2 * UNITS];
+// Tile geometry: BM x 256 (BM = 256 or 128), eight waves 2 (m) x 4 (n) of
+// BM/2 x 64 each, two LDS stages of (BM + 256) x 64 bf16.
+template <int BM>
+struct D2lCfg {
+  static constexpr int FM = BM / 64, FN = 2;             // 32 x 32 fragments per wave
+  static constexpr int A_UNITS = BM * 8, B_UNITS = 2048;  // 16-byte units per stage
+  static constexpr int STAGE = A_UNITS + B_UNITS;
+  static constexpr int ACPW = BM / 64, BCPW = 4;          // copy instructions per wave and stage
+};
+
+// One BM x 256 tile of C = A . B (logical block lb), S0 / S1 the two stages.
+// CS: the column sums of an MN-major B over K (a Linear weight gradient's bias
+// gradient) from the staged tiles: the tiles_m blocks of a column tile each
+// own 4 << cs_shift of its columns (block of m-tile mt: columns mt * width ..),
+// so every column is summed by exactly one block, over all K; a thread adds 4
+// consecutive owned columns of one k row per stage, in stage order, and the
+// k-row group sums are added in group order at the end.
+template <int BM, bool AT, bool BT, bool BIAS, bool CS>
+__device__ __forceinline__ void d2l_tile(const DenseArgs& g, const int lb, u32x4d* S0, u32x4d* S1) {
+  using Cfg = D2lCfg<BM>;
+  constexpr int FM = Cfg::FM, FN = Cfg::FN, UNITS_A = Cfg::A_UNITS;
+  constexpr int BKX = kD2lBK;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = (wave / WNW) * 128, wn = (wave % WNW) * (FN * 32);
-  const int lb = xcd_block(g.tiles_m * g.tiles_n);
+  const int wm = (wave >> 2) * (BM / 2), wn = (wave & 3) * 64;
   const int grp = lb / (kGroupM * g.tiles_n), first_m = grp * kGroupM;
   const int gm = min(g.tiles_m - first_m, kGroupM);
   const int in_grp = lb - grp * kGroupM * g.tiles_n;
-  const int m0 = (first_m + in_grp % gm) * 256, n0 = (in_grp / gm) * 256;
-  // the thread's load units per operand (k0 = 0; the stage's k0 is a scalar
-  // offset), copy instruction c = CPW * wave + i
-  auto unit_off = [&](bool mn, int rc0, int ld, int i) {
-    const int c = CPW * wave + i;
+  const int m0 = (first_m + in_grp % gm) * BM, n0 = (in_grp / gm) * 256;
+
+  // copy instruction c of an operand with R rows (R = BM or 256):
+  //  K-major: rows 8c .. 8c+7, lane -> row 8c + lane/8, slot lane%8 holds k
+  //    unit (lane%8) ^ ((row >> 1) & 7);
+  //  MN-major (UR = R/8 units per k row): k rows (64/UR) c .. , lane -> k row
+  //    (64/UR) c + lane/UR, slot lane%UR holds row unit slot ^ (4 (kr & 3)).
+  auto unit_off = [&](bool mn, int R, int rc0, int ld, int c) {
     if (!mn) {
       const int r = 8 * c + (lane >> 3), u = (lane & 7) ^ ((r >> 1) & 7);
       return ((rc0 + r) * ld + 8 * u) * 2;
     }
-    const int kr = 2 * c + (lane >> 5), mu = (lane & 31) ^ (4 * (kr & 3));
+    const int UR = R / 8;
+    const int kr = (64 / UR) * c + lane / UR, mu = (lane % UR) ^ (4 * (kr & 3));
     return (kr * ld + rc0 + 8 * mu) * 2;
   };
-  int aoff[CPW], boff[CPW];
+  int aoff[Cfg::ACPW], boff[Cfg::BCPW];
 #pragma unroll
-  for (int i = 0; i < CPW; ++i) {
-    aoff[i] = unit_off(AT, m0, g.lda, i);
-    boff[i] = unit_off(BT, n0, g.ldb, i);
-  }
+  for (int i = 0; i < Cfg::ACPW; ++i) aoff[i] = unit_off(AT, BM, m0, g.lda, Cfg::ACPW * wave + i);
+#pragma unroll
+  for (int i = 0; i < Cfg::BCPW; ++i) boff[i] = unit_off(BT, 256, n0, g.ldb, Cfg::BCPW * wave + i);
   const __amdgpu_buffer_rsrc_t ar = rsrc(g.a, g.a_bytes), br = rsrc(g.b, g.b_bytes);
   auto issue = [&](u32x4d* st, int k0) {
     const int ask = __builtin_amdgcn_readfirstlane(AT ? k0 * g.lda * 2 : k0 * 2);
     const int bsk = __builtin_amdgcn_readfirstlane(BT ? k0 * g.ldb * 2 : k0 * 2);
-    const uint32_t la = lds_addr(st) + wave * CPW * 64 * 16;
+    const uint32_t la = lds_addr(st);
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) d2l_copy(ar, aoff[i], ask, la + i * 64 * 16);
+    for (int i = 0; i < Cfg::ACPW; ++i) d2l_copy(ar, aoff[i], ask, la + (Cfg::ACPW * wave + i) * 64 * 16);
 #pragma unroll
-    for (int i = 0; i < CPW; ++i) d2l_copy(br, boff[i], bsk, la + (UNITS + i * 64) * 16);
+    for (int i = 0; i < Cfg::BCPW; ++i)
+      d2l_copy(br, boff[i], bsk, la + (UNITS_A + (Cfg::BCPW * wave + i) * 64) * 16);
   };
+
   // fragment addresses (bytes from the operand tile's start) of k step kk (0 .. 3)
   const int row_l = lane & 31, half_l = lane >> 5;
   // K-major: row = base + row_l (base a multiple of 32), k unit 2 kk + half_l
   int kfrag[4];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) kfrag[kk] = (8 * row_l + ((2 * kk + half_l) ^ ((row_l >> 1) & 7))) * 16;
-  // MN-major (transposing reads): k row 16 kk + 8 half_l + (lane & 15) / 4
-  // (+4 for the second read), columns 16 ((lane >> 4) & 1) + 4 (lane & 3) .. +3
+  // MN-major (transposing reads, UR units per k row): k row 16 kk + 8 half_l +
+  // (lane & 15) / 4 (+4 for the second read), columns 16 ((lane >> 4) & 1) +
+  // 4 (lane & 3) .. +3
   const int tr_row = 8 * half_l + ((lane & 15) >> 2), x4 = 4 * ((lane >> 2) & 3);
-  const int tr_lo = tr_row * 32 * 16 + (2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) * 16 + 8 * (lane & 1);
-  auto mn_unit0 = [&](int col0) { return ((col0 >> 3) ^ x4) * 16; };
-  int amn[4], bmn[FN];
+  const int tr_in = (2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) * 16 + 8 * (lane & 1);
+  auto mn_frag = [&](int UR, int col0) { return tr_row * UR * 16 + tr_in + ((col0 >> 3) ^ x4) * 16; };
+  int amn[FM], bmn[FN];
 #pragma unroll
-  for (int f = 0; f < 4; ++f) amn[f] = tr_lo + mn_unit0(wm + 32 * f);
+  for (int f = 0; f < FM; ++f) amn[f] = mn_frag(BM / 8, wm + 32 * f);
 #pragma unroll
-  for (int f = 0; f < FN; ++f) bmn[f] = tr_lo + mn_unit0(wn + 32 * f);
+  for (int f = 0; f < FN; ++f) bmn[f] = mn_frag(32, wn + 32 * f);
   typedef short v4i16 __attribute__((ext_vector_type(4)));
   typedef short v8i16 __attribute__((ext_vector_type(8)));
-  auto read_tr = [&](const u32x4d* tile, int byte) {
+  auto read_tr = [&](const u32x4d* tile, int byte, int UR) {
     const __attribute__((address_space(3))) char* p = (const __attribute__((address_space(3))) char*)tile + byte;
     const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)p);
-    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p + 4 * 32 * 16));
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p + 4 * UR * 16));
     const v8i16 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     return __builtin_bit_cast(bf16x8, v);
   };
   struct Frags {
-    bf16x8 a[4], b[FN];
+    bf16x8 a[FM], b[FN];
   };
   auto read = [&](const u32x4d* st, int kk, Frags& f) {
     const u32x4d* at = st;
-    const u32x4d* bt = st + UNITS;
+    const u32x4d* bt = st + UNITS_A;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      f.a[i] = AT ? read_tr(at, amn[i] + kk * 16 * 32 * 16)
+    for (int i = 0; i < FM; ++i)
+      f.a[i] = AT ? read_tr(at, amn[i] + kk * 16 * (BM / 8) * 16, BM / 8)
                   : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
                                                    reinterpret_cast<const char*>(at) + (wm + 32 * i) * 128 + kfrag[kk]));
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      f.b[j] = BT ? read_tr(bt, bmn[j] + kk * 16 * 32 * 16)
+      f.b[j] = BT ? read_tr(bt, bmn[j] + kk * 16 * 32 * 16, 32)
                   : __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4d*>(
                                                    reinterpret_cast<const char*>(bt) + (wn + 32 * j) * 128 + kfrag[kk]));
   };
-  f32x16 acc[4][FN];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x16{};
   auto mma = [&](const Frags& f) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
       for (int j = 0; j < FN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
   };
+
+  // column sums (CS): this block's columns cs_c0 .. cs_c0 + cs_w - 1 of the
+  // n-tile, thread t adds columns cs_c0 + 4 (t % ng) .. +3 of k rows t / ng,
+  // t / ng + 512 / ng, .. of each stage
+  const int cs_w = 4 << g.cs_shift, cs_c0 = (m0 / BM) * cs_w, ng = cs_w >> 2;
+  const bool cs_blk = CS && g.colsum != nullptr && cs_c0 < 256;  // block-uniform
+  const int cs_c = cs_c0 + 4 * (tid % ng), cs_k0 = tid / ng;
+  float csum[4] = {0.f, 0.f, 0.f, 0.f};
+  auto colsum_stage = [&](const u32x4d* st) {
+    const char* bt = reinterpret_cast<const char*>(st + UNITS_A);
+    for (int kr = cs_k0; kr < BKX; kr += 512 / ng) {
+      const u32x2d v =
+          *reinterpret_cast<const u32x2d*>(bt + (kr * 32 + ((cs_c >> 3) ^ (4 * (kr & 3)))) * 16 + (cs_c & 7) * 2);
+      csum[0] += __builtin_bit_cast(float, v[0] << 16);
+      csum[1] += __builtin_bit_cast(float, v[0] & 0xffff0000u);
+      csum[2] += __builtin_bit_cast(float, v[1] << 16);
+      csum[3] += __builtin_bit_cast(float, v[1] & 0xffff0000u);
+    }
+  };
+
   const int nst = g.K / BKX;  // even (K % 128 == 0)
   issue(S0, 0);
   d2l_sync();
@@ -595,6 +629,9 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
     if (s + 1 < nst) issue(nxt, (s + 1) * BKX);
     read(cur, 1, fb);
     mma(fa);
+    if constexpr (CS) {
+      if (cs_blk) colsum_stage(cur);
+    }
     read(cur, 2, fa);
     mma(fb);
     read(cur, 3, fb);
@@ -613,20 +650,36 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
     body(C0{}, s);
     body(C1{}, s + 1);
   }
-  // epilogue: fp32 (+ bias), one rounding, through LDS in two halves of the
-  // wave's 128 rows (pitch FN * 32 + 8 elements), out as 16-byte runs; waves
-  // 0 .. NW/2-1 stage in S0, the others in S1
   __syncthreads();  // every wave is done reading the stages
-  constexpr int WN = FN * 32, EP = WN + 8, CPR = WN / 8, RPI = 64 / CPR;
-  static_assert(NW / 2 * 64 * EP * 2 <= 2 * UNITS * 16, "epilogue regions exceed a stage array");
-  u32x4d* const earr = wave < NW / 2 ? S0 : S1;
-  uint16_t* eb = reinterpret_cast<uint16_t*>(earr) + (wave % (NW / 2)) * 64 * EP;
+
+  if constexpr (CS) {
+    if (cs_blk) {  // per owned column: the k-row group sums, added in group order
+      float* red = reinterpret_cast<float*>(S0);  // [512 / ng][cs_w]
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[cs_k0 * cs_w + cs_c - cs_c0 + e] = csum[e];
+      __syncthreads();
+      const int n = n0 + cs_c0 + tid;
+      if (tid < cs_w && n < g.N) {
+        float t = 0.f;
+        for (int j = 0; j < 512 / ng; ++j) t += red[j * cs_w + tid];
+        g.colsum[n] = f32_to_bf16(t);
+      }
+      __syncthreads();
+    }
+  }
+
+  // epilogue: fp32 (+ bias), one rounding, through LDS in halves of 64 of the
+  // wave's BM/2 rows (pitch 72 elements), out as 16-byte runs; waves 0-3 stage
+  // in S0, waves 4-7 in S1
+  constexpr int EP = 72, CPR = 8, RPI = 8;
+  static_assert(4 * 64 * EP * 2 <= Cfg::STAGE * 16, "epilogue regions exceed a stage");
+  uint16_t* eb = reinterpret_cast<uint16_t*>(wave < 4 ? S0 : S1) + (wave & 3) * 64 * EP;
   const __amdgpu_buffer_rsrc_t cr = rsrc(g.c, g.c_bytes);
   float bv[FN];
 #pragma unroll
   for (int j = 0; j < FN; ++j) bv[j] = BIAS ? bf16_to_f32(g.bias[n0 + wn + j * 32 + row_l]) : 0.f;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < FM / 2; ++h) {
 #pragma unroll
     for (int j = 0; j < FN; ++j)
 #pragma unroll
@@ -635,7 +688,7 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
         for (int v = 0; v < 16; ++v)
           eb[(ii * 32 + (v >> 2) * 8 + half_l * 4 + (v & 3)) * EP + j * 32 + row_l] =
               __builtin_bit_cast(uint16_t, (__bf16)(acc[2 * h + ii][j][v] + bv[j]));
-    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
     __builtin_amdgcn_wave_barrier();
     const int ch = lane % CPR, col = n0 + wn + ch * 8;
 #pragma unroll
@@ -647,6 +700,28 @@ void gemm_bf16_d2l_kernel(DenseArgs g) {
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
   }
+}
+
+template <bool AT, bool BT, bool BIAS>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_bf16_d2l_kernel(DenseArgs g) {
+  __shared__ __attribute__((aligned(16))) u32x4d S0[D2lCfg<256>::STAGE];
+  __shared__ __attribute__((aligned(16))) u32x4d S1[D2lCfg<256>::STAGE];
+  d2l_tile<256, AT, BT, BIAS, false>(g, xcd_block(g.tiles_m * g.tiles_n), S0, S1);
+}
+
+// Two products in one launch on 128 x 256 tiles (Linear's dX, K-major x
+// K-major, and dW, MN-major x MN-major with the bias gradient's column sums):
+// blocks 0 .. T0-1 take the first product's tiles, the rest the second's.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_bf16_d2l_pair_kernel(DenseArgs g0, DenseArgs g1) {
+  __shared__ __attribute__((aligned(16))) u32x4d S0[D2lCfg<128>::STAGE];
+  __shared__ __attribute__((aligned(16))) u32x4d S1[D2lCfg<128>::STAGE];
+  const int t0 = g0.tiles_m * g0.tiles_n, h = blockIdx.x;
+  if (h < t0)
+    d2l_tile<128, false, false, false, false>(g0, xcd_map(h, t0), S0, S1);
+  else
+    d2l_tile<128, true, true, false, true>(g1, xcd_map(h - t0, g1.tiles_m * g1.tiles_n), S0, S1);
 }
 
 // Column-sum ownership on BN-column tiles: 2^cs_shift groups of 4 columns per
@@ -735,9 +810,8 @@ int launch_d2l(const DenseArgs& a0, hipStream_t st) {
   DenseArgs a = a0;
   a.tiles_m = a.M / 256;
   a.tiles_n = a.N / 256;
-  constexpr int NW = VH_D2L_WAVES;
-  auto kern = a.bias ? gemm_bf16_d2l_kernel<AT, BT, true, NW> : gemm_bf16_d2l_kernel<AT, BT, false, NW>;
-  kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), NW * 64, 0, st>>>(a);
+  auto kern = a.bias ? gemm_bf16_d2l_kernel<AT, BT, true> : gemm_bf16_d2l_kernel<AT, BT, false>;
+  kern<<<dim3((unsigned)(a.tiles_m * a.tiles_n)), 512, 0, st>>>(a);
   VH_LAUNCH_CHECK();
   return VH_OK;
 }
@@ -757,6 +831,18 @@ int dense_bf16_gemm(const void* a, int lda, bool at, const void* b, int ldb, boo
 }
 
 namespace {
+int launch_d2l_pair(DenseArgs a0, DenseArgs a1, hipStream_t st) {
+  for (DenseArgs* a : {&a0, &a1}) {
+    a->tiles_m = a->M / 128;
+    a->tiles_n = a->N / 256;
+    a->cs_shift = colsum_shift(a->tiles_m, 256);
+  }
+  gemm_bf16_d2l_pair_kernel<<<dim3((unsigned)(a0.tiles_m * a0.tiles_n + a1.tiles_m * a1.tiles_n)), 512, 0, st>>>(a0,
+                                                                                                                 a1);
+  VH_LAUNCH_CHECK();
+  return VH_OK;
+}
+
 template <int BN, bool PC>
 int launch_pair(DenseArgs a0, DenseArgs a1, hipStream_t st) {
   for (DenseArgs* a : {&a0, &a1}) {
@@ -781,6 +867,13 @@ int dense_bf16_gemm_pair(const DenseProblem& p0, const DenseProblem& p1, hipStre
                                   nullptr);
   const DenseArgs a1 = dense_args(p1.a, p1.lda, p1.at, p1.b, p1.ldb, p1.bt, p1.c, p1.ldc, p1.M, p1.N, p1.K, nullptr,
                                   p1.colsum);
+  // whole 128 x 256 tiles of both, at least one block per CU: the
+  // direct-to-LDS pair kernel
+  auto whole = [](const DenseArgs& g) {
+    return g.M % 128 == 0 && g.N % 256 == 0 && g.K % (2 * kD2lBK) == 0 && g.vec_epi != 0;
+  };
+  if (whole(a0) && whole(a1) && (long)(a0.M / 128) * (a0.N / 256) + (long)(a1.M / 128) * (a1.N / 256) >= 256)
+    return launch_d2l_pair(a0, a1, st);
   const long t256 = (long)((p0.M + 127) / 128) * ((p0.N + 255) / 256) + (long)((p1.M + 127) / 128) * ((p1.N + 255) / 256);
   return t256 >= 256 ? launch_pair<256, true>(a0, a1, st) : launch_pair<128, false>(a0, a1, st);
 }
