@@ -462,6 +462,8 @@ constexpr int kD2lBK = 64;  // k per stage
 
 // buffer_load_dwordx4 ... lds: lane l's 16 bytes (voff + soff) land at LDS
 // byte la + 16 l; M0 holds la (the s_nop covers the M0 -> LDS DMA hazard).
+// M0 is listed as clobbered; nothing else in these kernels uses it (their
+// generated code references M0 only in these copies).
 __device__ __forceinline__ void d2l_copy(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t la) {
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                :
