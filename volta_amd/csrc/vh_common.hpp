@@ -87,6 +87,33 @@ __device__ __forceinline__ int xcd_map(int h, int nb) {
 }
 __device__ __forceinline__ int xcd_block(int nb) { return xcd_map(blockIdx.x, nb); }
 
+// Global -> LDS copy of 16 bytes per lane without registers
+// (buffer_load_dwordx4 ... lds): lane l's 16 bytes at buffer offset voff + soff
+// land at LDS byte la + 16 l (lanes off in EXEC copy nothing; an out-of-range
+// voff writes zeros).  M0 holds la (the s_nop covers the M0 -> LDS DMA
+// hazard).  Inline assembly, so the compiler's wait-count pass does not track
+// these copies: the caller waits for them itself (s_waitcnt vmcnt) before a
+// barrier, and keeps M0 free of other uses in its kernel.
+__device__ __forceinline__ void lds_copy16(__amdgpu_buffer_rsrc_t r, int voff, int soff, uint32_t la) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(r), "s"(soff), "s"(la)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) (N < 64), other counters untouched
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xf00);
+}
+
+// LDS byte address of a shared-memory pointer, wave-uniform
+template <typename T>
+__device__ __forceinline__ uint32_t lds_byte_addr(const T* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p);
+}
+
 // Deterministic reduction of split-K partial sums part[z][i] (z < splits,
 // i < total) by a 256-thread block: 64 consecutive outputs per pass, wave w
 // adds z = w, w+4, w+8, ... in order and the four wave sums are added in wave

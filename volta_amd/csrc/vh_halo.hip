@@ -147,6 +147,13 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   static_assert(FMT == 2 || (!FUSED && WM == 1), "32-row tiles: one wave row, not the fused form");
   constexpr int RS = Cfg::RS, BM = Cfg::BM, BN = Cfg::BN, FM = Cfg::FM, FN = Cfg::FN;
   constexpr int SU = FUSED ? kFusedStageUnits : 1;
+  // WDMA (fused producer / consumer form on the grouped weight copy): each
+  // group's weight tile, one contiguous run of the grouped copy that lands in
+  // LDS unchanged, is copied into its stage by LDS DMA (buffer_load ... lds)
+  // when the producers store the group's x cells, instead of being loaded into
+  // registers two groups ahead and stored by the producers (the two-set
+  // producers: at most 2 x items per thread)
+  constexpr bool WDMA = PC && FUSED && !WD && XI <= 2;
   __shared__ __attribute__((aligned(16))) u32x4 lds0[SU];
   __shared__ __attribute__((aligned(16))) u32x4 lds1[SU];
   extern __shared__ __attribute__((aligned(16))) u32x4 lds_dyn[];
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       for (int j = 0; j < 9; ++j)
         wdr[sI][j] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
                                                    crem > 0 ? wrsrc : zrsrc, wd_goff + 8 * j, c0 * 18, 0));
-    } else {
+    } else if constexpr (!WDMA) {
 #pragma unroll
       for (int it = 0; it < Cfg::WITER; ++it)
         wreg[sI][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -340,7 +347,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
         v[1] = two(18 + t, 27 + t);
         *reinterpret_cast<u32x2*>(wb + t * 32) = v;
       }
-    } else {
+    } else if constexpr (!WDMA) {
 #pragma unroll
       for (int it = 0; it < Cfg::WITER; ++it) WSM(st)[w_loff[it]] = wreg[sI][it];
     }
@@ -362,6 +369,22 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
         u32x4* base = XSM(st) + x_loff[it];
         base[xsw ? 1 : 0] = xsw ? c1v : c0v;
         base[xsw ? 0 : 1] = xsw ? c0v : c1v;
+      }
+    }
+  };
+
+  // WDMA: copy group g's weight tile (units 0 .. WUNITS-1 of the stage; rows
+  // past O read zeros) into stage st; copy instruction c = wave + 4 i covers
+  // units 64c .. 64c+63
+  auto wdma = [&](int st, int g) {
+    if constexpr (WDMA) {
+      const uint32_t la = lds_byte_addr(WSM(st));
+      const int soff = __builtin_amdgcn_readfirstlane(16 * g * OGP);
+#pragma unroll
+      for (int c = wave; c < (Cfg::WUNITS + 63) / 64; c += 4) {
+        const int u = 64 * c + lane;
+        const bool ok = u < Cfg::WUNITS && (full_o || o0 + u / Cfg::WPU < a.O);
+        if (u < Cfg::WUNITS) lds_copy16(wrsrc, ok ? (o0 * Cfg::WPU + u) * 16 : (int)0x80000000u, soff, la + c * 1024);
       }
     }
   };
@@ -435,8 +458,11 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       // address unit works on this wave's loads while its stores go to LDS.
       auto swap = [&](auto SET, int st, int c0n) {
         sstore(SET, st);
+        wdma(st, c0n / 16 - 2);  // the group just stored
         gload(SET, c0n);
-        constexpr int NW = WD ? 9 : Cfg::WITER;
+        // WDMA: the copy is older than this set's x loads, which may stay in flight
+        if constexpr (WDMA) wait_vmcnt<Cfg::XITER * 8>();
+        constexpr int NW = WD ? 9 : WDMA ? 0 : Cfg::WITER;
 #pragma unroll
         for (int i = 0; i < NW; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // LDS store
@@ -463,6 +489,8 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       // nk - kt (1 or 2) barriers left: one per remaining group of the consumers
       if (kt + 1 < nk) {
         sstore(I1{}, 1);
+        wdma(1, kt + 1);
+        if constexpr (WDMA) wait_vmcnt<0>();
         __syncthreads();
       }
       __syncthreads();
