@@ -106,7 +106,90 @@ def parse():
                     help="run only these passes (e.g. '3x3 256->256 @14 wgrad', several separated by ';', "
                          "or 'headline' for all twelve) --steps times each, then a 256 MiB device copy, for "
                          "rocprofv3 counter runs; prints only the pass names")
+    ap.add_argument("--vendor", action="store_true",
+                    help="time the same convolution passes and the 8192^3 product through PyTorch-ROCm's own "
+                         "libraries (MIOpen, hipBLASLt) instead, for comparison; prints one JSON line")
     return ap.parse_args()
+
+
+def vendor_reference(torch, dev, steps, warmup):
+    """The headline passes, configs[0]'s and configs[4]'s
+    convolution passes and the 8192^3 bf16 product through PyTorch-ROCm's
+    vendor libraries on the same GPU: torch.nn.functional.conv2d and
+    aten.convolution_backward (MIOpen) in NCHW -- the layout of the reference
+    and of this library -- and, for configs[2], in NHWC (channels_last, MIOpen's
+    preferred layout); torch.mm (hipBLASLt).  Eager calls between HIP events
+    (MIOpen calls are not captured in graphs), best of 5 timings of `steps` calls
+    after `warmup`.  Not part of the library: a reference point only."""
+    g = torch.Generator().manual_seed(0)
+
+    def best_ms(fn):
+        return min(time_eager_fn(torch, fn, steps, warmup) for _ in range(5))
+
+    def conv_passes(N, C, O, H, K, S, P, dt, nhwc=False):
+        x = torch.randn((N, C, H, H), generator=g).to(dev, dt)
+        w = (torch.randn((O, C, K, K), generator=g) * 0.05).to(dev, dt)
+        HO = conv_out(H, K, S, P)
+        dy = torch.randn((N, O, HO, HO), generator=g).to(dev, dt)
+        if nhwc:
+            x, w, dy = (t.contiguous(memory_format=torch.channels_last) for t in (x, w, dy))
+        bw = torch.ops.aten.convolution_backward
+        fns = {"fwd": lambda: torch.nn.functional.conv2d(x, w, None, S, P),
+               "dgrad": lambda: bw(dy, x, w, None, [S, S], [P, P], [1, 1], False, [0, 0], 1, [True, False, False]),
+               "wgrad": lambda: bw(dy, x, w, None, [S, S], [P, P], [1, 1], False, [0, 0], 1, [False, True, False])}
+        return {op: round(best_ms(fn), 4) for op, fn in fns.items()}
+
+    out = {"metric": "vendor-library reference (PyTorch-ROCm: MIOpen convolutions, hipBLASLt GEMM)",
+           "unit": "ms per call", "torch": torch.__version__}
+    for layout in ("nchw", "nhwc"):
+        passes = {}
+        for name, C, O, H, K, S, P in C3_LAYERS:
+            for op, ms in conv_passes(C3_BATCH, C, O, H, K, S, P, torch.bfloat16, layout == "nhwc").items():
+                passes[f"{name} {op}"] = ms
+        out[f"configs[2] bf16 {layout}"] = dict(passes=passes, sum_of_passes_ms=round(sum(passes.values()), 4))
+    for key, N, H, dt, specs in (("configs[0] f32 nchw", 64, 28, torch.float32,
+                                  [("L0 1->32 k3", 1, 32, 3, 1), ("L1 32->64 k3", 32, 64, 3, 1)]),
+                                 ("configs[4] bf16 nchw", 16, 256, torch.bfloat16,
+                                  [("L0 3->64 k5", 3, 64, 5, 2), ("L1 64->64 k3", 64, 64, 3, 1),
+                                   ("L2 64->32 k3", 64, 32, 3, 1), ("L3 32->27 k3", 32, 27, 3, 1)])):
+        passes = {}
+        for name, C, O, K, P in specs:
+            for op, ms in conv_passes(N, C, O, H, K, 1, P, dt).items():
+                passes[f"{name} {op}"] = ms
+        out[key] = dict(passes=passes, sum_of_passes_ms=round(sum(passes.values()), 4))
+    # configs[3]: ConvTranspose2d f32, N=128 (forward, then its input and weight gradients)
+    passes = {}
+    for CI, CO, H, K, S, P in C4_LAYERS:
+        x = torch.randn((C4_BATCH, CI, H, H), generator=g).to(dev)
+        w = (torch.randn((CI, CO, K, K), generator=g) * 0.02).to(dev)
+        HO = (H - 1) * S + K - 2 * P
+        dy = torch.randn((C4_BATCH, CO, HO, HO), generator=g).to(dev)
+        bw = torch.ops.aten.convolution_backward
+        nm = f"{CI}->{CO} @{HO}"
+        for op, fn in (("fwd", lambda: torch.nn.functional.conv_transpose2d(x, w, None, S, P)),
+                       ("dX", lambda: bw(dy, x, w, None, [S, S], [P, P], [1, 1], True, [0, 0], 1,
+                                         [True, False, False])),
+                       ("dW", lambda: bw(dy, x, w, None, [S, S], [P, P], [1, 1], True, [0, 0], 1,
+                                         [False, True, False]))):
+            passes[f"{nm} {op}"] = round(best_ms(fn), 4)
+    out["configs[3] f32 nchw"] = dict(passes=passes, sum_of_passes_ms=round(sum(passes.values()), 4))
+    # configs[1]: Linear 4096x1024 -> 4096 (y = x W + b, dX = dY W^T, dW = x^T dY), and the 8192^3 product
+    for dt, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        x = torch.randn((4096, 1024), generator=g).to(dev, dt)
+        w = torch.randn((1024, 4096), generator=g).to(dev, dt)
+        b = torch.randn((4096,), generator=g).to(dev, dt)
+        dy = torch.randn((4096, 4096), generator=g).to(dev, dt)
+        wt, xt = w.t().contiguous(), x.t().contiguous()
+        passes = {"fwd (+bias)": round(best_ms(lambda: torch.addmm(b, x, w)), 4),
+                  "dX": round(best_ms(lambda: torch.mm(dy, wt)), 4),
+                  "dW": round(best_ms(lambda: torch.mm(xt, dy)), 4)}
+        out[f"configs[1] Linear {name}"] = dict(passes=passes, sum_of_passes_ms=round(sum(passes.values()), 4))
+    n = 8192
+    a = torch.randn((n, n), generator=g).to(dev, torch.bfloat16)
+    b = torch.randn((n, n), generator=g).to(dev, torch.bfloat16)
+    ms = best_ms(lambda: torch.mm(a, b))
+    out["matmul 8192^3 bf16"] = dict(ms=round(ms, 4), tflops=round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1))
+    print(json.dumps(out), flush=True)
 
 
 def build_layers(torch, vnn, dev):
@@ -715,6 +798,9 @@ def main():
 
     if args.profile_op:
         profile_op(torch, vnn, dev, layers, args.profile_op, args.steps)
+        return
+    if args.vendor:
+        vendor_reference(torch, dev, args.steps, args.warmup)
         return
     if args.profile_step:
         step = make_train_step(torch, layers, None if args.one_stream else torch.cuda.Stream())
