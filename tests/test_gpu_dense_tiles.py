@@ -1,9 +1,10 @@
-"""GPU parity of the 256 x 256 bf16 product tiles (operands copied straight
-into LDS, swizzled layouts): whole outputs of every operand layout they serve
--- matmul (K-major x MN-major), its dA (K-major x K-major) and dB (MN-major x
-MN-major), and the Linear forward with its bias -- at shapes that take them
-(M and N multiples of 256 with at least 256 tiles, K a multiple of 128: one
-and three turns of the four-stage loop), against the CPU oracle.
+"""GPU parity of the 256 x 256 product tiles (operands copied straight into
+LDS, swizzled layouts), bf16 and f32: whole outputs of every operand layout
+they serve -- matmul (K-major x MN-major), its dA (K-major x K-major) and dB
+(MN-major x MN-major), and the Linear forward with its bias -- at shapes that
+take them (M and N multiples of 256 with at least 256 tiles, K a multiple of
+128 for bf16 -- one and three turns of its two-stage loop -- and of 64 for
+f32), against the CPU oracle.
 """
 import numpy as np
 import pytest
@@ -19,9 +20,14 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 
 
-def prep(a):
-    r = oracle.round_bf16(np.ascontiguousarray(a, np.float32))
-    return r, torch.from_numpy(r).to(DEV, torch.bfloat16)
+TORCH_DT = {"bf16": torch.bfloat16, "f32": torch.float32}
+
+
+def prep(a, dt):
+    r = np.ascontiguousarray(a, np.float32)
+    if dt == "bf16":
+        r = oracle.round_bf16(r)
+    return r, torch.from_numpy(r).to(DEV, TORCH_DT[dt])
 
 
 def host(t):
@@ -29,48 +35,51 @@ def host(t):
     return t.float().cpu().numpy()
 
 
-def check(got, fn, args, what, k, extra=None):
+def check(got, fn, args, what, k, dt, extra=None):
     ref = fn(*args)
     scale = fn(*[np.abs(a) for a in args])
     if extra is not None:
         ref = ref + extra
         scale = scale + np.abs(extra)
-    assert_parity(host(got), ref, scale, "bf16", what, k=k)
+    assert_parity(host(got), ref, scale, dt, what, k=k)
 
 
-@pytest.mark.parametrize("kk", [128, 384])
-def test_matmul_256_tiles(kk):
+@pytest.mark.parametrize("dt,kk", [("bf16", 128), ("bf16", 384), ("f32", 64), ("f32", 384)])
+def test_matmul_256_tiles(dt, kk):
     m, n = 4096, 4096
     g = np.random.default_rng(kk + 1)
-    a, at = prep(g.standard_normal((m, kk)))
-    b, bt = prep(g.standard_normal((kk, n)))
-    check(ops.gpu_matmul(at, bt, m, kk, n), oracle.matmul, (a, b), f"C = A.B, K = {kk}", k=kk)
+    a, at = prep(g.standard_normal((m, kk)), dt)
+    b, bt = prep(g.standard_normal((kk, n)), dt)
+    check(ops.gpu_matmul(at, bt, m, kk, n), oracle.matmul, (a, b), f"C = A.B, K = {kk}", kk, dt)
 
 
-def test_matmul_backward_a_256_tiles():
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_matmul_backward_a_256_tiles(dt):
     # dA[m][k] = G[m][n] . B[k][n]^T: M = m, N = k, contraction n
     m, k, n = 4096, 4096, 128
     g = np.random.default_rng(21)
-    gr, grt = prep(g.standard_normal((m, n)))
-    b, bt = prep(g.standard_normal((k, n)))
-    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), "dA", k=n)
+    gr, grt = prep(g.standard_normal((m, n)), dt)
+    b, bt = prep(g.standard_normal((k, n)), dt)
+    check(ops.gpu_matmul_backward_a(grt, bt, m, k, n), oracle.matmul_backward_a, (gr, b), "dA", n, dt)
 
 
-def test_matmul_backward_b_256_tiles():
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_matmul_backward_b_256_tiles(dt):
     # dB[k][n] = A[m][k]^T . G[m][n]: M = k, N = n, contraction m
     m, k, n = 128, 4096, 4096
     g = np.random.default_rng(22)
-    a, at = prep(g.standard_normal((m, k)))
-    gr, grt = prep(g.standard_normal((m, n)))
-    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), "dB", k=m)
+    a, at = prep(g.standard_normal((m, k)), dt)
+    gr, grt = prep(g.standard_normal((m, n)), dt)
+    check(ops.gpu_matmul_backward_b(at, grt, m, k, n), oracle.matmul_backward_b, (a, gr), "dB", m, dt)
 
 
-def test_linear_forward_256_tiles():
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_linear_forward_256_tiles(dt):
     m, i, o = 4096, 128, 4096
     g = np.random.default_rng(23)
-    x, xt = prep(g.standard_normal((m, i)))
-    w, wt = prep(g.uniform(-0.5, 0.5, (i, o)))
-    b, bt = prep(g.uniform(-1, 1, (o,)))
-    lin = vnn.Linear(i, o, device=DEV, dtype=torch.bfloat16)
+    x, xt = prep(g.standard_normal((m, i)), dt)
+    w, wt = prep(g.uniform(-0.5, 0.5, (i, o)), dt)
+    b, bt = prep(g.uniform(-1, 1, (o,)), dt)
+    lin = vnn.Linear(i, o, device=DEV, dtype=TORCH_DT[dt])
     lin.weight, lin.bias = wt, bt
-    check(lin.forward(xt), oracle.matmul, (x, w), "Linear y = x.W + b", k=i + 1, extra=b[None, :])
+    check(lin.forward(xt), oracle.matmul, (x, w), "Linear y = x.W + b", i + 1, dt, extra=b[None, :])

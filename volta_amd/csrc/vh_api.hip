@@ -823,6 +823,15 @@ static int dense_bf16_pair(const DenseProblem& p0, const DenseProblem& p1, hipSt
   return dense_bf16_gemm_pair(p0, p1, st);
 }
 
+static int dense_f32_pair(const DenseProblem& p0, const DenseProblem& p1, hipStream_t st) {
+  for (const DenseProblem* p : {&p0, &p1}) {
+    if (std::max({(long)p->M * p->K, (long)p->K * p->N, (long)p->M * p->N}) > kMaxElems) return VH_ERR_UNSUPPORTED;
+    if (!dense_f32_ok(p->M, p->N, p->K, p->at, p->lda, p->bt, p->ldb, p->ldc, p->a, p->b, p->c))
+      return VH_ERR_UNSUPPORTED;
+  }
+  return dense_f32_gemm_pair(p0, p1, st);
+}
+
 static int dense_f32(int ak, int bk, const void* a, int lda, const void* b, int ldb, void* c, int ldc, long M,
                      long N, long K, const void* bias, hipStream_t st) {
   const bool at = ak == KD_DENSE_MN, bt = bk == KD_DENSE_MN;
@@ -1496,6 +1505,17 @@ int vh_linear_backward(int dtype, const void* out_grad, const void* x, const voi
     const DenseProblem dw{x, (int)in_features, true, out_grad, (int)out_features, true,
                           grad_weight, (int)out_features, (int)in_features, (int)out_features, (int)m, grad_bias};
     const int r = dense_bf16_pair(dx, dw, st);
+    if (r != VH_OK && r != VH_ERR_UNSUPPORTED) return r;
+    if (r == VH_OK) grad_x = grad_weight = grad_bias = nullptr;  // all done
+  }
+  if (dtype == VH_F32 && g_fast_paths && grad_x && grad_weight && m * in_features * out_features &&
+      std::max({m, in_features, out_features}) < (1L << 31)) {
+    // the same pair in fp32 (whole 128 x 256 tiles only), db as column sums of dY
+    const DenseProblem dx{out_grad, (int)out_features, false, weight, (int)out_features, false,
+                          grad_x, (int)in_features, (int)m, (int)in_features, (int)out_features, nullptr};
+    const DenseProblem dw{x, (int)in_features, true, out_grad, (int)out_features, true,
+                          grad_weight, (int)out_features, (int)in_features, (int)out_features, (int)m, grad_bias};
+    const int r = dense_f32_pair(dx, dw, st);
     if (r != VH_OK && r != VH_ERR_UNSUPPORTED) return r;
     if (r == VH_OK) grad_x = grad_weight = grad_bias = nullptr;  // all done
   }

@@ -198,6 +198,17 @@ inline int reduce_vec4_grid(long total, int lg_g) {
   return (int)std::min<long>((total / 4 + qb - 1) / qb, 1L << 20);
 }
 
+// Column-sum ownership on BN-column tiles of a product whose column tile is
+// shared by tiles_m blocks: 2^cs_shift groups of 4 columns per block, the
+// smallest power-of-2 width >= BN / tiles_m (at least 16 columns).
+inline int colsum_shift(int tiles_m, int BN) {
+  int w = 16;
+  while (w < BN && w * tiles_m < BN) w <<= 1;
+  int sh = 0;
+  while ((4 << sh) < w) ++sh;
+  return sh;
+}
+
 // Raises a kernel's dynamic-LDS limit to the CU's 160 KB.  Each call site is
 // one template instantiation, so the flag is per kernel; std::call_once makes
 // concurrent first launches from several host threads safe.

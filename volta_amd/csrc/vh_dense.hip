@@ -726,16 +726,6 @@ void gemm_bf16_d2l_pair_kernel(DenseArgs g0, DenseArgs g1) {
     d2l_tile<128, true, true, false, true>(g1, xcd_map(h - t0, g1.tiles_m * g1.tiles_n), S0, S1);
 }
 
-// Column-sum ownership on BN-column tiles: 2^cs_shift groups of 4 columns per
-// block, the smallest power-of-2 width >= BN / tiles_m (at least 16 columns).
-int colsum_shift(int tiles_m, int BN) {
-  int w = 16;
-  while (w < BN && w * tiles_m < BN) w <<= 1;
-  int sh = 0;
-  while ((4 << sh) < w) ++sh;
-  return sh;
-}
-
 bool fits(long bytes) { return bytes >= 0 && bytes < (1L << 31) - 64; }
 
 template <int BM, int BN, bool BIAS, bool PC, bool AT, bool BT>

@@ -198,6 +198,9 @@ bool dense_f32_ok(long M, long N, long K, bool at, long lda, bool bt, long ldb, 
                   const void* b, const void* c);
 int dense_f32_gemm(const void* a, int lda, bool at, const void* b, int ldb, bool bt, void* c, int ldc, int M,
                    int N, int K, const void* bias, hipStream_t st);
+// Linear's dX and dW (+ column sums) in one launch, fp32 (each problem checked
+// by dense_f32_ok); VH_ERR_UNSUPPORTED: run them separately.
+int dense_f32_gemm_pair(const DenseProblem& p0, const DenseProblem& p1, hipStream_t st);
 
 // ---- strided 1x1 bf16 convolutions, pad 0 (vh_pointwise.hip) ----
 // w is the OIHW weight itself ([O][C]).  Each returns VH_ERR_UNSUPPORTED
