@@ -83,3 +83,23 @@ def test_linear_forward_256_tiles(dt):
     lin = vnn.Linear(i, o, device=DEV, dtype=TORCH_DT[dt])
     lin.weight, lin.bias = wt, bt
     check(lin.forward(xt), oracle.matmul, (x, w), "Linear y = x.W + b", i + 1, dt, extra=b[None, :])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_linear_backward_pair_tiles(dt):
+    # dX (K-major x K-major) and dW + db (MN-major x MN-major, the column sums
+    # of dY in the dW tiles) as one launch of 128 x 256 tiles: 32 + 256 tiles,
+    # 16 m-tiles sharing each dW column tile's 256 bias columns
+    m, i, o = 512, 2048, 4096
+    g = np.random.default_rng(24)
+    x, xt = prep(g.standard_normal((m, i)), dt)
+    w, wt = prep(g.uniform(-0.05, 0.05, (i, o)), dt)
+    dy, dyt = prep(g.standard_normal((m, o)), dt)
+    lin = vnn.Linear(i, o, device=DEV, dtype=TORCH_DT[dt])
+    lin.weight = wt
+    dx, dw, db = lin.backward(dyt, xt)
+    ref = oracle.linear_backward(dy, x, w)
+    sc = oracle.linear_backward(np.abs(dy), np.abs(x), np.abs(w))
+    assert_parity(host(dx), ref[0], sc[0], dt, "dX", k=o)
+    assert_parity(host(dw), ref[1], sc[1], dt, "dW", k=m)
+    assert_parity(host(db), ref[2], sc[2], dt, "db", k=m)
