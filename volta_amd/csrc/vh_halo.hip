@@ -1070,15 +1070,20 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   const int stage_units = BMt * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
-  const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= VH_HALO_WPE3_MIN_TILES && halo_xi(a) <= (WM == 1 ? 4 : 2);
-  if (wpe3) a.stages = 1;
-  const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
-  const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
   // Fused form (two register sets, whole channel groups, stages and the
   // vector epilogue within the static stage size): 3x3, 64 x 256 tiles with
   // at most 4 x items per thread.
-  const bool fused = !wpe3 && fm == 2 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
-                     stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16);
+  const bool fused_ok = fm == 2 && R == 3 && S == 3 && WM == 1 && nk >= 2 && C % 16 == 0 && halo_xi(a) <= 4 &&
+                        stage_units <= kFusedStageUnits && (!a.vec_epi || 4 * 64 * 72 * 2 <= kFusedStageUnits * 16);
+  // A forward over whole rows stays on the fused form, which reads W itself
+  // (no relayout launch): 64@56, 1568 tiles, 51.7 -> 47.5 us a pass; the
+  // input gradient and column strips measured faster three blocks per CU.
+  const bool wpe3 = R == 3 && S == 3 && nk >= 2 && tiles >= VH_HALO_WPE3_MIN_TILES && halo_xi(a) <= (WM == 1 ? 4 : 2) &&
+                    !(w_mode == 0 && whole && fused_ok);
+  if (wpe3) a.stages = 1;
+  const size_t lds_st = wpe3 ? best.lds / 2 : best.lds;
+  const size_t lds = a.vec_epi ? std::max<size_t>(lds_st, 4 * 64 * 72 * 2) : lds_st;
+  const bool fused = !wpe3 && fused_ok;
   // The fused forward reads W [O][C][3][3] directly (no relayout launch).  Each
   // block then repacks its weights itself: free in the fused form (128@28 and
   // 256@14 ran as fast as with the grouped copy), 4 us more than the relayout
