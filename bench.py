@@ -49,8 +49,8 @@ METRIC = "Conv2d fwd+bwd TFLOP/s & % MFMA peak (1 GPU); GEMM TFLOP/s; vs CPU"
 # Keyed by pass name; used for roofline.traffic when that pass is the dominant
 # one (which pass is the slowest varies by a few percent from run to run).
 MEASURED_TRAFFIC_BYTES = {
-    # relayout_grouped_kernel: fetch 77 x2, write 76; conv_halo_bf16_kernel: fetch 25684 x2, write 50176
-    "3x3 64->64 @56 fwd": int((25761 * 2 + 50252) * 1024),
+    # conv_halo_bf16_kernel (fused form, W read directly): fetch 25510 x2, write 50176
+    "3x3 64->64 @56 fwd": int((25510 * 2 + 50176) * 1024),
     # relayout_grouped_kernel: fetch 202 x2, write 76; conv_halo_bf16_kernel: fetch 25682 x2, write 50176
     "3x3 64->64 @56 dgrad": int((25884 * 2 + 50252) * 1024),
     # wgrad_rows_bf16_kernel: fetch 52800 x2, write 9216; wgrad_reduce_frag_bf16_kernel: fetch 4646 x2, write 72
