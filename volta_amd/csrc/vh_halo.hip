@@ -15,9 +15,17 @@
 // shift.  x is read from HBM once per block (plus the halo rows), with dword
 // loads along rows that are transposed to channel-packed cells in registers.
 //
-// LDS is split into two half-planes (channels 0-7, 8-15) so that the 64 lanes
-// of one fragment read walk consecutive 16-byte cells: lanes 0-31 read plane 0,
-// lanes 32-63 plane 1, each at consecutive positions / output channels.
+// Each ext row holds two half-planes (channels 0-7, 8-15) side by side so that
+// the 64 lanes of one fragment read walk consecutive 16-byte cells: lanes 0-31
+// read plane 0, lanes 32-63 plane 1, each at consecutive positions / output
+// channels.  A ds_read_b128 serves 16 lanes per cycle, lanes {0-3, 12-15,
+// 20-27} and {4-11, 16-19, 28-31} (and the same sets + 32), which together
+// read 16 positions spread over 28 consecutive ones: those are on distinct
+// banks only if every row end (and image end) moves the cell index by a
+// multiple of 16 cells, hence the row pitch Wp = TW (mod 16) and the per-image
+// offset img_d.  Putting both half-planes in one row pitch is what makes the
+// aligned pitch fit the fused form's stage (2 Wr + 15 cells a row instead of
+// 2 (Wr + 15)).
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -46,8 +54,13 @@ struct HaloArgs {
   // past Q are computed and dropped).  One strip (TW = Q) means whole rows.
   int TW, nstrips;
   int Hp;                // padded input rows: H + 2*ph
-  int Wp;                // LDS cells per ext row (even): >= TW + S - 1 + cs, = TW mod 16 (or 8)
-                         // where the LDS budget allows (bank-conflict-free fragment reads)
+  int Wp;                // LDS cells per ext row, both half-planes: plane 0 at cells [0, Wr),
+                         // plane 1 at [hoff, hoff + Wr) (Wr = TW + S - 1 + cs, even; Wp >= 2 Wr),
+                         // = TW mod 16 where the LDS budget allows (conflict-free fragment reads)
+  int hoff;              // cell offset of half-plane 1 within an ext row
+  int img_d;             // extra cells per virtual image past the block's first: keeps the
+                         // cell jump between images = 0 mod 16 (0 when Wp is not aligned)
+  int xcells;            // x cells per LDS stage: rows_max * Wp + (images spanned - 1) * img_d
   int cs;                // cell of input column strip*TW - pw (0, or 1 for strips
                          // with pw odd: cell 0 then sits on an even input column)
   int lcol0, lcell0;     // first loaded column pair: input column strip*TW + lcol0
@@ -173,10 +186,10 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   const int m0 = (lb / a.tiles_o) * BN;
   const int o0 = (lb % a.tiles_o) * BM;
   const int Wp = a.Wp;
-  const int cells = a.rows_max * Wp;       // cells per half-plane
+  const int cells = a.xcells;              // x cells per stage (both half-planes)
   const int w_units = BM * Cfg::WPU;       // 16-byte units per weight stage
-  const int stage = w_units + 2 * cells + 2;  // uint4 per stage; the last 2 units are a
-                                              // sink for stores of unused load items
+  const int stage = w_units + cells + 2;   // uint4 per stage; the last 2 units are a
+                                           // sink for stores of unused load items
   // stage st: weights at the stage's start, x halo right after them
 #define WSM(st) (FUSED ? ((st) ? lds1 : lds0) : lds + (st) * stage)
 #define XSM(st) (WSM(st) + w_units)
@@ -192,17 +205,21 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   a.fQ.divmod(pq_b, p_b, q_b);
   const int rows = (int)n_b * a.Hp + (int)p_b + R - e_start;  // ext rows used by this block
 
+  // first cell of ext row e (block-relative) of half-plane 0: rows of the
+  // block's later virtual images sit img_d cells further per image
+  auto row_cell = [&](int e) { return e * Wp + ((int)a.fHp.div((uint32_t)(e_start + e)) - (int)n_a) * a.img_d; };
+
   // whole rows: zero the padding cells once (never written by the loader):
-  // per (stage, half-plane, ext row) the cells [0, pw) and [W + pw, Wp).
+  // per (stage, half-plane, ext row used) the cells [0, pw) and [W + pw, W + 2 pw).
   // Strips load every cell (columns outside the image load as zeros).
   if (a.nstrips == 1) {
     const u32x4 z = {0u, 0u, 0u, 0u};
-    const int padc = Wp - a.W;
     for (int i = tid; i < 2 * a.stages * a.rows_max; i += 256) {
       uint32_t sh, e;
       a.fRowsMax.divmod((uint32_t)i, sh, e);
-      u32x4* rowp = XSM(sh >> 1) + (sh & 1) * cells + e * Wp;
-      for (int pc = 0; pc < padc; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
+      if ((int)e >= rows) continue;
+      u32x4* rowp = XSM(sh >> 1) + (sh & 1) * a.hoff + row_cell((int)e);
+      for (int pc = 0; pc < 2 * a.pw; ++pc) rowp[pc < a.pw ? pc : a.W + pc] = z;
     }
   }
   // per-lane cell index of each B fragment column (fixed for the whole block)
@@ -215,7 +232,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       uint32_t n, pq, p, q;
       a.fPQ.divmod((uint32_t)m, n, pq);
       a.fQ.divmod(pq, p, q);
-      cidx = ((int)n * a.Hp + (int)p - e_start) * Wp + (int)q + a.cs;
+      cidx = ((int)n * a.Hp + (int)p - e_start) * Wp + ((int)n - (int)n_a) * a.img_d + (int)q + a.cs;
     }
     bcell[j] = cidx;
   }
@@ -252,10 +269,10 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
       const int col = (int)strip * a.TW + a.lcol0 + 2 * (int)wi;
       if (h >= 0 && h < a.H && col >= 0 && col < a.W)
         voff = (int)((((long)n * a.C + half * 8) * HW + (long)h * a.W + col) * 2);
-      loff = half * cells + (int)e * Wp + a.lcell0 + 2 * (int)wi;
+      loff = half * a.hoff + (int)e * Wp + ((int)vimg - (int)n_a) * a.img_d + a.lcell0 + 2 * (int)wi;
     }
     x_voff[it] = voff;
-    x_loff[it] = loff >= 0 ? loff : 2 * cells;  // unused items store to the sink
+    x_loff[it] = loff >= 0 ? loff : cells;  // unused items store to the sink
   }
 
   const bool full_o = o0 + BM <= a.O;  // uniform: no per-row checks needed
@@ -280,7 +297,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
     const int u = tid + it * 256;
     const bool ok = u < Cfg::WUNITS && (full_o || o0 + u / Cfg::WPU < a.O);
     w_goff[it] = ok ? (o0 * Cfg::WPU + u) * 16 : (int)0x80000000u;
-    w_loff[it] = u < Cfg::WUNITS ? u : w_units + 2 * cells;  // sink
+    w_loff[it] = u < Cfg::WUNITS ? u : w_units + cells;  // sink
   }
 
   // With two register sets (DEPTH 2) the global loads of channel group kt+2
@@ -400,7 +417,7 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   const int half_l = lane >> 5, row_l = lane & 31;
   auto compute = [&](int st) {
     const u32x4* Wp_ = WSM(st) + (wm + row_l) * Cfg::WPU + half_l;
-    const u32x4* Xp_ = XSM(st) + half_l * cells;
+    const u32x4* Xp_ = XSM(st) + half_l * a.hoff;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
@@ -975,7 +992,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   // blocks per CU (LDS <= 80 KB), then the fewest computed columns (strips
   // past Q are waste), then the fewest staged input cells per block.
   struct Cand {
-    int TW, WM, rows_max, Wp;
+    int TW, WM, rows_max, Wr, Wp, img_d, xcells;  // Wr: cells per row and half-plane
     size_t lds;
     long cols;  // virtual columns per row: nstrips * TW
   };
@@ -989,14 +1006,14 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
     if (Mv >= (1L << 31)) return false;
     const bool whole = TW == Q;
     const int cs = whole ? 0 : (pw & 1);
-    const int Wp = whole ? W + 2 * pw : (TW + S - 1 + cs + 1) & ~1;
-    const int npairs = whole ? W / 2 : Wp / 2;
+    const int Wr = whole ? W + 2 * pw : (TW + S - 1 + cs + 1) & ~1;
+    const int npairs = whole ? W / 2 : Wr / 2;
     const long PQv = (long)P * TW;
     const int rows_max = halo_rows_max(Mv, BN, PQv, TW, a.Hp, R);
-    const size_t stage = (size_t)(BM * (2 * R * S + 1) + 2 * rows_max * Wp + 2) * 16;
+    const size_t stage = (size_t)(BM * (2 * R * S + 1) + rows_max * 2 * Wr + 2) * 16;
     const size_t lds = a.stages * stage;
     if (lds > 160 * 1024 || 2 * ((rows_max * npairs + 255) / 256) > 8) return false;
-    c = Cand{TW, WM, rows_max, Wp, lds, (long)nstrips * TW};
+    c = Cand{TW, WM, rows_max, Wr, 2 * Wr, 0, rows_max * 2 * Wr, lds, (long)nstrips * TW};
     return true;
   };
   Cand best{}, c{};
@@ -1020,29 +1037,35 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
   if (!have) return VH_ERR_UNSUPPORTED;
   // Row pitch: the 32 lanes of a fragment read consecutive positions, i.e.
   // consecutive 16-byte cells except at a row end, where the cell index jumps
-  // by Wp - TW.  With Wp = TW (mod 16) the jump keeps every group of 16 lanes
-  // on distinct banks (mod 8: groups of 8).  Take the widest alignment whose
-  // larger stage keeps every decision the base pitch led to (blocks per CU,
-  // fused form's static stage size).
+  // by Wp - TW, and at an image end, by (Hp - P) Wp + Wp - TW + img_d.  With
+  // both = 0 (mod 16) every 16 lanes that share a read cycle are on distinct
+  // banks.  Taken when the larger stage keeps every decision the tight pitch
+  // 2 Wr led to (blocks per CU, fused form's static stage size).
   {
-    const int WMb = best.WM, BMb = WMb * fm * 32;
-    auto units = [&](int wp) { return BMb * (2 * R * S + 1) + 2 * best.rows_max * wp + 2; };
+    const int BMb = best.WM * fm * 32, BNb = (4 / best.WM) * 64;
+    const long PQv = (long)P * best.TW;
+    const int imgs = (int)((BNb - 1 + PQv - 1) / PQv) + 1;  // virtual images a block can span
+    auto units = [&](int xc) { return BMb * (2 * R * S + 1) + xc + 2; };
     const bool two = best.lds <= 80 * 1024;
-    const bool fused_base = units(best.Wp) <= kFusedStageUnits;
-    for (int al : {16, 8}) {
-      const int wp = best.Wp + ((best.TW - best.Wp) % al + al) % al;
-      const size_t lds_wp = (size_t)a.stages * units(wp) * 16;
-      if (lds_wp > (two ? 80 * 1024 : 160 * 1024)) continue;
-      if (fused_base && units(wp) > kFusedStageUnits) continue;
+    const bool fused_base = units(best.xcells) <= kFusedStageUnits;
+    const int wp = best.Wp + (((best.TW - best.Wp) % 16) + 16) % 16;
+    const int d = (((-(a.Hp - P) * wp) % 16) + 16) % 16;
+    const int xc = best.rows_max * wp + (imgs - 1) * d;
+    const size_t lds_wp = (size_t)a.stages * units(xc) * 16;
+    if (lds_wp <= (two ? 80 * 1024 : 160 * 1024) && !(fused_base && units(xc) > kFusedStageUnits)) {
       best.Wp = wp;
+      best.img_d = d;
+      best.xcells = xc;
       best.lds = lds_wp;
-      break;
     }
   }
   const int WM = best.WM, rows_max = best.rows_max;
   a.TW = best.TW;
   a.nstrips = (Q + a.TW - 1) / a.TW;
   a.Wp = best.Wp;
+  a.hoff = best.Wr;
+  a.img_d = best.img_d;
+  a.xcells = best.xcells;
   a.M = N * a.nstrips * P * a.TW;
   a.fPQ = FastDiv((uint32_t)(P * a.TW));
   a.fQ = FastDiv((uint32_t)a.TW);
@@ -1067,7 +1090,7 @@ int halo_conv_bf16(const void* x, const void* w, int w_mode, void* ws, const voi
                    ? 1 : 0;
   const int BMt = WM * fm * 32;
   const long tiles = ((long)a.M + (4 / WM) * 64 - 1) / ((4 / WM) * 64) * ((O + BMt - 1) / BMt);
-  const int stage_units = BMt * (2 * R * S + 1) + 2 * rows_max * a.Wp + 2;
+  const int stage_units = BMt * (2 * R * S + 1) + a.xcells + 2;
   // Three blocks per CU with one LDS stage pays off for grids of many blocks
   // with several channel groups (one group is single-stage already).
   // Fused form (two register sets, whole channel groups, stages and the
