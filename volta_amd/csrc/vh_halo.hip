@@ -288,7 +288,11 @@ __global__ __launch_bounds__(PC ? 512 : 256) __attribute__((amdgpu_waves_per_eu(
   // offset c0 * 18), and the LDS byte offset of its tap-0 store
   int wd_goff = 0, wd_loff = 0;
   if constexpr (WD) {
-    const int o = tid >> 2, q = tid & 3;
+    // wave w stages rows 16w .. 16w+15, lanes 0-31 the even ones and lanes
+    // 32-63 the odd ones: rows 19 units apart, 8 even rows cover all 64 banks
+    // once per 8-byte store, where 8 consecutive rows overlap (measured: two
+    // cycles per ds_write_b64 instead of one)
+    const int o = (tid >> 6) * 16 + 2 * ((tid >> 2) & 7) + ((tid >> 5) & 1), q = tid & 3;
     wd_goff = o0 + o < a.O ? ((o0 + o) * a.C + 4 * q) * 18 : (int)0x80000000u;
     wd_loff = (o * Cfg::WPU + (q >> 1)) * 16 + (q & 1) * 8;
   }
